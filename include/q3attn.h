@@ -1,0 +1,94 @@
+/*
+ * q3attn -- MI355X (gfx950) attention for the Qwen3-TTS engine's hot path, as a C ABI.
+ *
+ * Every pointer is a device pointer owned by the caller.  Every entry point only enqueues kernels
+ * on `stream` (a hipStream_t passed as void*; NULL = the legacy default stream): no allocation,
+ * no host synchronisation, no blocking copy, so calls are capturable into a HIP graph and two
+ * streams may call concurrently as long as they pass distinct output/workspace buffers.
+ *
+ * Strides are in elements.  Return value: 0 on success, or a negative Q3A_E* code; the message
+ * for the last failure on the calling thread is in q3a_last_error().  The library never prints
+ * and never aborts.
+ */
+#ifndef Q3ATTN_H
+#define Q3ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q3A_OK 0
+#define Q3A_EINVAL (-22)  /* bad shape, stride, alignment or argument */
+#define Q3A_ELAUNCH (-5)  /* the HIP runtime refused the launch */
+#define Q3A_ESPACE (-28)  /* workspace smaller than q3a_paged_decode_workspace_bytes() */
+
+/* ABI version of this header (bumped on any signature change). */
+int q3a_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* q3a_last_error(void);
+
+/*
+ * Talker decode attention over the paged KV pool.
+ *
+ * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=ctx, block_table=bt,
+ * softmax_scale=scale, causal=True) at engine/talker.py:77 (fp32 semantics: engine/talker.py:82-88).
+ *
+ *   q            [B, Hq, D] bf16   row stride q_stride_b, head stride q_stride_h, dim stride 1
+ *   k_cache      [num_pages, page_size, Hkv, D] bf16, strides kv_stride_page / kv_stride_tok /
+ *   v_cache      kv_stride_head, dim stride 1 (both caches share the strides)
+ *   cache_seqlens[B] int32   context length of each row (tokens 0..ctx-1 are attended)
+ *   block_table  [B, max_pages_per_seq] int32, row stride bt_stride_b: token t of row b lives at
+ *                page block_table[b][t / page_size], offset t % page_size
+ *   out          [B, Hq, D] bf16   row stride o_stride_b, head stride o_stride_h
+ *   workspace    fp32 split-K partials, at least q3a_paged_decode_workspace_bytes() bytes
+ *                (uninitialised memory is fine)
+ *
+ * Query head h reads KV head h / (Hq/Hkv).  softmax is float32.  Rows with ctx <= 0 produce zeros;
+ * ctx is clamped to max_pages_per_seq*page_size; a page index outside [0, num_pages) contributes
+ * no tokens.  Requirements: D == 128, Hq == 2*Hkv, 1 <= Hkv <= 16, page_size % 16 == 0,
+ * 16-byte aligned rows.  split_tokens (a multiple of 16) is the number of context tokens one
+ * workgroup streams; 0 selects q3a_paged_decode_default_split().
+ */
+int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void* k_cache, const void* v_cache, int64_t kv_stride_page,
+                     int64_t kv_stride_tok, int64_t kv_stride_head, int num_pages, int page_size,
+                     const int32_t* cache_seqlens, const int32_t* block_table, int64_t bt_stride_b,
+                     int max_pages_per_seq, void* out, int64_t o_stride_b, int64_t o_stride_h,
+                     void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
+                     int num_kv_heads, int head_dim, float softmax_scale, int split_tokens,
+                     void* stream);
+
+/* Bytes of workspace q3a_paged_decode needs for this shape and split (0 if none is needed). */
+size_t q3a_paged_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                        int max_pages_per_seq, int page_size, int split_tokens);
+
+/* The split size q3a_paged_decode uses when split_tokens == 0. */
+int q3a_paged_decode_default_split(int batch, int num_kv_heads, int max_pages_per_seq,
+                                   int page_size);
+
+/*
+ * Code-predictor attention over the 16-slot K/V scratch.
+ *
+ * Replaces cp_attn(q, K, V, n_live, scale) (engine/cp_attn.py:33-39), whose in-graph torch form is
+ * engine/code_predictor.py:46-47: slots >= n_live are masked (and never read), scores and softmax
+ * are float32, the probabilities are rounded to bf16 before P.V, P.V accumulates in float32.
+ *
+ *   q   [B, Hq, D] bf16 with row stride q_stride_b (head stride D)
+ *   k,v [B, Hkv, S, D] bf16 with strides kv_stride_b / kv_stride_h / kv_stride_s (dim stride 1)
+ *   out [B, Hq*D] bf16 with row stride o_stride_b
+ * Requirements: D == 128, Hq == 2*Hkv, 1 <= n_live <= 16.
+ */
+int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
+                int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,
+                int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                int n_live, float softmax_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q3ATTN_H */

@@ -1,0 +1,153 @@
+// Code-predictor attention over the 16-slot K/V scratch, for gfx950.
+//
+// Semantics (engine/cp_attn.py:13-30; in-graph torch form engine/code_predictor.py:46-47): for
+// row b and KV head g, the two query heads 2g, 2g+1 attend over slots 0..n_live-1 of K/V[b, g];
+// scores and softmax in float32, probabilities rounded to bf16, P.V accumulated in float32,
+// output rounded to bf16.  Slots >= n_live are never read.
+//
+// One wave per (row, KV head).  Scores: lane l takes slot l/4 and a quarter of the head
+// dimension (4 x 16 B loads; the 4 lanes of a slot read 64 contiguous bytes per instruction) and
+// reduces with two quad DPP steps.  P.V: lane l owns output dims 2l, 2l+1 of both query heads and
+// walks the slots; each slot is one 256 B coalesced load and the slot's probability is broadcast
+// with v_readlane.  All loads of the wave are issued before the first use.
+#include "q3a_common.h"
+#include "../../include/q3attn.h"
+
+namespace q3a {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kG = 2;
+constexpr int kSlots = 16;
+constexpr int kWavesPerBlock = 4;
+
+struct CpArgs {
+  const uint16_t* q;
+  int64_t q_sb;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t kv_sb, kv_sh, kv_ss;
+  uint16_t* out;
+  int64_t o_sb;
+  int pairs, hkv, n_live;
+  float scale_log2;
+};
+
+__global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpArgs a) {
+  const int wave = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (wave >= a.pairs) return;
+  const int b = wave / a.hkv;
+  const int g = wave - b * a.hkv;
+  const int lane = threadIdx.x & 63;
+  const int slot = lane >> 2;
+  const int c = lane & 3;
+  const bool live = slot < a.n_live;
+
+  const uint16_t* kb = a.k + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
+  const uint16_t* vb = a.v + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
+  const uint16_t* qb = a.q + (int64_t)b * a.q_sb + (int64_t)(kG * g) * kD;
+
+  // Lane (slot, c) holds dims 32*i + 8*c .. +8 for i = 0..3, of K[slot] and of both query heads.
+  uint4 kr[4], qr[kG][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 32 * i + 8 * c;
+    kr[i] = live ? *reinterpret_cast<const uint4*>(kb + (int64_t)slot * a.kv_ss + d)
+                 : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int h = 0; h < kG; ++h) qr[h][i] = *reinterpret_cast<const uint4*>(qb + h * kD + d);
+  }
+  uint32_t vr[kSlots];
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s)
+    vr[s] = s < a.n_live ? *reinterpret_cast<const uint32_t*>(vb + (int64_t)s * a.kv_ss + 2 * lane) : 0u;
+
+  float p[kG];
+#pragma unroll
+  for (int h = 0; h < kG; ++h) {
+    float x = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x = dot2_bf16(qr[h][i].x, kr[i].x, x);
+      x = dot2_bf16(qr[h][i].y, kr[i].y, x);
+      x = dot2_bf16(qr[h][i].z, kr[i].z, x);
+      x = dot2_bf16(qr[h][i].w, kr[i].w, x);
+    }
+    x = quad_sum(x);
+    x = live ? x * a.scale_log2 : -INFINITY;
+    // Max and sum over the 16 slots: quad-uniform values, 4 quads per row, 4 rows per wave.
+    float mx = quads_max(x);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float e = fast_exp2(x - mx);
+    float z = quads_sum(e);
+    z += __shfl_xor(z, 16);
+    z += __shfl_xor(z, 32);
+    p[h] = round_bf16(e / z);
+  }
+
+  float o[kG][2];
+#pragma unroll
+  for (int h = 0; h < kG; ++h) o[h][0] = o[h][1] = 0.f;
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) {
+    const float lo = bf16_lo(vr[s]);
+    const float hi = bf16_hi(vr[s]);
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+      const float ps = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[h]), 4 * s));
+      o[h][0] = fmaf(ps, lo, o[h][0]);
+      o[h][1] = fmaf(ps, hi, o[h][1]);
+    }
+  }
+  uint16_t* ob = a.out + (int64_t)b * a.o_sb + (int64_t)(kG * g) * kD;
+#pragma unroll
+  for (int h = 0; h < kG; ++h)
+    *reinterpret_cast<uint32_t*>(ob + h * kD + 2 * lane) = pack_bf16x2(o[h][0], o[h][1]);
+}
+
+}  // namespace
+}  // namespace q3a
+
+using namespace q3a;
+
+extern "C" int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
+                           int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,
+                           int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads,
+                           int head_dim, int n_live, float softmax_scale, void* stream) {
+  if (batch < 0) return fail(Q3A_EINVAL, "cp_attn: batch %d < 0", batch);
+  if (batch == 0) return Q3A_OK;
+  if (head_dim != kD) return fail(Q3A_EINVAL, "cp_attn: head_dim %d unsupported (need %d)", head_dim, kD);
+  if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
+    return fail(Q3A_EINVAL, "cp_attn: num_q_heads %d must be %d * num_kv_heads %d", num_q_heads, kG, num_kv_heads);
+  if (n_live < 1 || n_live > kSlots) return fail(Q3A_EINVAL, "cp_attn: n_live %d outside [1, %d]", n_live, kSlots);
+  if (!q || !k || !v || !out) return fail(Q3A_EINVAL, "cp_attn: null pointer argument");
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;
+  if (align % 16 != 0) return fail(Q3A_EINVAL, "cp_attn: q/K/V/out must be 16-byte aligned");
+  if ((q_stride_b | kv_stride_b | kv_stride_h | kv_stride_s | o_stride_b) % 8 != 0)
+    return fail(Q3A_EINVAL, "cp_attn: strides must be multiples of 8 elements (16 bytes)");
+  const int64_t pairs = (int64_t)batch * num_kv_heads;
+  if (pairs > ((int64_t)1 << 30)) return fail(Q3A_EINVAL, "cp_attn: batch too large");
+
+  CpArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_stride_b;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.kv_sb = kv_stride_b;
+  a.kv_sh = kv_stride_h;
+  a.kv_ss = kv_stride_s;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_sb = o_stride_b;
+  a.pairs = (int)pairs;
+  a.hkv = num_kv_heads;
+  a.n_live = n_live;
+  a.scale_log2 = softmax_scale * kLog2e;
+  const int blocks = (int)((pairs + kWavesPerBlock - 1) / kWavesPerBlock);
+  hipLaunchKernelGGL(cp_attn_kernel, dim3(blocks), dim3(64 * kWavesPerBlock), 0,
+                     static_cast<hipStream_t>(stream), a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "cp_attn: launch failed: %s", hipGetErrorString(e));
+  return Q3A_OK;
+}

@@ -1,0 +1,84 @@
+// Shared device helpers and host error plumbing for the q3attn HIP library (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q3a {
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Running-max seed: finite, so exp2(m_old - m_new) never evaluates (-inf) - (-inf).
+constexpr float kMaxSeed = -1.0e30f;
+
+// ---------------------------------------------------------------------------------- arithmetic
+// a.lo*b.lo + a.hi*b.hi + c with bf16 pairs and an fp32 accumulator (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+// Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Round a float to the nearest bf16 value, returned as float.
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float(pack_bf16x2(x, 0.f) << 16);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------------- lane moves
+// DPP lane permutations within 16-lane rows.  All lanes of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within each 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <-> 15-i within each 16 lanes
+
+// Sum over each aligned group of 16 lanes; every lane of the group gets the same bits.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<kDppXor1>(x);
+  x += dpp_f32<kDppXor2>(x);
+  x += dpp_f32<kDppHalfMirror>(x);
+  x += dpp_f32<kDppMirror>(x);
+  return x;
+}
+
+// Sum over each aligned quad of lanes.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += dpp_f32<kDppXor1>(x);
+  x += dpp_f32<kDppXor2>(x);
+  return x;
+}
+
+// For values that are uniform within each quad: combine the 4 quads of a 16-lane row.
+__device__ __forceinline__ float quads_sum(float x) {
+  x += dpp_f32<kDppHalfMirror>(x);
+  x += dpp_f32<kDppMirror>(x);
+  return x;
+}
+__device__ __forceinline__ float quads_max(float x) {
+  x = fmaxf(x, dpp_f32<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp_f32<kDppMirror>(x));
+  return x;
+}
+
+}  // namespace q3a
+
+// ---------------------------------------------------------------------------------- host side
+namespace q3a {
+// Records a message for q3a_last_error() on this thread and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+}  // namespace q3a

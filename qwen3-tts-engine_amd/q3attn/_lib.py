@@ -1,0 +1,82 @@
+"""Loader for the q3attn C-ABI library (``libq3attn.so``, built from ``csrc/`` for gfx950).
+
+torch is imported first on purpose: the library's ``libamdhip64.so.7`` dependency then binds to
+the HIP runtime torch already loaded, so both share one runtime, one device context and the
+same stream handles.  There is no fallback: a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede the library load, see above)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
+ABI_VERSION = 1
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_vp = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+_c_float = ctypes.c_float
+
+# Exported symbols and their C signatures (include/q3attn.h).
+SIGNATURES = {
+    "q3a_abi_version": (_c_int, []),
+    "q3a_last_error": (ctypes.c_char_p, []),
+    "q3a_paged_decode": (_c_int, [
+        _c_vp, _c_i64, _c_i64,                      # q, q_stride_b, q_stride_h
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,       # k_cache, v_cache, kv strides (page, tok, head)
+        _c_int, _c_int,                             # num_pages, page_size
+        _c_vp, _c_vp, _c_i64, _c_int,               # cache_seqlens, block_table, bt_stride_b, max_pages
+        _c_vp, _c_i64, _c_i64,                      # out, o_stride_b, o_stride_h
+        _c_vp, _c_size,                             # workspace, workspace_bytes
+        _c_int, _c_int, _c_int, _c_int,             # batch, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                    # softmax_scale, split_tokens, stream
+    ]),
+    "q3a_paged_decode_workspace_bytes": (_c_size, [_c_int] * 7),
+    "q3a_paged_decode_default_split": (_c_int, [_c_int] * 4),
+    "q3a_cp_attn": (_c_int, [
+        _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,   # q, q_sb, k, v, kv strides (b, h, s)
+        _c_vp, _c_i64,                                         # out, o_stride_b
+        _c_int, _c_int, _c_int, _c_int, _c_int,                # batch, Hq, Hkv, D, n_live
+        _c_float, _c_vp,                                       # softmax_scale, stream
+    ]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class Q3AttnError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise Q3AttnError(
+                    f"q3attn: HIP library not found at {LIB_PATH}; build it first "
+                    "(python qwen3-tts-engine_amd/build.py or __graft_entry__.build())")
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            ver = handle.q3a_abi_version()
+            if ver != ABI_VERSION:
+                raise Q3AttnError(f"q3attn: library ABI {ver} != expected {ABI_VERSION}; rebuild")
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().q3a_last_error().decode(errors="replace")
+        raise Q3AttnError(f"{what} failed ({rc}): {msg}")

@@ -1,0 +1,120 @@
+"""Attention entry points of the talker, as torch custom ops over the q3attn C ABI.
+
+``flash_attn_with_kvcache`` keeps the call signature and tensor layouts the engine uses at
+engine/talker.py:77, so the talker's import line (engine/talker.py:13) can point here instead.
+The ops are registered with ``torch.library.custom_op`` (opaque to torch.compile, with fake
+implementations for tracing), enqueue on the current HIP stream, allocate only through torch's
+caching allocator and never synchronise, so they can be captured into HIP graphs.  They run on
+the GPU only: CPU tensors raise.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ._lib import check, lib
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table):
+    _req(q.is_cuda, "q3attn.paged_decode: tensors must be on a GPU (there is no CPU path)")
+    dev = q.device
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("cache_seqlens", cache_seqlens),
+                    ("block_table", block_table)):
+        _req(t.device == dev, f"q3attn.paged_decode: {name} is on {t.device}, q on {dev}")
+    _req(q.dtype == torch.bfloat16, f"q3attn.paged_decode: q must be bfloat16, got {q.dtype}")
+    _req(k_cache.dtype == torch.bfloat16 and v_cache.dtype == torch.bfloat16,
+         "q3attn.paged_decode: k_cache/v_cache must be bfloat16")
+    _req(q.dim() == 3, f"q3attn.paged_decode: q must be [batch, heads, head_dim], got {tuple(q.shape)}")
+    _req(k_cache.dim() == 4, "q3attn.paged_decode: k_cache must be [num_pages, page_size, kv_heads, head_dim]")
+    _req(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(),
+         "q3attn.paged_decode: k_cache and v_cache must have the same shape and strides")
+    _req(q.stride(-1) == 1 and k_cache.stride(-1) == 1, "q3attn.paged_decode: last dimension must be contiguous")
+    B, Hq, D = q.shape
+    _req(k_cache.shape[3] == D, "q3attn.paged_decode: head_dim mismatch between q and k_cache")
+    _req(cache_seqlens.dtype == torch.int32 and cache_seqlens.shape == (B,),
+         "q3attn.paged_decode: cache_seqlens must be int32 [batch]")
+    _req(cache_seqlens.is_contiguous(), "q3attn.paged_decode: cache_seqlens must be contiguous")
+    _req(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == B,
+         "q3attn.paged_decode: block_table must be int32 [batch, max_pages]")
+    _req(block_table.stride(1) == 1, "q3attn.paged_decode: block_table rows must be contiguous")
+
+
+@torch.library.custom_op("q3attn::paged_decode", mutates_args=())
+def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 cache_seqlens: torch.Tensor, block_table: torch.Tensor, softmax_scale: float,
+                 split_tokens: int = 0) -> torch.Tensor:
+    """o[b, h] = softmax(q[b, h] . K_b^T * scale) . V_b over the ctx = cache_seqlens[b] tokens of
+    row b, gathered through ``block_table``; query head h reads KV head h // (Hq / Hkv).
+
+    q [B, Hq, D] bf16; k_cache, v_cache [num_pages, page_size, Hkv, D] bf16; cache_seqlens [B]
+    int32; block_table [B, max_pages] int32.  Returns [B, Hq, D] bf16.  fp32 semantics:
+    engine/talker.py:82-88; the call it replaces: engine/talker.py:77.
+    """
+    _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table)
+    B, Hq, D = q.shape
+    num_pages, page, Hkv, _ = k_cache.shape
+    max_pages = block_table.shape[1]
+    out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    if B == 0:
+        return out
+    L = lib()
+    split = int(split_tokens) or L.q3a_paged_decode_default_split(B, Hkv, max_pages, page)
+    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    rc = L.q3a_paged_decode(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        num_pages, page,
+        cache_seqlens.data_ptr(), block_table.data_ptr(), block_table.stride(0), max_pages,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), ws_bytes,
+        B, Hq, Hkv, D, float(softmax_scale), split, _stream(q.device))
+    check(rc, "q3a_paged_decode")
+    return out
+
+
+@paged_decode.register_fake
+def _paged_decode_fake(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, split_tokens=0):
+    return q.new_empty(q.shape)
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
+                            cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None,
+                            block_table=None, softmax_scale=None, causal=False, window_size=(-1, -1),
+                            softcap=0.0, rotary_interleaved=True, alibi_slopes=None, num_splits=0,
+                            return_softmax_lse=False):
+    """Drop-in for the paged-decode subset of ``flash_attn.flash_attn_with_kvcache`` that the talker
+    calls (engine/talker.py:77): q [B, 1, Hq, D], paged caches, int32 ``cache_seqlens`` and
+    ``block_table``, ``softmax_scale``, ``causal`` (a no-op for one query token).  Returns
+    [B, 1, Hq, D].  Arguments the talker does not use raise NotImplementedError."""
+    unsupported = {"k": k, "v": v, "rotary_cos": rotary_cos, "rotary_sin": rotary_sin,
+                   "cache_batch_idx": cache_batch_idx, "cache_leftpad": cache_leftpad,
+                   "alibi_slopes": alibi_slopes}
+    for name, val in unsupported.items():
+        if val is not None:
+            raise NotImplementedError(f"q3attn.flash_attn_with_kvcache: argument {name!r} is not supported")
+    if tuple(window_size) != (-1, -1) or softcap != 0.0 or return_softmax_lse:
+        raise NotImplementedError("q3attn.flash_attn_with_kvcache: window_size/softcap/return_softmax_lse unsupported")
+    _req(cache_seqlens is not None and block_table is not None,
+         "q3attn.flash_attn_with_kvcache: cache_seqlens and block_table are required")
+    _req(q.dim() == 4 and q.shape[1] == 1,
+         f"q3attn.flash_attn_with_kvcache: q must be [batch, 1, heads, head_dim], got {tuple(q.shape)}")
+    if isinstance(cache_seqlens, int):
+        cache_seqlens = torch.full((q.shape[0],), cache_seqlens, dtype=torch.int32, device=q.device)
+    scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
+    split = 0
+    if num_splits and num_splits > 0:
+        max_ctx = block_table.shape[1] * k_cache.shape[1]
+        split = max(16, 16 * math.ceil(math.ceil(max_ctx / num_splits) / 16))
+    o = paged_decode(q[:, 0], k_cache, v_cache, cache_seqlens, block_table, float(scale), split)
+    return o.unsqueeze(1)

@@ -1,0 +1,183 @@
+"""Seeded synthetic inputs for the attention hot path, at the engine's real shapes.
+
+q and k are drawn N(0, 1), scaled to unit RMS per head (the role of the qk-RMSNorm,
+engine/ops.py:51-55) and rotated by rotate-half RoPE with theta = 1e6 (engine/ops.py:58-60) at
+each token's position; v is N(0, 1).  Everything is generated on the target device with a seeded
+``torch.Generator``; integer draws (context lengths, page permutations) use numpy's seeded PCG64.
+
+Decode workloads (16 query heads over 8 KV heads, head_dim 128, pages of 16 tokens):
+  * ``c1``: 1 row, ctx 64, identity page table (the CPU-runnable case);
+  * ``c3``: 256 rows, ctx ~ U[200, 1200], random table over a 65,536-page pool;
+  * ``c5``: 576 rows, 518 live with ctx = round(exp(U[ln 64, ln 1800])) and 58 padded rows with
+    ctx = 0 at the tail, random table over a 131,072-page pool.
+The code-predictor workload ``cp`` is 512 rows with dense 16-slot K/V buffers.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import numpy as np
+import torch
+
+HQ, HKV, HEAD_DIM, PAGE = 16, 8, 128, 16
+ROPE_THETA = 1.0e6
+
+
+def rope_tables(n_pos: int, device, head_dim: int = HEAD_DIM, theta: float = ROPE_THETA):
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64, device=device) / head_dim))
+    ang = torch.arange(n_pos, dtype=torch.float64, device=device)[:, None] * inv[None, :]
+    emb = torch.cat([ang, ang], dim=-1)
+    return emb.cos().float(), emb.sin().float()
+
+
+def _unit_rms(x: torch.Tensor) -> torch.Tensor:
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+
+
+def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return x * cos + torch.cat((-x[..., h:], x[..., :h]), dim=-1) * sin
+
+
+@dataclasses.dataclass
+class DecodeLayer:
+    q: torch.Tensor              # [B, Hq, D] bf16
+    block_table: torch.Tensor    # [B, max_pages] int32
+
+
+@dataclasses.dataclass
+class DecodeWorkload:
+    name: str
+    k_cache: torch.Tensor        # [num_pages, page, Hkv, D] bf16
+    v_cache: torch.Tensor
+    cache_seqlens: torch.Tensor  # [B] int32
+    layers: list                 # list[DecodeLayer]
+    ctx: np.ndarray              # host copy of the context lengths
+    scale: float = HEAD_DIM ** -0.5
+
+    @property
+    def batch(self) -> int:
+        return int(self.ctx.shape[0])
+
+    @property
+    def page_size(self) -> int:
+        return int(self.k_cache.shape[1])
+
+    def algorithmic_bytes(self) -> int:
+        """Bytes one decode call must move: K+V of every attended token, q in, o out, the page-table
+        entries read and the context lengths."""
+        return decode_bytes(self.ctx, self.page_size, HQ, int(self.k_cache.shape[2]), int(self.k_cache.shape[3]))
+
+
+def decode_bytes(ctx, page: int, hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM) -> int:
+    ctx = np.asarray(ctx, dtype=np.int64)
+    kv = 2 * hkv * d * 2 * int(ctx.sum())
+    qo = 2 * hq * d * 2 * int(ctx.shape[0])
+    pages = 4 * int(((ctx + page - 1) // page).sum())
+    return kv + qo + pages + 4 * int(ctx.shape[0])
+
+
+def draw_contexts(name: str, seed: int = 0) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    if name == "c1":
+        return np.array([64], dtype=np.int64)
+    if name == "c3":
+        return rng.integers(200, 1201, size=256).astype(np.int64)
+    if name == "c5":
+        n_rows, n_pad = 576, 58
+        live = np.rint(np.exp(rng.uniform(math.log(64), math.log(1800), size=n_rows - n_pad))).astype(np.int64)
+        return np.concatenate([live, np.zeros(n_pad, dtype=np.int64)])
+    raise ValueError(f"unknown decode workload {name!r}")
+
+
+POOL_PAGES = {"c1": 4, "c3": 65536, "c5": 131072}
+MAX_CTX = {"c1": 64, "c3": 1200, "c5": 1800}
+
+
+def make_decode(name: str, device, layers: int = 1, seed: int = 0, ctx: np.ndarray | None = None,
+                num_pages: int | None = None, max_ctx: int | None = None, page: int = PAGE,
+                identity: bool | None = None, chunk_pages: int = 4096) -> DecodeWorkload:
+    """Build a decode workload.  ``ctx``/``num_pages``/``max_ctx`` override the named config (used
+    by the tests for small ragged cases)."""
+    device = torch.device(device)
+    ctx = draw_contexts(name, seed) if ctx is None else np.asarray(ctx, dtype=np.int64)
+    num_pages = POOL_PAGES.get(name) if num_pages is None else num_pages
+    max_ctx = MAX_CTX.get(name, int(ctx.max(initial=1))) if max_ctx is None else max_ctx
+    identity = (name == "c1") if identity is None else identity
+    B = int(ctx.shape[0])
+    P = max(1, -(-max_ctx // page))
+    if B * P > num_pages:
+        raise ValueError(f"pool of {num_pages} pages cannot hold {B} rows x {P} pages")
+    rng = np.random.default_rng(seed + 1)
+    tables = []
+    for layer in range(layers):
+        if identity:
+            bt = np.arange(B * P, dtype=np.int64).reshape(B, P)
+        else:
+            bt = rng.permutation(num_pages)[: B * P].reshape(B, P)
+        tables.append(bt)
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    # Token positions of each pool page under layer 0's table (unreferenced pages: position 0).
+    pos_base = np.zeros(num_pages, dtype=np.int64)
+    pos_base[tables[0].reshape(-1)] = np.tile(np.arange(P, dtype=np.int64) * page, B)
+    pos_base_t = torch.from_numpy(pos_base).to(device)
+    cos, sin = rope_tables(max(P * page, 1), device)
+
+    k_cache = torch.empty((num_pages, page, HKV, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    v_cache = torch.empty_like(k_cache)
+    ar = torch.arange(page, device=device)
+    for c0 in range(0, num_pages, chunk_pages):
+        n = min(chunk_pages, num_pages - c0)
+        x = _unit_rms(torch.randn((n, page, HKV, HEAD_DIM), generator=gen, device=device))
+        pos = pos_base_t[c0:c0 + n, None] + ar[None, :]
+        x = _rope(x, cos[pos][:, :, None, :], sin[pos][:, :, None, :])
+        k_cache[c0:c0 + n] = x.to(torch.bfloat16)
+        v_cache[c0:c0 + n] = torch.randn((n, page, HKV, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        del x
+
+    qpos = torch.from_numpy(np.maximum(ctx - 1, 0)).to(device)
+    out_layers = []
+    for layer in range(layers):
+        q = _unit_rms(torch.randn((B, HQ, HEAD_DIM), generator=gen, device=device))
+        q = _rope(q, cos[qpos][:, None, :], sin[qpos][:, None, :]).to(torch.bfloat16)
+        out_layers.append(DecodeLayer(q=q, block_table=torch.from_numpy(tables[layer]).to(torch.int32).to(device)))
+    seqlens = torch.from_numpy(ctx).to(torch.int32).to(device)
+    return DecodeWorkload(name=name, k_cache=k_cache, v_cache=v_cache, cache_seqlens=seqlens,
+                          layers=out_layers, ctx=ctx)
+
+
+@dataclasses.dataclass
+class CpWorkload:
+    q: torch.Tensor      # [B, Hq, D] bf16, one per AR step (list)
+    K: torch.Tensor      # [B, Hkv, 16, D] bf16
+    V: torch.Tensor
+    scale: float = HEAD_DIM ** -0.5
+
+
+def make_cp(batch: int, device, seed: int = 0, steps: int = 16, kv_pad: int = 0) -> tuple:
+    """Dense 16-slot K/V scratch (engine/code_predictor.py:20-21) filled for all 16 slots and one
+    query per step p (RoPE at position p).  ``kv_pad`` > 0 allocates the slot rows wider than
+    head_dim to exercise non-trivial strides.  Returns (qs: list of [B, Hq, D], K, V)."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    cos, sin = rope_tables(16, device)
+    Kb = torch.zeros((batch, HKV, 16, HEAD_DIM + kv_pad), dtype=torch.bfloat16, device=device)
+    Vb = torch.zeros_like(Kb)
+    k = _unit_rms(torch.randn((batch, HKV, 16, HEAD_DIM), generator=gen, device=device))
+    k = _rope(k, cos[None, None], sin[None, None])
+    Kb[..., :HEAD_DIM] = k.to(torch.bfloat16)
+    Vb[..., :HEAD_DIM] = torch.randn((batch, HKV, 16, HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+    qs = []
+    for p in range(steps):
+        q = _unit_rms(torch.randn((batch, HQ, HEAD_DIM), generator=gen, device=device))
+        qs.append(_rope(q, cos[p], sin[p]).to(torch.bfloat16))
+    return qs, Kb[..., :HEAD_DIM], Vb[..., :HEAD_DIM]
+
+
+def cp_bytes(batch: int, n_live: int, hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM) -> int:
+    """Bytes of one cp_attn call: K+V of the live slots, q in, o out."""
+    return batch * (2 * hkv * n_live * d * 2 + 2 * hq * d * 2)

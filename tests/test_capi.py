@@ -1,0 +1,128 @@
+"""CPU tests of the boundary: the C-ABI library loads, exports every symbol include/q3attn.h
+declares, rejects bad arguments with error codes and messages (no kernel is launched), and the
+Python entry points refuse CPU tensors instead of falling back to anything."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import q3attn
+from q3attn import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "q3attn.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(q3a_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = _declared()
+    assert "q3a_paged_decode" in names and "q3a_cp_attn" in names
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert L.q3a_abi_version() == _lib.ABI_VERSION
+
+
+def _decode(**kw):
+    args = dict(q=16, q_sb=2048, q_sh=128, k=16, v=16, sp=16384, st=1024, sh=128, num_pages=8, page=16,
+                seqlens=16, bt=16, bt_sb=4, max_pages=4, out=16, o_sb=2048, o_sh=128, ws=16, ws_bytes=1 << 30,
+                B=2, Hq=16, Hkv=8, D=128, scale=0.088, split=0)
+    args.update(kw)
+    L = _lib.lib()
+    return L.q3a_paged_decode(args["q"], args["q_sb"], args["q_sh"], args["k"], args["v"], args["sp"], args["st"],
+                              args["sh"], args["num_pages"], args["page"], args["seqlens"], args["bt"],
+                              args["bt_sb"], args["max_pages"], args["out"], args["o_sb"], args["o_sh"],
+                              args["ws"], args["ws_bytes"], args["B"], args["Hq"], args["Hkv"], args["D"],
+                              args["scale"], args["split"], None)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(D=64), "head_dim"),
+    (dict(Hq=8), "num_q_heads"),
+    (dict(Hkv=32, Hq=64), "num_kv_heads"),
+    (dict(page=24), "page_size"),
+    (dict(q=None), "null pointer"),
+    (dict(q=18), "aligned"),
+    (dict(st=1020), "strides"),
+    (dict(split=40), "split_tokens"),
+    (dict(max_pages=4096, split=16), "splits exceed"),
+    (dict(ws_bytes=10), "workspace"),
+    (dict(B=-1), "batch"),
+])
+def test_paged_decode_rejects_bad_arguments(kw, frag):
+    rc = _decode(**kw)
+    assert rc < 0
+    assert frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_paged_decode_empty_batch_is_a_noop():
+    assert _decode(B=0) == 0
+
+
+def test_workspace_and_default_split():
+    L = _lib.lib()
+    # C5 shape: 576 rows, 113 pages of 16 tokens
+    split = L.q3a_paged_decode_default_split(576, 8, 113, 16)
+    assert split % 16 == 0 and split >= 16
+    n_splits = -(-113 * 16 // split)
+    assert n_splits <= 64
+    assert L.q3a_paged_decode_workspace_bytes(576, 16, 8, 128, 113, 16, split) == 576 * n_splits * 8 * 260 * 4
+    # one split: no workspace
+    assert L.q3a_paged_decode_workspace_bytes(4, 16, 8, 128, 4, 16, 64) == 0
+    # small batches get smaller splits (more workgroups)
+    assert L.q3a_paged_decode_default_split(1, 8, 4, 16) == 16
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(n_live=0), "n_live"), (dict(n_live=17), "n_live"), (dict(D=64), "head_dim"),
+    (dict(Hq=12), "num_q_heads"), (dict(q=None), "null"), (dict(kv_ss=100), "strides"),
+])
+def test_cp_attn_rejects_bad_arguments(kw, frag):
+    a = dict(q=16, q_sb=2048, k=16, v=16, kv_sb=16384, kv_sh=2048, kv_ss=128, out=16, o_sb=2048,
+             B=4, Hq=16, Hkv=8, D=128, n_live=3, scale=0.088)
+    a.update(kw)
+    rc = _lib.lib().q3a_cp_attn(a["q"], a["q_sb"], a["k"], a["v"], a["kv_sb"], a["kv_sh"], a["kv_ss"], a["out"],
+                                a["o_sb"], a["B"], a["Hq"], a["Hkv"], a["D"], a["n_live"], a["scale"], None)
+    assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_python_entry_points_refuse_cpu_tensors():
+    q = torch.zeros(2, 1, 16, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16)
+    sl = torch.ones(2, dtype=torch.int32)
+    bt = torch.zeros(2, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        q3attn.flash_attn_with_kvcache(q, kc, kc, cache_seqlens=sl, block_table=bt, softmax_scale=0.1, causal=True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        q3attn.cp_attn(torch.zeros(2, 16, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16),
+                       torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16), 3, 0.1)
+
+
+def test_unsupported_flash_attn_arguments_raise():
+    q = torch.zeros(2, 1, 16, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        q3attn.flash_attn_with_kvcache(q, kc, kc, k=q, cache_seqlens=torch.ones(2, dtype=torch.int32),
+                                       block_table=torch.zeros(2, 2, dtype=torch.int32))
+
+
+def test_fake_impl_traces_shapes():
+    """The custom ops carry fake implementations, so torch.compile / export can trace through them
+    without running the kernels."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        q = torch.empty(3, 16, 128, dtype=torch.bfloat16)
+        kc = torch.empty(10, 16, 8, 128, dtype=torch.bfloat16)
+        o = torch.ops.q3attn.paged_decode(q, kc, kc, torch.empty(3, dtype=torch.int32),
+                                          torch.empty(3, 4, dtype=torch.int32), 0.1, 0)
+        assert o.shape == (3, 16, 128) and o.dtype == torch.bfloat16
+        c = torch.ops.q3attn.cp_attn(q, torch.empty(3, 8, 16, 128, dtype=torch.bfloat16),
+                                     torch.empty(3, 8, 16, 128, dtype=torch.bfloat16), 4, 0.1)
+        assert c.shape == (3, 2048)

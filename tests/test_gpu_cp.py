@@ -1,0 +1,72 @@
+"""GPU parity of the code-predictor attention (q3a_cp_attn through the C ABI) against the oracle's
+two reference rounding sequences (engine/cp_attn.py:19-30 and engine/code_predictor.py:46-47)."""
+import numpy as np
+import pytest
+import torch
+
+import q3attn
+from helpers import to_np
+from oracle import attention as ora
+from q3attn import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(qs, K, V):
+    return [to_np(q) for q in qs], to_np(K), to_np(V)
+
+
+@pytest.mark.parametrize("kv_pad", [0, 8])
+def test_all_steps_c2(cuda_device, kv_pad):
+    B = 512
+    qs, K, V = W.make_cp(B, cuda_device, seed=kv_pad, kv_pad=kv_pad)
+    qn, Kn, Vn = _np(qs, K, V)
+    for p in range(16):
+        n_live = p + 1
+        o = q3attn.cp_attn(qs[p], K, V, n_live, W.HEAD_DIM ** -0.5)
+        torch.cuda.synchronize()
+        got = to_np(o)
+        for fn in (ora.cp_attn_triton_path, ora.cp_attn_torch_path):
+            ok, st = ora.compare(got, fn(qn[p], Kn, Vn, n_live, W.HEAD_DIM ** -0.5))
+            print(f"[parity] cp n_live={n_live} pad={kv_pad} {fn.__name__} {st}", flush=True)
+            assert ok, (n_live, fn.__name__, st)
+
+
+def test_n_live_1_is_exact(cuda_device):
+    qs, K, V = W.make_cp(64, cuda_device, seed=3)
+    o = q3attn.cp_attn(qs[0], K, V, 1, 0.088).reshape(64, 8, 2, 128)
+    torch.cuda.synchronize()
+    assert torch.equal(o, V[:, :, 0:1].expand(-1, -1, 2, -1))
+
+
+def test_stale_slots_never_read(cuda_device):
+    qs, K, V = W.make_cp(128, cuda_device, seed=4)
+    for n_live in (1, 6, 15):
+        a = q3attn.cp_attn(qs[n_live - 1], K, V, n_live, 0.088)
+        Kp, Vp = K.clone(), V.clone()
+        Kp[:, :, n_live:] = float("nan")
+        Vp[:, :, n_live:] = float("nan")
+        b = q3attn.cp_attn(qs[n_live - 1], Kp, Vp, n_live, 0.088)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+
+
+def test_batch_stride_wider_than_live_batch(cuda_device):
+    """K/V are slices [l, :B] of a [layers, max_bs, 8, 16, 128] scratch (engine/code_predictor.py:56)."""
+    max_bs, B = 96, 40
+    qs, K, V = W.make_cp(max_bs, cuda_device, seed=5)
+    Kbig = torch.stack([torch.zeros_like(K), K])
+    Vbig = torch.stack([torch.zeros_like(V), V])
+    o = q3attn.cp_attn(qs[9][:B].reshape(B, 2048), Kbig[1, :B], Vbig[1, :B], 10, 0.088)
+    full = q3attn.cp_attn(qs[9], K, V, 10, 0.088)
+    torch.cuda.synchronize()
+    assert torch.equal(o, full[:B])
+
+
+def test_odd_batch_sizes(cuda_device):
+    for B in (1, 3, 5, 272, 577):
+        qs, K, V = W.make_cp(B, cuda_device, seed=B, steps=4)
+        o = q3attn.cp_attn(qs[3], K, V, 4, 0.088)
+        torch.cuda.synchronize()
+        ok, st = ora.compare(to_np(o), ora.cp_attn_triton_path(to_np(qs[3]), to_np(K), to_np(V), 4, 0.088))
+        assert ok, (B, st)

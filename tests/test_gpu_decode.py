@@ -1,0 +1,156 @@
+"""GPU parity of the talker paged decode (q3a_paged_decode through the C ABI) against the oracle.
+
+Bar (bf16 output): max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32-softmax oracle on the same
+bf16 inputs.  Full-size workloads are checked on an oracle subset plus size-independent properties
+(bitwise determinism, page-table permutation invariance, split-size invariance)."""
+import numpy as np
+import pytest
+import torch
+
+import q3attn
+from helpers import decode_oracle, to_np
+from oracle import attention as ora
+from q3attn import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def run(wl, layer=0, split=0, q=None, k=None, v=None, bt=None, seqlens=None):
+    L = wl.layers[layer]
+    q = L.q if q is None else q
+    out = q3attn.flash_attn_with_kvcache(
+        q.unsqueeze(1), wl.k_cache if k is None else k, wl.v_cache if v is None else v,
+        cache_seqlens=wl.cache_seqlens if seqlens is None else seqlens,
+        block_table=L.block_table if bt is None else bt, softmax_scale=wl.scale, causal=True,
+        num_splits=0) if split == 0 else q3attn.paged_decode(
+        q, wl.k_cache if k is None else k, wl.v_cache if v is None else v,
+        wl.cache_seqlens if seqlens is None else seqlens, L.block_table if bt is None else bt, wl.scale, split)
+    torch.cuda.synchronize()
+    return out[:, 0] if out.dim() == 4 else out
+
+
+def assert_parity(out, ref, what=""):
+    ok, st = ora.compare(to_np(out), ref)
+    print(f"[parity] {what} {st}", flush=True)
+    assert ok, (what, st)
+
+
+RAGGED = [0, 1, 2, 15, 16, 17, 31, 33, 63, 64, 65, 100, 127, 128, 129, 200, 255, 256, 257, 511, 700, 1023, 1800, 5]
+
+
+def test_c1_single_row(cuda_device):
+    wl = W.make_decode("c1", cuda_device)
+    out = run(wl)
+    assert_parity(out, decode_oracle(wl), "c1")
+
+
+@pytest.mark.parametrize("split", [0, 32, 64, 128, 2048])
+def test_ragged_contexts_all_splits(cuda_device, split):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=5)
+    out = run(wl, split=split)
+    ref = decode_oracle(wl)
+    assert_parity(out, ref, f"ragged split={split}")
+    assert not out[0].float().abs().sum().item(), "ctx == 0 row must be zeros"
+
+
+def test_short_contexts_split16(cuda_device):
+    ctx = np.array([c for c in RAGGED if c <= 1000])
+    wl = W.make_decode("short", cuda_device, ctx=ctx, num_pages=2048, max_ctx=1000, seed=4)
+    assert_parity(run(wl, split=16), decode_oracle(wl), "short split=16")
+
+
+def test_ctx1_is_exact_v_row(cuda_device):
+    wl = W.make_decode("one", cuda_device, ctx=np.array([1, 1, 1]), num_pages=64, max_ctx=64, seed=9)
+    out = run(wl)
+    bt = wl.layers[0].block_table[:, 0].long()
+    want = wl.v_cache[bt, 0]                                   # [B, Hkv, D]
+    assert torch.equal(out, want.repeat_interleave(2, dim=1))
+
+
+def test_reference_layout_page256_identity(cuda_device):
+    """The reference's own pool geometry: 256-token pages, identity table, seat_len 768
+    (engine/talker.py:23-31, 42)."""
+    ctx = np.array([1, 77, 255, 256, 257, 420, 767, 768])
+    wl = W.make_decode("ref", cuda_device, ctx=ctx, num_pages=8 * 3, max_ctx=768, page=256, identity=True, seed=2)
+    assert_parity(run(wl), decode_oracle(wl), "page256")
+
+
+def test_stale_nan_slots_and_garbage_table_entries(cuda_device):
+    """Slots past ctx in a row's last page and table entries past its last page are never read."""
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=6)
+    clean = run(wl)
+    bt = wl.layers[0].block_table.clone()
+    k, v = wl.k_cache.clone(), wl.v_cache.clone()
+    page = wl.page_size
+    for b, c in enumerate(RAGGED):
+        used = (c + page - 1) // page
+        if c % page:
+            pg = int(bt[b, used - 1])
+            k[pg, c % page:] = float("nan")
+            v[pg, c % page:] = float("nan")
+        bt[b, used:] = -7 if b % 2 else 1 << 30
+    dirty = run(wl, k=k, v=v, bt=bt)
+    assert torch.equal(clean, dirty)
+
+
+def test_out_of_range_page_ids_do_not_fault(cuda_device):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array([40, 40]), num_pages=64, max_ctx=64, seed=3)
+    bt = wl.layers[0].block_table.clone()
+    bt[0, 1] = -1
+    bt[1, 0] = 1 << 30
+    out = run(wl, bt=bt)
+    assert torch.isfinite(out.float()).all()
+
+
+def test_page_table_permutation_invariance(cuda_device):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=8)
+    a = run(wl)
+    perm = torch.randperm(4096, generator=torch.Generator().manual_seed(1)).to(cuda_device)
+    inv = torch.argsort(perm)
+    b = run(wl, k=wl.k_cache[perm], v=wl.v_cache[perm], bt=inv[wl.layers[0].block_table.long()].int())
+    assert torch.equal(a, b)
+
+
+def test_strided_cache_and_query(cuda_device):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED[:12]), num_pages=512, max_ctx=256, seed=10)
+    NP, P, H, D = wl.k_cache.shape
+    kb = torch.zeros(NP, P, H, D + 8, dtype=torch.bfloat16, device=cuda_device)
+    vb = torch.zeros_like(kb)
+    kb[..., :D] = wl.k_cache
+    vb[..., :D] = wl.v_cache
+    qkv = torch.zeros(wl.batch, 4096, dtype=torch.bfloat16, device=cuda_device)
+    qkv[:, :2048] = wl.layers[0].q.reshape(wl.batch, 2048)
+    q = qkv[:, :2048].view(wl.batch, 16, 128)                   # row stride 4096
+    out = run(wl, q=q, k=kb[..., :D], v=vb[..., :D])
+    assert torch.equal(out, run(wl))
+
+
+def test_c3_full(cuda_device):
+    wl = W.make_decode("c3", cuda_device)
+    out = run(wl)
+    assert_parity(out, decode_oracle(wl), "c3")
+    del wl
+    torch.cuda.empty_cache()
+
+
+def test_c5_full_size(cuda_device):
+    wl = W.make_decode("c5", cuda_device, layers=2)
+    ctx = wl.ctx
+    out0 = run(wl, 0)
+    # oracle on a subset: the longest, shortest and padded rows plus a seeded sample
+    rng = np.random.default_rng(0)
+    rows = sorted(set([int(ctx.argmax()), int(np.argmin(np.where(ctx > 0, ctx, 10 ** 9))), 575, 520])
+                  | set(rng.choice(576, 60, replace=False).tolist()))
+    assert_parity(out0[rows], decode_oracle(wl, 0, rows), "c5 layer0 subset")
+    out1 = run(wl, 1)
+    assert_parity(out1[rows], decode_oracle(wl, 1, rows), "c5 layer1 subset")
+    assert not out0[518:].float().abs().sum().item()
+    # bitwise determinism
+    assert torch.equal(out0, run(wl, 0))
+    # split-size invariance (different reduction trees; within rounding)
+    for split in (32, 256):
+        o = run(wl, 0, split=split)
+        ok, st = ora.compare(to_np(o), to_np(out0), max_abs=8e-3, mean_abs=2e-4)
+        assert ok, (split, st)
+    del wl
+    torch.cuda.empty_cache()
