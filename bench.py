@@ -96,6 +96,8 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (calibrates rocprof byte counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -111,6 +113,15 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
+        return 0
     t0 = time.time()
     wl = W.make_decode("c5", dev, layers=LAYERS, seed=args.seed)
     torch.cuda.synchronize()
@@ -156,8 +167,7 @@ def main() -> int:
         cpu = cpu_baseline(wl)
         log(f"[bench] cpu baseline {cpu['us_per_layer_call']:.0f} us/call in {time.time() - t0:.1f} s")
 
-    split = args.split or q3attn.lib().q3a_paged_decode_default_split(wl.batch, 8, wl.layers[0].block_table.shape[1],
-                                                                    wl.page_size)
+    split = args.split or "stream-K"
     rec = {
         "metric": METRIC,
         "value": round(us_per_step, 2),
@@ -191,7 +201,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None,
-            "kernel": "paged_decode_split_kernel + paged_decode_combine_kernel (one decode call)",
+            "kernel": "paged decode call (decode kernel + combine kernel)",
             "bytes_per_call": nbytes,
         },
         "cpu_baseline": cpu,

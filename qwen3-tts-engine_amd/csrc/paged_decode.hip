@@ -4,16 +4,23 @@
 // head h, o[b,h] = softmax(q[b,h] . K[b, h/2, :ctx]^T * scale) . V[b, h/2, :ctx], where token t of
 // row b sits in page block_table[b][t / page_size] at offset t % page_size.
 //
-// Work decomposition.  One workgroup = (row b, split s) with one wave per KV head.  A split is
-// `split_tokens` consecutive context tokens; rows shorter than that have one split and write the
-// output directly, longer rows write fp32 partials (running max m, sum l, unnormalised o) that the
-// combine kernel merges.  Inside a wave, one load instruction fetches 4 tokens x 256 B of one KV
-// head (lane l: token l/16, dims 8*(l%16)..+8, 16 B per lane), so a page of 16 tokens is 4
-// instructions for K and 4 for V, and the 8 waves of the workgroup together sweep each 32 KiB page
-// contiguously.  Both query heads of the GQA pair are applied to every K/V register the wave loads.
-// Each 16-lane group keeps its own online-softmax state over the tokens it saw; the four groups
-// are merged once at the end of the split.  The next 16-token tile is loaded while the current
-// one is computed.
+// Tile engine.  A wave streams 16-token tiles of one KV head: one 16 B buffer load per lane fetches
+// 4 tokens x 256 B (lane l: token l/16, dims 8*(l%16)..+8), so a tile is 4 loads of K and 4 of V;
+// the loads carry the non-temporal hint and are bounds-checked by the buffer descriptor (tokens
+// past the context and invalid pages return zeros without touching memory).  Two register tiles
+// alternate so one is in flight while the other is consumed.  Both query heads of the GQA pair
+// are applied to every loaded K/V register (bf16 dot2 for q.k, fp32 FMA for p.v).  Each 16-lane
+// group keeps its own online-softmax state; the four groups are merged at the end of a segment.
+// The tiles a wave will stream are described lane-wise (lane i = tile i: page, offset, valid
+// tokens), so the per-tile page lookup is a v_readlane, not a memory access.
+//
+// Work decomposition (default): stream-K.  The grid is exactly the number of workgroups the GPU
+// holds at once; the flattened sequence of (row, tile) pairs is cut into equal contiguous ranges,
+// one per workgroup, and every wave of a workgroup streams its KV head over that range.  Rows that
+// straddle a range boundary leave fp32 partials (m, l, unnormalised o) in at most two slots per
+// workgroup; the combine kernel merges them and writes zeros for ctx == 0 rows.
+// Alternative (split_tokens > 0): one workgroup per (row, fixed-size split), partials merged by
+// the same kind of combine.
 #include "q3a_common.h"
 #include "../../include/q3attn.h"
 
@@ -25,6 +32,10 @@ constexpr int kG = 2;                              // query heads per KV head
 constexpr int kPartFloats = kG * kD + 2 * kG;      // acc[G][D], m[G], l[G]
 constexpr int kMaxSplits = 64;
 constexpr int kTile = 16;                          // tokens per pipeline stage
+constexpr int kMaxSplitTokens = 64 * kTile;        // one VGPR lane per tile of a split
+constexpr int kSkMaxRows = 4096;                   // rows the stream-K prologue scans in LDS
+constexpr int kSkSlots = 2;                        // partial records per stream-K workgroup
+constexpr int kSkMaxGrid = 4096;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -33,14 +44,16 @@ struct DecodeArgs {
   const uint16_t* vc;
   int64_t kv_sp, kv_st, kv_sh;
   int num_pages, page_size;
+  uint32_t page_bytes;  // byte extent of one page's tokens (bounds of the buffer loads)
   const int32_t* seqlens;
   const int32_t* bt;
   int64_t bt_sb;
   int max_pages;
   uint16_t* out;
   int64_t o_sb, o_sh;
-  float* ws;
-  int hkv, split_tokens, max_splits;
+  float* ws;            // partial records
+  int* prefix;          // stream-K: [batch + 1] tile prefix sums
+  int batch, hkv, split_tokens, max_splits, grid;
   float scale_log2;
 };
 
@@ -49,45 +62,55 @@ struct KVTile {
   uint4 v[4];
 };
 
-__device__ __forceinline__ int row_ctx(const DecodeArgs& a, int b) {
-  const int c = a.seqlens[b];
+// Up to 64 consecutive tiles of one wave, described lane-wise.
+struct TileList {
+  int page;    // lane i: page index of tile i
+  int off;     // lane i: token offset of tile i inside its page
+  int nvalid;  // lane i: valid tokens of tile i (1..16), 0 past the list
+  int n;       // number of tiles (uniform)
+};
+
+__device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int c) {
   const int cap = a.max_pages * a.page_size;
   return c < 0 ? 0 : (c > cap ? cap : c);
 }
 
-// Loads the 16-token tile starting at context token t (t % 16 == 0) for KV head g.  Tokens at or
-// past t1 and tokens of an out-of-range page are not read and come back as zeros.
-__device__ __forceinline__ bool load_tile(const DecodeArgs& a, int b, int g, int grp, int dl, int t,
-                                          int t1, KVTile& T) {
-  const int pidx = t / a.page_size;
-  const int off = t - pidx * a.page_size;
-  const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
-  const bool page_ok = (unsigned)page < (unsigned)a.num_pages;
-  const int64_t base = (int64_t)page * a.kv_sp + (int64_t)g * a.kv_sh + dl;
+__device__ __forceinline__ int readlane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+// Issues the 8 loads of tile j.  A tile past the list or with an invalid page issues loads against a
+// zero-length descriptor (they return zeros and read nothing), so every path issues the same number
+// of loads and the compiler's vmcnt bookkeeping stays exact across the ping-pong buffers.
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, const TileList& L, uint32_t lane_off,
+                                           int grp, int j, KVTile& T) {
+  const int jj = j < L.n ? j : 0;
+  const int page = readlane(L.page, jj);
+  const int off = readlane(L.off, jj);
+  const int nv = j < L.n ? readlane(L.nvalid, jj) : 0;
+  const bool ok = nv > 0 && (unsigned)page < (unsigned)a.num_pages;
+  const int64_t pbase = ok ? (int64_t)page * a.kv_sp : 0;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kc + pbase, ok ? a.page_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + pbase, ok ? a.page_bytes : 0u);
+  const uint32_t tok_bytes = (uint32_t)(a.kv_st * 2);
+  const uint32_t base = lane_off + (uint32_t)off * tok_bytes;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int tok = 4 * i + grp;
-    if (page_ok && t + tok < t1) {
-      const int64_t o = base + (int64_t)(off + tok) * a.kv_st;
-      T.k[i] = *reinterpret_cast<const uint4*>(a.kc + o);
-      T.v[i] = *reinterpret_cast<const uint4*>(a.vc + o);
-    } else {
-      T.k[i] = make_uint4(0u, 0u, 0u, 0u);
-      T.v[i] = make_uint4(0u, 0u, 0u, 0u);
-    }
+    const uint32_t o = (4 * i + grp < nv) ? base + (uint32_t)(4 * i) * tok_bytes : kOutOfRange;
+    T.k[i] = buffer_load16_stream(rk, o);
+    T.v[i] = buffer_load16_stream(rv, o);
   }
-  return page_ok;
 }
 
 __device__ __forceinline__ uint32_t u4get(const uint4& v, int c) {
   return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
 }
 
-// Online-softmax update of one 16-lane group with its 4 tokens of the tile.
-__device__ __forceinline__ void tile_update(const uint4 (&q)[kG], const KVTile& T, int t, int t1,
-                                            int grp, bool page_ok, float scale_log2,
-                                            float (&m)[kG], float (&l)[kG],
-                                            float (&acc)[kG][8]) {
+// Online-softmax update of one 16-lane group with its 4 tokens of tile j.
+__device__ __forceinline__ void tile_update(const DecodeArgs& a, const TileList& L, const uint4 (&q)[kG],
+                                            const KVTile& T, int j, int grp, float (&m)[kG],
+                                            float (&l)[kG], float (&acc)[kG][8]) {
+  const int page = readlane(L.page, j);
+  const int nv = readlane(L.nvalid, j);
+  const bool ok = (unsigned)page < (unsigned)a.num_pages;
   float sc[kG][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -102,19 +125,9 @@ __device__ __forceinline__ void tile_update(const uint4 (&q)[kG], const KVTile& 
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const bool valid = page_ok && (t + 4 * i + grp < t1);
+    const bool valid = ok && (4 * i + grp < nv);
 #pragma unroll
-    for (int h = 0; h < kG; ++h) sc[h][i] = valid ? sc[h][i] * scale_log2 : -INFINITY;
-  }
-  float vf[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t w = u4get(T.v[i], c);
-      vf[i][2 * c] = bf16_lo(w);
-      vf[i][2 * c + 1] = bf16_hi(w);
-    }
+    for (int h = 0; h < kG; ++h) sc[h][i] = valid ? sc[h][i] * a.scale_log2 : -INFINITY;
   }
 #pragma unroll
   for (int h = 0; h < kG; ++h) {
@@ -127,12 +140,28 @@ __device__ __forceinline__ void tile_update(const uint4 (&q)[kG], const KVTile& 
     l[h] = l[h] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     m[h] = mn;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      float x = acc[h][d] * alpha;
+    for (int cc = 0; cc < 4; ++cc) {
+      float x0 = acc[h][2 * cc] * alpha;
+      float x1 = acc[h][2 * cc + 1] * alpha;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x = fmaf(p[i], vf[i][d], x);
-      acc[h][d] = x;
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = u4get(T.v[i], cc);
+        x0 = fmaf(p[i], bf16_lo(w), x0);
+        x1 = fmaf(p[i], bf16_hi(w), x1);
+      }
+      acc[h][2 * cc] = x0;
+      acc[h][2 * cc + 1] = x1;
     }
+  }
+}
+
+__device__ __forceinline__ void reset_state(float (&m)[kG], float (&l)[kG], float (&acc)[kG][8]) {
+#pragma unroll
+  for (int h = 0; h < kG; ++h) {
+    m[h] = kMaxSeed;
+    l[h] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
   }
 }
 
@@ -165,64 +194,24 @@ __device__ __forceinline__ void store_row8(uint16_t* dst, const float (&x)[8], f
   *reinterpret_cast<uint4*>(dst) = v;
 }
 
-__global__ __launch_bounds__(1024) void paged_decode_split_kernel(const DecodeArgs a) {
-  const int b = blockIdx.x;
-  const int s = blockIdx.y;
-  const int g = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int grp = lane >> 4;
-  const int dl = (lane & 15) * 8;
-
-  const int ctx = row_ctx(a, b);
-  if (ctx == 0) {
-    if (s == 0 && grp == 0) {
-      const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int h = 0; h < kG; ++h) store_row8(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + dl, z, 0.f);
-    }
-    return;
-  }
-  const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
-  if (s >= ns) return;
-  const int t0 = s * a.split_tokens;
-  const int t1 = min(ctx, t0 + a.split_tokens);
-
-  uint4 q[kG];
+__device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int g, int dl, uint4 (&q)[kG]) {
 #pragma unroll
   for (int h = 0; h < kG; ++h)
     q[h] = *reinterpret_cast<const uint4*>(a.q + b * a.q_sb + (kG * g + h) * a.q_sh + dl);
+}
 
-  float m[kG], l[kG], acc[kG][8];
+// Lanes 0..15 hold the merged state: the normalised output row of both query heads.
+__device__ __forceinline__ void write_output(const DecodeArgs& a, int b, int g, int grp, int dl,
+                                             const float (&l)[kG], const float (&acc)[kG][8]) {
+  if (grp == 0) {
 #pragma unroll
-  for (int h = 0; h < kG; ++h) {
-    m[h] = kMaxSeed;
-    l[h] = 0.f;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
+    for (int h = 0; h < kG; ++h)
+      store_row8(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + dl, acc[h], l[h] > 0.f ? 1.f / l[h] : 0.f);
   }
+}
 
-  KVTile cur, nxt;
-  bool ok_cur = load_tile(a, b, g, grp, dl, t0, t1, cur);
-  for (int t = t0; t < t1; t += kTile) {
-    bool ok_nxt = false;
-    if (t + kTile < t1) ok_nxt = load_tile(a, b, g, grp, dl, t + kTile, t1, nxt);
-    tile_update(q, cur, t, t1, grp, ok_cur, a.scale_log2, m, l, acc);
-    cur = nxt;
-    ok_cur = ok_nxt;
-  }
-
-  merge_lanes(16, m, l, acc);
-  merge_lanes(32, m, l, acc);
-
-  if (ns == 1) {
-    if (grp == 0) {
-#pragma unroll
-      for (int h = 0; h < kG; ++h)
-        store_row8(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + dl, acc[h], l[h] > 0.f ? 1.f / l[h] : 0.f);
-    }
-    return;
-  }
-  float* P = a.ws + (((int64_t)b * a.max_splits + s) * a.hkv + g) * kPartFloats;
+__device__ __forceinline__ void write_partial(float* P, int lane, int grp, int dl, const float (&m)[kG],
+                                              const float (&l)[kG], const float (&acc)[kG][8]) {
   if (grp == 0) {
 #pragma unroll
     for (int h = 0; h < kG; ++h) {
@@ -240,80 +229,347 @@ __global__ __launch_bounds__(1024) void paged_decode_split_kernel(const DecodeAr
   }
 }
 
-// Merges the split partials of rows that have more than one split.  One workgroup per row, one
-// wave per KV head; lane l owns query head 2g + l/32 and dims 4*(l%32)..+4.
-__global__ __launch_bounds__(1024) void paged_decode_combine_kernel(const DecodeArgs a) {
-  const int b = blockIdx.x;
-  const int g = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int ctx = row_ctx(a, b);
-  if (ctx == 0) return;
-  const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
-  if (ns <= 1) return;
-  const float* base = a.ws + ((int64_t)b * a.max_splits * a.hkv + g) * kPartFloats;
-  const int64_t sstride = (int64_t)a.hkv * kPartFloats;
-
-  // Pass 1: lane j < ns reads split j's (m, l) for both heads; wave max and weighted sum.
-  float mj[kG], lj[kG];
+// Merges `count` partial records (rec(i) -> record i) of one (row, KV head) into the output row.
+// The whole wave participates; lane l owns query head l/32 and dims 4*(l%32)..+4.
+template <typename RecFn>
+__device__ __forceinline__ void merge_records(const DecodeArgs& a, int b, int g, int lane, int count,
+                                              RecFn rec) {
+  // Pass 1: global max and weighted sum of l over all records, 64 records per step.
+  float M[kG], L[kG];
 #pragma unroll
   for (int h = 0; h < kG; ++h) {
-    mj[h] = kMaxSeed;
-    lj[h] = 0.f;
+    M[h] = kMaxSeed;
+    L[h] = 0.f;
   }
-  if (lane < ns) {
-    const float* P = base + lane * sstride;
+  for (int c0 = 0; c0 < count; c0 += 64) {
+    float mj[kG], lj[kG];
 #pragma unroll
     for (int h = 0; h < kG; ++h) {
-      mj[h] = P[kG * kD + h];
-      lj[h] = P[kG * kD + kG + h];
+      mj[h] = kMaxSeed;
+      lj[h] = 0.f;
+    }
+    if (c0 + lane < count) {
+      const float* P = rec(c0 + lane);
+#pragma unroll
+      for (int h = 0; h < kG; ++h) {
+        mj[h] = P[kG * kD + h];
+        lj[h] = P[kG * kD + kG + h];
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+      float x = mj[h];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+      const float mn = fmaxf(M[h], x);
+      float y = lj[h] * fast_exp2(mj[h] - mn);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) y += __shfl_xor(y, o);
+      L[h] = L[h] * fast_exp2(M[h] - mn) + y;
+      M[h] = mn;
     }
   }
-  float M[kG], wj[kG], L[kG];
-#pragma unroll
-  for (int h = 0; h < kG; ++h) {
-    float x = mj[h];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-    M[h] = x;
-    wj[h] = lane < ns ? fast_exp2(mj[h] - x) : 0.f;
-    float y = lj[h] * wj[h];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) y += __shfl_xor(y, off);
-    L[h] = y;
-  }
-
-  // Pass 2: weighted sum of the unnormalised partial outputs.
+  // Pass 2: weighted sum of the unnormalised partial outputs, 8 independent loads in flight.
   const int h = lane >> 5;
   const int d0 = (lane & 31) * 4;
-  const float lsel = h == 0 ? L[0] : L[1];
-  const float wsel_inv = lsel > 0.f ? 1.f / lsel : 0.f;
+  const float Mh = h == 0 ? M[0] : M[1];
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-  for (int s = 0; s < ns; ++s) {
-    const float w0 = __shfl(wj[0], s);
-    const float w1 = __shfl(wj[1], s);
-    const float w = h == 0 ? w0 : w1;
-    const float4 v = *reinterpret_cast<const float4*>(base + s * sstride + h * kD + d0);
-    A.x = fmaf(v.x, w, A.x);
-    A.y = fmaf(v.y, w, A.y);
-    A.z = fmaf(v.z, w, A.z);
-    A.w = fmaf(v.w, w, A.w);
+  for (int s0 = 0; s0 < count; s0 += 8) {
+    float4 v[8];
+    float w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s0 + u < count) {
+        const float* P = rec(s0 + u);
+        v[u] = *reinterpret_cast<const float4*>(P + h * kD + d0);
+        w[u] = fast_exp2(P[kG * kD + h] - Mh);
+      } else {
+        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        w[u] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      A.x = fmaf(v[u].x, w[u], A.x);
+      A.y = fmaf(v[u].y, w[u], A.y);
+      A.z = fmaf(v[u].z, w[u], A.z);
+      A.w = fmaf(v[u].w, w[u], A.w);
+    }
   }
+  const float lsel = h == 0 ? L[0] : L[1];
+  const float inv = lsel > 0.f ? 1.f / lsel : 0.f;
   uint2 o;
-  o.x = pack_bf16x2(A.x * wsel_inv, A.y * wsel_inv);
-  o.y = pack_bf16x2(A.z * wsel_inv, A.w * wsel_inv);
+  o.x = pack_bf16x2(A.x * inv, A.y * inv);
+  o.y = pack_bf16x2(A.z * inv, A.w * inv);
   *reinterpret_cast<uint2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0) = o;
 }
 
+__device__ __forceinline__ void write_zero_row(const DecodeArgs& a, int b, int g, int lane) {
+  const int h = lane >> 5;
+  const int d0 = (lane & 31) * 4;
+  *reinterpret_cast<uint2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0) = make_uint2(0u, 0u);
+}
+
+// ------------------------------------------------------------------------------ stream-K path
+__device__ __forceinline__ int64_t sk_lo(int64_t k, int64_t nt, int64_t grid) { return k * nt / grid; }
+
+constexpr int kFirst = 1;     // tile opens a segment (first tile of the row or of the range)
+constexpr int kLast = 2;      // tile closes a segment
+constexpr int kRowStart = 4;  // tile is tile 0 of its row
+constexpr int kRowEnd = 8;    // tile is the last tile of its row
+
+__global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs a) {
+  __shared__ int s_ctx[kSkMaxRows];
+  __shared__ int s_prefix[kSkMaxRows + 1];
+  __shared__ int s_wsum[16];
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  const int g = tid >> 6;
+  const int lane = tid & 63;
+  const int grp = lane >> 4;
+  const int dl = (lane & 15) * 8;
+  const int B = a.batch;
+
+  // Prologue: tiles per row and their exclusive prefix sum (block-wide scan).
+  const int per = (B + nthr - 1) / nthr;
+  const int r0 = min(B, tid * per), r1 = min(B, r0 + per);
+  int sum = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int c = clamp_ctx(a, a.seqlens[r]);
+    s_ctx[r] = c;
+    sum += (c + kTile - 1) / kTile;
+  }
+  int x = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_wsum[g] = x;
+  __syncthreads();
+  int wbase = 0;
+  for (int w = 0; w < g; ++w) wbase += s_wsum[w];
+  int run = wbase + x - sum;
+  for (int r = r0; r < r1; ++r) {
+    s_prefix[r] = run;
+    run += (s_ctx[r] + kTile - 1) / kTile;
+  }
+  if (tid == nthr - 1) s_prefix[B] = wbase + x;
+  __syncthreads();
+  const int NT = s_prefix[B];
+  if (blockIdx.x == 0) {
+    for (int r = tid; r <= B; r += nthr) a.prefix[r] = s_prefix[r];
+  }
+  // Effective grid min(grid, NT): every participating workgroup then owns at least one tile, so the
+  // workgroups covering a row are exactly a contiguous index range (the combine relies on it).
+  const int ge = min(a.grid, NT);
+  if ((int)blockIdx.x >= ge) return;
+  const int lo = (int)sk_lo(blockIdx.x, NT, ge);
+  const int hi = (int)sk_lo(blockIdx.x + 1, NT, ge);
+
+  const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
+  float* part = a.ws + (int64_t)blockIdx.x * kSkSlots * a.hkv * kPartFloats;
+
+  uint4 q[kG];
+  float m[kG], l[kG], acc[kG][8];
+  reset_state(m, l, acc);
+  int seg_row = 0, seg_flags = 0, seg_slot = 0;
+  q[0] = q[1] = make_uint4(0u, 0u, 0u, 0u);
+
+  for (int cb = lo; cb < hi; cb += 64) {
+    TileList L;
+    L.n = min(64, hi - cb);
+    L.page = -1;
+    L.off = 0;
+    L.nvalid = 0;
+    int vrow = 0, vflags = 0;
+    if (lane < L.n) {
+      const int t = cb + lane;
+      int lo_r = 0, hi_r = B;  // largest row with prefix[row] <= t
+      while (hi_r - lo_r > 1) {
+        const int mid = (lo_r + hi_r) >> 1;
+        if (s_prefix[mid] <= t) lo_r = mid; else hi_r = mid;
+      }
+      const int row = lo_r;
+      const int mt = t - s_prefix[row];
+      const int ntr = s_prefix[row + 1] - s_prefix[row];
+      const int tok = mt * kTile;
+      const int pidx = tok / a.page_size;
+      L.page = a.bt[(int64_t)row * a.bt_sb + pidx];
+      L.off = tok - pidx * a.page_size;
+      L.nvalid = min(kTile, s_ctx[row] - tok);
+      vrow = row;
+      vflags = ((mt == 0 || t == lo) ? kFirst : 0) | ((mt == ntr - 1 || t == hi - 1) ? kLast : 0) |
+               (mt == 0 ? kRowStart : 0) | (mt == ntr - 1 ? kRowEnd : 0);
+    }
+
+    auto process = [&](const KVTile& T, int j) {
+      const int fl = readlane(vflags, j);
+      if (fl & kFirst) {
+        seg_row = readlane(vrow, j);
+        seg_flags = fl;
+        seg_slot = (cb + j == lo) ? 0 : 1;
+        reset_state(m, l, acc);
+        load_q(a, seg_row, g, dl, q);
+      }
+      tile_update(a, L, q, T, j, grp, m, l, acc);
+      if (fl & kLast) {
+        merge_lanes(16, m, l, acc);
+        merge_lanes(32, m, l, acc);
+        if ((seg_flags & kRowStart) && (fl & kRowEnd)) {
+          write_output(a, seg_row, g, grp, dl, l, acc);
+        } else {
+          write_partial(part + (seg_slot * a.hkv + g) * kPartFloats, lane, grp, dl, m, l, acc);
+        }
+      }
+    };
+
+    KVTile A, Bt;
+    issue_tile(a, L, lane_off, grp, 0, A);
+    for (int j = 0; j < L.n; j += 2) {
+      issue_tile(a, L, lane_off, grp, j + 1, Bt);
+      process(A, j);
+      issue_tile(a, L, lane_off, grp, j + 2, A);
+      if (j + 1 < L.n) process(Bt, j + 1);
+    }
+  }
+}
+
+// One workgroup per row: merges the partial records of rows that straddle workgroup ranges, and
+// writes zeros for rows with no context.
+__global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int g = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int p0 = a.prefix[b];
+  const int p1 = a.prefix[b + 1];
+  const int NT = a.prefix[a.batch];
+  if (p1 == p0) {
+    write_zero_row(a, b, g, lane);
+    return;
+  }
+  const int64_t G = min(a.grid, NT);
+  const int kf = (int)(((int64_t)(p0 + 1) * G - 1) / NT);
+  const int kl = (int)(((int64_t)p1 * G - 1) / NT);
+  if (kf == kl) return;
+  const int first_slot = sk_lo(kf, NT, G) < p0 ? 1 : 0;
+  merge_records(a, b, g, lane, kl - kf + 1, [&](int i) -> const float* {
+    const int k = kf + i;
+    const int slot = i == 0 ? first_slot : 0;
+    return a.ws + (((int64_t)k * kSkSlots + slot) * a.hkv + g) * kPartFloats;
+  });
+}
+
+// ------------------------------------------------------------------------------ fixed-split path
+__global__ __launch_bounds__(1024) void paged_decode_split_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int s = blockIdx.y;
+  const int g = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int grp = lane >> 4;
+  const int dl = (lane & 15) * 8;
+
+  const int ctx = clamp_ctx(a, a.seqlens[b]);
+  if (ctx == 0) {
+    if (s == 0) write_zero_row(a, b, g, lane);
+    return;
+  }
+  const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
+  if (s >= ns) return;
+  const int t0 = s * a.split_tokens;
+  const int t1 = min(ctx, t0 + a.split_tokens);
+
+  TileList L;
+  L.n = (t1 - t0 + kTile - 1) / kTile;
+  L.page = -1;
+  L.off = 0;
+  L.nvalid = 0;
+  if (lane < L.n) {
+    const int t = t0 + kTile * lane;
+    const int pidx = t / a.page_size;
+    L.page = a.bt[(int64_t)b * a.bt_sb + pidx];
+    L.off = t - pidx * a.page_size;
+    L.nvalid = min(kTile, t1 - t);
+  }
+  const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
+
+  uint4 q[kG];
+  load_q(a, b, g, dl, q);
+  float m[kG], l[kG], acc[kG][8];
+  reset_state(m, l, acc);
+
+  KVTile A, Bt;
+  issue_tile(a, L, lane_off, grp, 0, A);
+  for (int j = 0; j < L.n; j += 2) {
+    issue_tile(a, L, lane_off, grp, j + 1, Bt);
+    tile_update(a, L, q, A, j, grp, m, l, acc);
+    issue_tile(a, L, lane_off, grp, j + 2, A);
+    if (j + 1 < L.n) tile_update(a, L, q, Bt, j + 1, grp, m, l, acc);
+  }
+
+  merge_lanes(16, m, l, acc);
+  merge_lanes(32, m, l, acc);
+  if (ns == 1) {
+    write_output(a, b, g, grp, dl, l, acc);
+  } else {
+    write_partial(a.ws + (((int64_t)b * a.max_splits + s) * a.hkv + g) * kPartFloats, lane, grp, dl, m, l, acc);
+  }
+}
+
+__global__ __launch_bounds__(1024) void paged_decode_split_combine_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int g = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int ctx = clamp_ctx(a, a.seqlens[b]);
+  if (ctx == 0) return;
+  const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
+  if (ns <= 1) return;
+  merge_records(a, b, g, lane, ns, [&](int s) -> const float* {
+    return a.ws + (((int64_t)b * a.max_splits + s) * a.hkv + g) * kPartFloats;
+  });
+}
+
+// ------------------------------------------------------------------------------ host side
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int default_split(int batch, int hkv, int max_pages, int page_size) {
   const int64_t max_ctx = (int64_t)max_pages * page_size;
   int split = 64;
   (void)hkv;
   while (split > kTile && (int64_t)batch * ceil_div(max_ctx, split) < 1024) split /= 2;
-  while (ceil_div(max_ctx, split) > kMaxSplits) split *= 2;
+  while (ceil_div(max_ctx, split) > kMaxSplits && split < kMaxSplitTokens) split *= 2;
   return split;
+}
+
+// Workgroups of the stream-K kernel the current device holds at once (cached per device).
+int sk_grid(int hkv) {
+  static int cache[64][17];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kSkMaxGrid;
+  int& c = cache[dev][hkv];
+  if (c > 0) return c;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return kSkMaxGrid;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel, 64 * hkv, 0) != hipSuccess)
+    return kSkMaxGrid;
+  int g = cus * (per_cu > 0 ? per_cu : 1);
+  g = g < 1 ? 1 : (g > kSkMaxGrid ? kSkMaxGrid : g);
+  c = g;
+  return g;
+}
+
+bool use_sk(int batch, int split_tokens) { return split_tokens == 0 && batch <= kSkMaxRows; }
+
+size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int split_tokens) {
+  if (use_sk(batch, split_tokens)) {
+    return align256((size_t)(batch + 1) * sizeof(int)) +
+           (size_t)sk_grid(hkv) * kSkSlots * hkv * kPartFloats * sizeof(float);
+  }
+  if (split_tokens <= 0) split_tokens = default_split(batch, hkv, max_pages, page_size);
+  const int max_splits = ceil_div((int64_t)max_pages * page_size, split_tokens);
+  if (max_splits <= 1) return 0;
+  return (size_t)batch * max_splits * hkv * kPartFloats * sizeof(float);
 }
 
 }  // namespace
@@ -332,11 +588,9 @@ extern "C" size_t q3a_paged_decode_workspace_bytes(int batch, int num_q_heads, i
                                                    int page_size, int split_tokens) {
   (void)num_q_heads;
   (void)head_dim;
-  if (batch <= 0 || num_kv_heads <= 0 || max_pages_per_seq <= 0 || page_size <= 0) return 0;
-  if (split_tokens <= 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
-  const int max_splits = ceil_div((int64_t)max_pages_per_seq * page_size, split_tokens);
-  if (max_splits <= 1) return 0;
-  return (size_t)batch * max_splits * num_kv_heads * kPartFloats * sizeof(float);
+  if (batch <= 0 || num_kv_heads <= 0 || num_kv_heads > 16 || max_pages_per_seq <= 0 || page_size <= 0)
+    return 0;
+  return workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, split_tokens);
 }
 
 extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -345,7 +599,7 @@ extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
                                 int page_size, const int32_t* cache_seqlens,
                                 const int32_t* block_table, int64_t bt_stride_b,
                                 int max_pages_per_seq, void* out, int64_t o_stride_b,
-                                int64_t o_stride_h, void* workspace, size_t workspace_bytes,
+                                int64_t o_stride_h, void* workspace, size_t workspace_bytes_,
                                 int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                 float softmax_scale, int split_tokens, void* stream) {
   if (batch < 0) return fail(Q3A_EINVAL, "paged_decode: batch %d < 0", batch);
@@ -365,18 +619,25 @@ extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   if (align % 16 != 0) return fail(Q3A_EINVAL, "paged_decode: q/k_cache/v_cache/out must be 16-byte aligned");
   if ((q_stride_b | q_stride_h | kv_stride_page | kv_stride_tok | kv_stride_head | o_stride_b | o_stride_h) % 8 != 0)
     return fail(Q3A_EINVAL, "paged_decode: strides must be multiples of 8 elements (16 bytes)");
-  if (split_tokens == 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
-  if (split_tokens < kTile || split_tokens % kTile != 0)
-    return fail(Q3A_EINVAL, "paged_decode: split_tokens %d is not a positive multiple of %d", split_tokens, kTile);
+  if (split_tokens < 0 || split_tokens % kTile != 0)
+    return fail(Q3A_EINVAL, "paged_decode: split_tokens %d is not 0 or a positive multiple of %d", split_tokens, kTile);
+  if (split_tokens > kMaxSplitTokens)
+    return fail(Q3A_EINVAL, "paged_decode: split_tokens %d exceeds %d", split_tokens, kMaxSplitTokens);
+  const int64_t page_extent =
+      ((int64_t)(page_size - 1) * kv_stride_tok + (int64_t)(num_kv_heads - 1) * kv_stride_head + head_dim) * 2;
+  if (kv_stride_tok <= 0 || kv_stride_head <= 0 || page_extent >= ((int64_t)1 << 31))
+    return fail(Q3A_EINVAL, "paged_decode: page extent %lld bytes unsupported (need positive strides, < 2 GiB)",
+                (long long)page_extent);
   const int64_t max_ctx = (int64_t)max_pages_per_seq * page_size;
   if (max_ctx > (int64_t)1 << 30) return fail(Q3A_EINVAL, "paged_decode: context capacity too large");
-  const int max_splits = ceil_div(max_ctx, split_tokens);
-  if (max_splits > kMaxSplits)
+  const bool sk = use_sk(batch, split_tokens);
+  if (!sk && split_tokens == 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
+  const int max_splits = sk ? 0 : ceil_div(max_ctx, split_tokens);
+  if (!sk && max_splits > kMaxSplits)
     return fail(Q3A_EINVAL, "paged_decode: %d splits exceed %d (raise split_tokens)", max_splits, kMaxSplits);
-  const size_t need = q3a_paged_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim,
-                                                       max_pages_per_seq, page_size, split_tokens);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-    return fail(Q3A_ESPACE, "paged_decode: workspace %zu bytes < %zu needed", workspace_bytes, need);
+  const size_t need = workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, sk ? 0 : split_tokens);
+  if (need > 0 && (workspace == nullptr || workspace_bytes_ < need))
+    return fail(Q3A_ESPACE, "paged_decode: workspace %zu bytes < %zu needed", workspace_bytes_, need);
   if (need > 0 && (uintptr_t)workspace % 16 != 0)
     return fail(Q3A_EINVAL, "paged_decode: workspace must be 16-byte aligned");
 
@@ -391,6 +652,7 @@ extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   a.kv_sh = kv_stride_head;
   a.num_pages = num_pages;
   a.page_size = page_size;
+  a.page_bytes = (uint32_t)page_extent;
   a.seqlens = cache_seqlens;
   a.bt = block_table;
   a.bt_sb = bt_stride_b;
@@ -398,7 +660,7 @@ extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   a.out = static_cast<uint16_t*>(out);
   a.o_sb = o_stride_b;
   a.o_sh = o_stride_h;
-  a.ws = static_cast<float*>(workspace);
+  a.batch = batch;
   a.hkv = num_kv_heads;
   a.split_tokens = split_tokens;
   a.max_splits = max_splits;
@@ -406,11 +668,27 @@ extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 block(64 * num_kv_heads);
+  hipError_t e;
+  if (sk) {
+    a.grid = sk_grid(num_kv_heads);
+    a.prefix = static_cast<int*>(workspace);
+    a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256((size_t)(batch + 1) * sizeof(int)));
+    hipLaunchKernelGGL(paged_decode_sk_kernel, dim3(a.grid), block, 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: stream-K launch failed: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(paged_decode_sk_combine_kernel, dim3(batch), block, 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: combine launch failed: %s", hipGetErrorString(e));
+    return Q3A_OK;
+  }
+  a.grid = 0;
+  a.prefix = nullptr;
+  a.ws = static_cast<float*>(workspace);
   hipLaunchKernelGGL(paged_decode_split_kernel, dim3(batch, max_splits), block, 0, st, a);
-  hipError_t e = hipGetLastError();
+  e = hipGetLastError();
   if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: split launch failed: %s", hipGetErrorString(e));
   if (max_splits > 1) {
-    hipLaunchKernelGGL(paged_decode_combine_kernel, dim3(batch), block, 0, st, a);
+    hipLaunchKernelGGL(paged_decode_split_combine_kernel, dim3(batch), block, 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: combine launch failed: %s", hipGetErrorString(e));
   }

@@ -68,7 +68,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     if B == 0:
         return out
     L = lib()
-    split = int(split_tokens) or L.q3a_paged_decode_default_split(B, Hkv, max_pages, page)
+    split = int(split_tokens)            # 0: the library's default decomposition (stream-K)
     ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
     rc = L.q3a_paged_decode(

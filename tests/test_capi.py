@@ -53,6 +53,8 @@ def _decode(**kw):
     (dict(st=1020), "strides"),
     (dict(split=40), "split_tokens"),
     (dict(max_pages=4096, split=16), "splits exceed"),
+    (dict(split=2048), "exceeds 1024"),
+    (dict(sh=-128), "page extent"),
     (dict(ws_bytes=10), "workspace"),
     (dict(B=-1), "batch"),
 ])

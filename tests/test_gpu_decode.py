@@ -44,7 +44,7 @@ def test_c1_single_row(cuda_device):
     assert_parity(out, decode_oracle(wl), "c1")
 
 
-@pytest.mark.parametrize("split", [0, 32, 64, 128, 2048])
+@pytest.mark.parametrize("split", [0, 32, 64, 128, 1024])
 def test_ragged_contexts_all_splits(cuda_device, split):
     wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=5)
     out = run(wl, split=split)
@@ -53,10 +53,12 @@ def test_ragged_contexts_all_splits(cuda_device, split):
     assert not out[0].float().abs().sum().item(), "ctx == 0 row must be zeros"
 
 
-def test_short_contexts_split16(cuda_device):
+@pytest.mark.parametrize("split", [16, 1024])
+def test_short_contexts(cuda_device, split):
+    """split 16: many splits per row; split 1024: every row in one split (no partials)."""
     ctx = np.array([c for c in RAGGED if c <= 1000])
     wl = W.make_decode("short", cuda_device, ctx=ctx, num_pages=2048, max_ctx=1000, seed=4)
-    assert_parity(run(wl, split=16), decode_oracle(wl), "short split=16")
+    assert_parity(run(wl, split=split), decode_oracle(wl), f"short split={split}")
 
 
 def test_ctx1_is_exact_v_row(cuda_device):
@@ -154,3 +156,38 @@ def test_c5_full_size(cuda_device):
         assert ok, (split, st)
     del wl
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("ctx", [[1], [0, 17, 0], [0, 0], [5, 1800], [2000 // 16 * 16]])
+def test_stream_k_tiny_workloads(cuda_device, ctx):
+    """Fewer tiles than stream-K workgroups: most workgroups own nothing and rows span several
+    one-tile workgroups."""
+    ctx = np.array(ctx)
+    wl = W.make_decode("tiny", cuda_device, ctx=ctx, num_pages=512, max_ctx=2000, seed=int(ctx.sum()) % 97)
+    out = run(wl)
+    assert_parity(out, decode_oracle(wl), f"tiny {ctx.tolist()}")
+
+
+def test_stream_k_many_short_rows(cuda_device):
+    """Thousands of short rows: many segments per workgroup, rows split at every range boundary."""
+    rng = np.random.default_rng(17)
+    ctx = rng.integers(0, 41, size=4000)
+    wl = W.make_decode("short_rows", cuda_device, ctx=ctx, num_pages=16384, max_ctx=48, seed=17)
+    out = run(wl)
+    assert_parity(out, decode_oracle(wl), "4000 short rows")
+    assert not out[ctx == 0].float().abs().sum().item()
+
+
+def test_batch_beyond_stream_k_limit_uses_fixed_splits(cuda_device):
+    rng = np.random.default_rng(19)
+    ctx = rng.integers(0, 33, size=4100)
+    wl = W.make_decode("big_batch", cuda_device, ctx=ctx, num_pages=12800, max_ctx=48, seed=19)
+    assert_parity(run(wl), decode_oracle(wl), "4100 rows")
+
+
+def test_stream_k_matches_fixed_split(cuda_device):
+    wl = W.make_decode("c3", cuda_device)
+    a = run(wl)
+    b = run(wl, split=128)
+    ok, st = ora.compare(to_np(a), to_np(b), max_abs=8e-3, mean_abs=2e-4)
+    assert ok, st
