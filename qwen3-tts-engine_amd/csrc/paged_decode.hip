@@ -105,6 +105,11 @@ __device__ __forceinline__ uint32_t u4get(const uint4& v, int c) {
 }
 
 // Online-softmax update of one 16-lane group with its 4 tokens of tile j.
+//
+// q.k: 4 bf16 dot2 per (token, head) then a 16-lane DPP sum.  p.v: the probabilities are packed to
+// bf16 pairs (tokens 0,1 and 2,3) and each output dim takes two dot2 against the matching V pairs
+// built with v_perm_b32, the rounding point flash-attention also uses for P.  The running max
+// rarely grows after the first tiles, so the rescale of (l, acc) runs only when a lane's max grew.
 __device__ __forceinline__ void tile_update(const DecodeArgs& a, const TileList& L, const uint4 (&q)[kG],
                                             const KVTile& T, int j, int grp, float (&m)[kG],
                                             float (&l)[kG], float (&acc)[kG][8]) {
@@ -129,28 +134,51 @@ __device__ __forceinline__ void tile_update(const DecodeArgs& a, const TileList&
 #pragma unroll
     for (int h = 0; h < kG; ++h) sc[h][i] = valid ? sc[h][i] * a.scale_log2 : -INFINITY;
   }
+  float mt[kG];
+  bool grow = false;
 #pragma unroll
   for (int h = 0; h < kG; ++h) {
-    const float mt = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
-    const float mn = fmaxf(m[h], mt);
-    const float alpha = fast_exp2(m[h] - mn);
+    mt[h] = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
+    grow |= mt[h] > m[h];
+  }
+  if (__any(grow)) {
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+      const float mn = fmaxf(m[h], mt[h]);
+      const float alpha = fast_exp2(m[h] - mn);
+      m[h] = mn;
+      l[h] *= alpha;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[h][d] *= alpha;
+    }
+  }
+  // V pairs: vp[pair][c][0] = (v[2*pair][dim 2c], v[2*pair+1][dim 2c]), [1] for dim 2c+1.
+  uint32_t vp[2][4][2];
+#pragma unroll
+  for (int pr = 0; pr < 2; ++pr) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t v0 = u4get(T.v[2 * pr], c);
+      const uint32_t v1 = u4get(T.v[2 * pr + 1], c);
+      vp[pr][c][0] = perm_b32(v1, v0, kPermLoLo);
+      vp[pr][c][1] = perm_b32(v1, v0, kPermHiHi);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < kG; ++h) {
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sc[h][i] - mn);
-    l[h] = l[h] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m[h] = mn;
+    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sc[h][i] - m[h]);
+    l[h] += (p[0] + p[1]) + (p[2] + p[3]);
+    const uint32_t p01 = pack_bf16x2(p[0], p[1]);
+    const uint32_t p23 = pack_bf16x2(p[2], p[3]);
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      float x0 = acc[h][2 * cc] * alpha;
-      float x1 = acc[h][2 * cc + 1] * alpha;
+    for (int c = 0; c < 4; ++c) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t w = u4get(T.v[i], cc);
-        x0 = fmaf(p[i], bf16_lo(w), x0);
-        x1 = fmaf(p[i], bf16_hi(w), x1);
+      for (int e = 0; e < 2; ++e) {
+        float x = dot2_bf16(p01, vp[0][c][e], acc[h][2 * c + e]);
+        acc[h][2 * c + e] = dot2_bf16(p23, vp[1][c][e], x);
       }
-      acc[h][2 * cc] = x0;
-      acc[h][2 * cc + 1] = x1;
     }
   }
 }

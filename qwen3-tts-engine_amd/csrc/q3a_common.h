@@ -28,6 +28,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Byte permute (v_perm_b32): bytes 0-3 of `lo` and 4-7 of `hi`, selected by `sel`.
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// (lo half of a, lo half of b) and (hi half of a, hi half of b) as bf16 pairs.
+constexpr uint32_t kPermLoLo = 0x05040100u;
+constexpr uint32_t kPermHiHi = 0x07060302u;
+
 // Round a float to the nearest bf16 value, returned as float.
 __device__ __forceinline__ float round_bf16(float x) {
   return __uint_as_float(pack_bf16x2(x, 0.f) << 16);
