@@ -88,6 +88,19 @@ def cpu_baseline(wl, reps_min: int = 3, budget_s: float = 12.0):
     }
 
 
+def measured_traffic():
+    """HBM bytes per decode-kernel launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE scaled by a plain-copy calibration), or None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "paged_decode_c5.md")
+    try:
+        for ln in open(path):
+            if ln.startswith("traffic_bytes_per_launch"):
+                return int(ln.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,7 +241,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "paged decode call (stream-K decode kernel + combine kernel), per call inside the graph",
             "bytes_per_call": nbytes,
         },
