@@ -50,8 +50,10 @@ const char* q3a_last_error(void);
  * Query head h reads KV head h / (Hq/Hkv).  softmax is float32.  Rows with ctx <= 0 produce zeros;
  * ctx is clamped to max_pages_per_seq*page_size; a page index outside [0, num_pages) contributes
  * no tokens.  Requirements: D == 128, Hq == 2*Hkv, 1 <= Hkv <= 16, page_size % 16 == 0,
- * 16-byte aligned rows.  split_tokens (a multiple of 16) is the number of context tokens one
- * workgroup streams; 0 selects q3a_paged_decode_default_split().
+ * 16-byte aligned rows.  split_tokens == 0 selects the stream-K decomposition (a persistent grid
+ * sized to the device, balanced over all rows' 16-token tiles; batch <= 4096, larger batches fall
+ * back to q3a_paged_decode_default_split()); split_tokens > 0 (a multiple of 16, <= 1024) selects
+ * one workgroup per (row, split of that many tokens).
  */
 int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      const void* k_cache, const void* v_cache, int64_t kv_stride_page,
@@ -66,7 +68,7 @@ int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 size_t q3a_paged_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                         int max_pages_per_seq, int page_size, int split_tokens);
 
-/* The split size q3a_paged_decode uses when split_tokens == 0. */
+/* The fixed split size used for batches beyond the stream-K limit. */
 int q3a_paged_decode_default_split(int batch, int num_kv_heads, int max_pages_per_seq,
                                    int page_size);
 
@@ -86,6 +88,32 @@ int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
                 int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,
                 int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                 int n_live, float softmax_scale, void* stream);
+
+/*
+ * Talker prefill attention (packed variable-length, MFMA).
+ *
+ * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, ..., causal=True) at
+ * engine/talker.py:169 (fp32 form engine/talker.py:163-167) and the prefix + new flash_attn_func(q, K, V,
+ * causal=True) of engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131).
+ *
+ *   q       [T, Hq, D] bf16, token stride q_stride_t, head stride q_stride_h; sequence s owns tokens
+ *           cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1
+ *   k, v    block_table == NULL: packed [Tk, Hkv, D] (token stride kv_stride_tok, head stride kv_stride_head),
+ *           sequence s owns rows cu_seqlens_k[s] .. cu_seqlens_k[s+1]-1;
+ *           block_table != NULL: the paged pool [num_pages, page_size, Hkv, D] (kv_stride_page/tok/head), key j
+ *           of sequence s at page block_table[s][j / page_size], offset j % page_size, with
+ *           Lk = cu_seqlens_k[s+1] - cu_seqlens_k[s] keys
+ *   out     [T, Hq, D] bf16 (token stride o_stride_t, head stride o_stride_h)
+ * With causal != 0, query i of a sequence sees keys j <= Lk - Lq + i (bottom-right aligned; for Lq == Lk the
+ * standard causal mask).  Query rows that see no key are zeros.  Requirements: D == 128, Hq == 2*Hkv,
+ * 16-byte aligned rows; max_seqlen_q >= every Lq.
+ */
+int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
+                const void* k, const void* v, int64_t kv_stride_page, int64_t kv_stride_tok,
+                int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                int64_t bt_stride_b, int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out,
+                int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads,
+                int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,314 @@
+// Talker prefill attention for gfx950, on MFMA.
+//
+// Semantics: packed variable-length causal attention.  Sequence s owns query tokens
+// [cu_q[s], cu_q[s+1]) of q [T, Hq, D] and keys 0..Lk-1 with Lk = cu_k[s+1] - cu_k[s], read either
+// from a packed [Tk, Hkv, D] tensor (token j at row cu_k[s] + j) or from the paged KV pool
+// (token j at page block_table[s][j / page_size], offset j % page_size).  With `causal`, query i
+// sees keys j <= Lk - Lq + i (bottom-right alignment).  This covers flash_attn_varlen_func at
+// engine/talker.py:169 (cu_q == cu_k, fp32 form engine/talker.py:163-167), the prefix + new form
+// of flash_attn_func at engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131), and both
+// read from the pool after the K/V append (engine/talker.py:161-162, engine/arrivals.py:144-145).
+//
+// Work: one workgroup (4 waves) per (sequence, 32-query tile, KV head); wave w takes query head
+// 2g + (w & 1) and tokens 16*(w >> 1)..+16 of the tile, so the workgroup's 64 MFMA rows are the two
+// query heads of the GQA pair over 32 tokens and every K/V tile staged in LDS serves both heads.
+// Key tiles of 64 are staged in LDS (K row-major, V transposed); the next tile is prefetched into
+// registers while the current one is consumed.  v_mfma_f32_16x16x32_bf16 layouts: A lane l = row
+// l%16, k 8*(l/16)..+8; B lane l = column l%16, same k; C lane l = column l%16, rows 4*(l/16)..+4.
+//   S^T = K Q^T  : A = K (rows = keys), B = Q^T (columns = this lane's query token)
+//   O^T = V^T P^T: A = V^T from LDS, B = P^T taken straight from S^T's C registers
+// so the softmax statistics, P and the O accumulators of a query token all live on the lanes with
+// that token in column l%16; a row's max over a tile needs only two cross-lane steps.
+#include "q3a_common.h"
+#include "../../include/q3attn.h"
+
+namespace q3a {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kG = 2;
+constexpr int kQT = 32;        // query tokens per workgroup
+constexpr int kKT = 64;        // keys per LDS tile
+constexpr int kKs = kD + 8;    // K tile row stride in LDS (bf16 elements, padded)
+constexpr int kVs = kKT + 8;   // V^T tile row stride in LDS (bf16 elements, padded)
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t q_st, q_sh;
+  const int32_t* cu_q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t kv_sp, kv_st, kv_sh;
+  int num_pages, page_size;
+  const int32_t* bt;  // nullptr: packed K/V
+  int64_t bt_sb;
+  int max_pages;
+  const int32_t* cu_k;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  int causal;
+  float scale_log2;
+};
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
+  __shared__ __align__(16) uint16_t Ks[kKT * kKs];
+  __shared__ __align__(16) uint16_t Vt[kD * kVs];
+
+  const int s = blockIdx.x;
+  const int qt = gridDim.y - 1 - blockIdx.y;  // longest query tiles dispatch first
+  const int g = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int col = lane & 15;
+  const int g4 = lane >> 4;
+
+  const int q0 = a.cu_q[s];
+  const int Lq = a.cu_q[s + 1] - q0;
+  if (qt * kQT >= Lq) return;
+  const int k0 = a.cu_k[s];
+  int Lk = a.cu_k[s + 1] - k0;
+  if (a.bt != nullptr) Lk = min(Lk, a.max_pages * a.page_size);
+  Lk = max(Lk, 0);
+
+  const int h = kG * g + (wave & 1);
+  const int tq = qt * kQT + (wave >> 1) * 16 + col;  // this lane's query token
+  const bool qvalid = tq < Lq;
+  const int qpos = Lk - Lq + tq;                       // last key this token may see when causal
+
+  // Q^T as the B operand of S^T = K Q^T: 4 chunks of 32 dims.
+  bf16x8_t qb[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if (qvalid) x = *reinterpret_cast<const uint4*>(a.q + (int64_t)(q0 + tq) * a.q_st + h * a.q_sh + 32 * kk + 8 * g4);
+    qb[kk] = as_bf16x8(x);
+  }
+
+  int kend = Lk;
+  if (a.causal) {
+    const int last = min(Lq - 1, qt * kQT + kQT - 1);
+    kend = min(Lk, Lk - Lq + last + 1);
+  }
+  const int ntiles = kend > 0 ? (kend + kKT - 1) / kKT : 0;
+
+  // Element offset of key j's row (head 0), or -1 when its page is not in the pool.
+  auto key_row = [&](int j) -> int64_t {
+    if (a.bt == nullptr) return (int64_t)(k0 + j) * a.kv_st;
+    const int pidx = j / a.page_size;
+    const int p = a.bt[(int64_t)s * a.bt_sb + pidx];
+    if ((unsigned)p >= (unsigned)a.num_pages) return -1;
+    return (int64_t)p * a.kv_sp + (int64_t)(j - pidx * a.page_size) * a.kv_st;
+  };
+
+  // Cooperative tile loads: K chunk (key (tid>>4) + 16r, dims 8*(tid&15)); V keys 4*(tid&15)+r,
+  // dims 8*(tid>>4).
+  uint4 kr[4], vr[4];
+  auto load_tile = [&](int t) {
+    const int kb = t * kKT;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = kb + (tid >> 4) + 16 * r;
+      kr[r] = make_uint4(0u, 0u, 0u, 0u);
+      if (j < Lk) {
+        const int64_t row = key_row(j);
+        if (row >= 0) kr[r] = *reinterpret_cast<const uint4*>(a.k + row + g * a.kv_sh + 8 * (tid & 15));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = kb + 4 * (tid & 15) + r;
+      vr[r] = make_uint4(0u, 0u, 0u, 0u);
+      if (j < Lk) {
+        const int64_t row = key_row(j);
+        if (row >= 0) vr[r] = *reinterpret_cast<const uint4*>(a.v + row + g * a.kv_sh + 8 * (tid >> 4));
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<uint4*>(&Ks[((tid >> 4) + 16 * r) * kKs + 8 * (tid & 15)]) = kr[r];
+    // V transposed: for each of this thread's 8 dims, its 4 keys as one 8-byte row segment.
+    const int kq = 4 * (tid & 15);
+    const int d0 = 8 * (tid >> 4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t w0 = c == 0 ? vr[0].x : c == 1 ? vr[0].y : c == 2 ? vr[0].z : vr[0].w;
+      const uint32_t w1 = c == 0 ? vr[1].x : c == 1 ? vr[1].y : c == 2 ? vr[1].z : vr[1].w;
+      const uint32_t w2 = c == 0 ? vr[2].x : c == 1 ? vr[2].y : c == 2 ? vr[2].z : vr[2].w;
+      const uint32_t w3 = c == 0 ? vr[3].x : c == 1 ? vr[3].y : c == 2 ? vr[3].z : vr[3].w;
+      uint2 lo, hi;
+      lo.x = perm_b32(w1, w0, kPermLoLo);
+      lo.y = perm_b32(w3, w2, kPermLoLo);
+      hi.x = perm_b32(w1, w0, kPermHiHi);
+      hi.y = perm_b32(w3, w2, kPermHiHi);
+      *reinterpret_cast<uint2*>(&Vt[(d0 + 2 * c) * kVs + kq]) = lo;
+      *reinterpret_cast<uint2*>(&Vt[(d0 + 2 * c + 1) * kVs + kq]) = hi;
+    }
+  };
+
+  f32x4_t acc[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m = kMaxSeed, l = 0.f;
+
+  if (ntiles > 0) load_tile(0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    store_tile();
+    __syncthreads();
+    if (t + 1 < ntiles) load_tile(t + 1);
+
+    // S^T for the tile's 4 blocks of 16 keys.
+    f32x4_t st[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      st[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint4 kv = *reinterpret_cast<const uint4*>(&Ks[(kb * 16 + col) * kKs + 32 * kk + 8 * g4]);
+        st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv), qb[kk], st[kb], 0, 0, 0);
+      }
+    }
+    // Scale, mask, per-token max over the tile (this lane's 16 keys, then the 4 lanes of the token).
+    float x[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = t * kKT + kb * 16 + 4 * g4 + i;
+        const bool ok = j < Lk && (!a.causal || j <= qpos);
+        x[kb][i] = ok ? st[kb][i] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, x[kb][i]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);
+    if (__any(mn > m)) {
+      const float alpha = fast_exp2(m - mn);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        acc[db][0] *= alpha;
+        acc[db][1] *= alpha;
+        acc[db][2] *= alpha;
+        acc[db][3] *= alpha;
+      }
+      m = mn;
+    }
+    // P^T as the B operand: k slot 8*g4 + i <- key 32*s2 + 4*g4 + i, slot 8*g4 + 4 + i <- key
+    // 32*s2 + 16 + 4*g4 + i (blocks 2*s2 and 2*s2+1 of this lane's C registers).
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = fast_exp2(x[2 * s2][i] - m);
+        p[4 + i] = fast_exp2(x[2 * s2 + 1][i] - m);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l += p[i];
+      uint4 w;
+      w.x = pack_bf16x2(p[0], p[1]);
+      w.y = pack_bf16x2(p[2], p[3]);
+      w.z = pack_bf16x2(p[4], p[5]);
+      w.w = pack_bf16x2(p[6], p[7]);
+      pb[s2] = as_bf16x8(w);
+    }
+    // O^T += V^T P^T; V^T rows are dims, the same key order as the B operand.
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const uint16_t* vrow = &Vt[(db * 16 + col) * kVs + 32 * s2 + 4 * g4];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
+        acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb[s2],
+                                                          acc[db], 0, 0, 0);
+      }
+    }
+  }
+
+  // The 4 lanes of a token hold partial sums over disjoint keys.
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (qvalid) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* o = a.out + (int64_t)(q0 + tq) * a.o_st + h * a.o_sh + 4 * g4;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      uint2 w;
+      w.x = pack_bf16x2(acc[db][0] * inv, acc[db][1] * inv);
+      w.y = pack_bf16x2(acc[db][2] * inv, acc[db][3] * inv);
+      *reinterpret_cast<uint2*>(o + db * 16) = w;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace q3a
+
+using namespace q3a;
+
+extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
+                           const void* k, const void* v, int64_t kv_stride_page, int64_t kv_stride_tok,
+                           int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                           int64_t bt_stride_b, int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out,
+                           int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int max_seqlen_q,
+                           int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal,
+                           void* stream) {
+  if (num_seqs < 0 || max_seqlen_q < 0) return fail(Q3A_EINVAL, "prefill: negative num_seqs/max_seqlen_q");
+  if (num_seqs == 0 || max_seqlen_q == 0) return Q3A_OK;
+  if (head_dim != kD) return fail(Q3A_EINVAL, "prefill: head_dim %d unsupported (need %d)", head_dim, kD);
+  if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
+    return fail(Q3A_EINVAL, "prefill: num_q_heads %d must be %d * num_kv_heads %d", num_q_heads, kG, num_kv_heads);
+  if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out) return fail(Q3A_EINVAL, "prefill: null pointer argument");
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;
+  if (align % 16 != 0) return fail(Q3A_EINVAL, "prefill: q/k/v/out must be 16-byte aligned");
+  if ((q_stride_t | q_stride_h | kv_stride_tok | kv_stride_head | o_stride_t | o_stride_h) % 8 != 0)
+    return fail(Q3A_EINVAL, "prefill: strides must be multiples of 8 elements (16 bytes)");
+  if (block_table != nullptr) {
+    if (page_size <= 0 || num_pages <= 0 || max_pages_per_seq <= 0)
+      return fail(Q3A_EINVAL, "prefill: paged K/V needs page_size, num_pages and max_pages_per_seq > 0");
+    if (kv_stride_page % 8 != 0) return fail(Q3A_EINVAL, "prefill: page stride must be a multiple of 8 elements");
+  }
+  const int nqt = (max_seqlen_q + kQT - 1) / kQT;
+  if (num_seqs > 0x7fffffff || nqt > 65535 || num_kv_heads > 65535)
+    return fail(Q3A_EINVAL, "prefill: grid too large (%d seqs x %d query tiles)", num_seqs, nqt);
+
+  PrefillArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.cu_q = cu_seqlens_q;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.kv_sp = kv_stride_page;
+  a.kv_st = kv_stride_tok;
+  a.kv_sh = kv_stride_head;
+  a.num_pages = num_pages;
+  a.page_size = page_size;
+  a.bt = block_table;
+  a.bt_sb = bt_stride_b;
+  a.max_pages = max_pages_per_seq;
+  a.cu_k = cu_seqlens_k;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_st = o_stride_t;
+  a.o_sh = o_stride_h;
+  a.causal = causal ? 1 : 0;
+  a.scale_log2 = softmax_scale * kLog2e;
+  hipLaunchKernelGGL(prefill_kernel, dim3(num_seqs, nqt, num_kv_heads), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "prefill: launch failed: %s", hipGetErrorString(e));
+  return Q3A_OK;
+}

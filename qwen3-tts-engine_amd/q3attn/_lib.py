@@ -43,6 +43,14 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int,                # batch, Hq, Hkv, D, n_live
         _c_float, _c_vp,                                       # softmax_scale, stream
     ]),
+    "q3a_prefill": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_vp,                          # q, q_stride_t, q_stride_h, cu_seqlens_q
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k, v, kv strides (page, tok, head)
+        _c_int, _c_int, _c_vp, _c_i64, _c_int,                 # num_pages, page_size, block_table, bt stride, max pages
+        _c_vp, _c_vp, _c_i64, _c_i64,                          # cu_seqlens_k, out, o_stride_t, o_stride_h
+        _c_int, _c_int, _c_int, _c_int, _c_int,                # num_seqs, max_seqlen_q, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
+    ]),
 }
 
 _lock = threading.Lock()

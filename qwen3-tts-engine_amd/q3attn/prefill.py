@@ -1,0 +1,118 @@
+"""Talker prefill attention (packed variable-length, MFMA) as torch custom ops over the q3attn C ABI.
+
+``flash_attn_varlen_func`` keeps the signature the talker uses at engine/talker.py:169 and ``flash_attn_func``
+the one at engine/arrivals.py:148 (bottom-right causal for a K/V prefix longer than the queries).  Both also
+accept the paged KV pool through ``block_table`` (the layout the talker writes at engine/talker.py:161-162),
+so prefill can read K/V back from the pool.  GPU only.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ._lib import check, lib
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+@torch.library.custom_op("q3attn::prefill", mutates_args=())
+def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+            cu_seqlens_k: torch.Tensor, block_table: Optional[torch.Tensor], max_seqlen_q: int,
+            softmax_scale: float, causal: bool) -> torch.Tensor:
+    """q [T, Hq, D]; k, v packed [Tk, Hkv, D] (block_table None) or the paged pool
+    [num_pages, page, Hkv, D]; cu_seqlens int32 [n+1].  Returns [T, Hq, D] bf16."""
+    _req(q.is_cuda, "q3attn.prefill: tensors must be on a GPU (there is no CPU path)")
+    for name, t in (("k", k), ("v", v), ("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k)):
+        _req(t.device == q.device, f"q3attn.prefill: {name} is on {t.device}, q on {q.device}")
+    _req(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
+         "q3attn.prefill: q, k, v must be bfloat16")
+    _req(q.dim() == 3 and q.stride(-1) == 1, "q3attn.prefill: q must be [tokens, heads, head_dim], dim contiguous")
+    _req(k.shape == v.shape and k.stride() == v.stride(), "q3attn.prefill: k and v must match in shape and strides")
+    _req(k.stride(-1) == 1, "q3attn.prefill: k/v head_dim must be contiguous")
+    _req(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32,
+         "q3attn.prefill: cu_seqlens must be int32")
+    _req(cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous() and cu_seqlens_q.shape == cu_seqlens_k.shape,
+         "q3attn.prefill: cu_seqlens_q/k must be contiguous [n+1]")
+    T, Hq, D = q.shape
+    n = cu_seqlens_q.shape[0] - 1
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if n <= 0 or T == 0:
+        return out.zero_() if T else out
+    if block_table is None:
+        _req(k.dim() == 3 and k.shape[2] == D, "q3attn.prefill: packed k/v must be [tokens, kv_heads, head_dim]")
+        Hkv = k.shape[1]
+        sp, st, sh, num_pages, page, bt_ptr, bt_sb, max_pages = 0, k.stride(0), k.stride(1), 0, 0, None, 0, 0
+    else:
+        _req(k.dim() == 4 and k.shape[3] == D, "q3attn.prefill: paged k/v must be [num_pages, page, kv_heads, head_dim]")
+        _req(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == n
+             and block_table.stride(1) == 1 and block_table.device == q.device,
+             "q3attn.prefill: block_table must be int32 [n, max_pages] with contiguous rows")
+        num_pages, page, Hkv = k.shape[0], k.shape[1], k.shape[2]
+        sp, st, sh = k.stride(0), k.stride(1), k.stride(2)
+        bt_ptr, bt_sb, max_pages = block_table.data_ptr(), block_table.stride(0), block_table.shape[1]
+    rc = lib().q3a_prefill(
+        q.data_ptr(), q.stride(0), q.stride(1), cu_seqlens_q.data_ptr(),
+        k.data_ptr(), v.data_ptr(), sp, st, sh, num_pages, page, bt_ptr, bt_sb, max_pages,
+        cu_seqlens_k.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+        n, int(max_seqlen_q), Hq, Hkv, D, float(softmax_scale), 1 if causal else 0,
+        torch.cuda.current_stream(q.device).cuda_stream)
+    check(rc, "q3a_prefill")
+    return out
+
+
+@prefill.register_fake
+def _prefill_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, max_seqlen_q, softmax_scale, causal):
+    return torch.empty_like(q, memory_format=torch.contiguous_format)
+
+
+def _unsupported(dropout_p, window_size, softcap, alibi_slopes, return_attn_probs):
+    if dropout_p or tuple(window_size) != (-1, -1) or softcap or alibi_slopes is not None or return_attn_probs:
+        raise NotImplementedError("q3attn: dropout, windows, softcap, alibi and returned probabilities are unsupported")
+
+
+def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
+                           softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                           deterministic=False, return_attn_probs=False, block_table=None):
+    """Drop-in for ``flash_attn.flash_attn_varlen_func`` as the talker calls it (engine/talker.py:169):
+    q [T, Hq, D], k/v [Tk, Hkv, D] (or the paged pool with ``block_table``), int32 cumulative lengths.
+    Returns [T, Hq, D]."""
+    _unsupported(dropout_p, window_size, softcap, alibi_slopes, return_attn_probs)
+    scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
+    return prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, int(max_seqlen_q), float(scale), bool(causal))
+
+
+_CU_CACHE: dict = {}
+
+
+def _cu(n: int, length: int, device) -> torch.Tensor:
+    key = (n, length, str(device))
+    t = _CU_CACHE.get(key)
+    if t is None:
+        t = torch.arange(0, (n + 1) * length, length, dtype=torch.int32, device=device)
+        _CU_CACHE[key] = t
+    return t
+
+
+def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                    alibi_slopes=None, deterministic=False, return_attn_probs=False):
+    """Drop-in for ``flash_attn.flash_attn_func`` as the fast-admission path calls it (engine/arrivals.py:148):
+    q [S, R, Hq, D], k/v [S, n, Hkv, D]; with ``causal`` query i sees the n - R prefix keys and the new keys
+    <= i (bottom-right).  Returns [S, R, Hq, D]."""
+    _unsupported(dropout_p, window_size, softcap, alibi_slopes, return_attn_probs)
+    _req(q.dim() == 4 and k.dim() == 4 and k.shape == v.shape, "q3attn.flash_attn_func: q [S,R,H,D], k/v [S,n,Hkv,D]")
+    S, R, Hq, D = q.shape
+    n = k.shape[1]
+    if q.stride(0) != R * q.stride(1):
+        q = q.contiguous()
+    if k.stride(0) != n * k.stride(1):
+        k = k.contiguous()
+    if v.stride(0) != n * v.stride(1):
+        v = v.contiguous()
+    scale = softmax_scale if softmax_scale is not None else D ** -0.5
+    o = prefill(q.reshape(S * R, Hq, D), k.reshape(S * n, k.shape[2], D), v.reshape(S * n, v.shape[2], D),
+                _cu(S, R, q.device), _cu(S, n, q.device), None, R, float(scale), bool(causal))
+    return o.view(S, R, Hq, D)

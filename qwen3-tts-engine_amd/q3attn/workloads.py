@@ -181,3 +181,73 @@ def make_cp(batch: int, device, seed: int = 0, steps: int = 16, kv_pad: int = 0)
 def cp_bytes(batch: int, n_live: int, hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM) -> int:
     """Bytes of one cp_attn call: K+V of the live slots, q in, o out."""
     return batch * (2 * hkv * n_live * d * 2 + 2 * hq * d * 2)
+
+
+@dataclasses.dataclass
+class PrefillWorkload:
+    q: torch.Tensor              # [T, Hq, D] bf16, packed sequences
+    k: torch.Tensor              # [T, Hkv, D] bf16, packed
+    v: torch.Tensor
+    cu_seqlens: torch.Tensor     # [n + 1] int32
+    lens: np.ndarray
+    k_cache: torch.Tensor | None = None   # paged pool holding the same K/V
+    v_cache: torch.Tensor | None = None
+    block_table: torch.Tensor | None = None
+    scale: float = HEAD_DIM ** -0.5
+
+    @property
+    def max_len(self) -> int:
+        return int(self.lens.max(initial=0))
+
+    def flops(self) -> int:
+        """Causal attention flops (QK^T and PV over the keys each query sees)."""
+        L = self.lens.astype(np.int64)
+        return int((4 * HEAD_DIM * HQ * (L * (L + 1) // 2)).sum())
+
+    def algorithmic_bytes(self) -> int:
+        """q read + o write + K/V read once per sequence and KV head + cu_seqlens and table entries."""
+        T = int(self.lens.sum())
+        pages = int(((self.lens + PAGE - 1) // PAGE).sum()) if self.block_table is not None else 0
+        return 2 * T * HQ * HEAD_DIM * 2 + 2 * T * HKV * HEAD_DIM * 2 + 4 * (len(self.lens) + 1) + 4 * pages
+
+
+def prefill_lengths(name: str, seed: int = 0) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    if name == "c4":
+        return rng.integers(150, 401, size=32).astype(np.int64)
+    raise ValueError(f"unknown prefill workload {name!r}")
+
+
+def make_prefill(device, lens, seed: int = 0, paged: bool = True, page: int = PAGE, num_pages: int | None = None,
+                 identity: bool = False) -> PrefillWorkload:
+    """Prompt prefill: each sequence's q/k get RoPE at positions 0..L-1; with ``paged`` the K/V are also
+    written into a pool through a seeded random (or identity) page table, as the talker does before it
+    attends (engine/talker.py:161-162)."""
+    device = torch.device(device)
+    lens = np.asarray(lens, dtype=np.int64)
+    T = int(lens.sum())
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    cos, sin = rope_tables(max(int(lens.max(initial=1)), 1), device)
+    pos = torch.from_numpy(np.concatenate([np.arange(L) for L in lens]) if T else np.zeros(0, np.int64)).to(device)
+    q = _rope(_unit_rms(torch.randn((T, HQ, HEAD_DIM), generator=gen, device=device)), cos[pos][:, None], sin[pos][:, None])
+    k = _rope(_unit_rms(torch.randn((T, HKV, HEAD_DIM), generator=gen, device=device)), cos[pos][:, None], sin[pos][:, None])
+    v = torch.randn((T, HKV, HEAD_DIM), generator=gen, device=device)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).to(device)
+    wl = PrefillWorkload(q=q.to(torch.bfloat16), k=k.to(torch.bfloat16), v=v.to(torch.bfloat16), cu_seqlens=cu,
+                         lens=lens)
+    if paged:
+        n = len(lens)
+        P = max(1, -(-int(lens.max(initial=1)) // page))
+        num_pages = n * P if num_pages is None else num_pages
+        rng = np.random.default_rng(seed + 7)
+        bt = np.arange(n * P).reshape(n, P) if identity else rng.permutation(num_pages)[: n * P].reshape(n, P)
+        slots = np.concatenate([bt[s, np.arange(L) // page] * page + np.arange(L) % page for s, L in enumerate(lens)])
+        slots_t = torch.from_numpy(slots.astype(np.int64)).to(device)
+        kc = torch.zeros((num_pages, page, HKV, HEAD_DIM), dtype=torch.bfloat16, device=device)
+        vc = torch.zeros_like(kc)
+        kc.view(-1, HKV, HEAD_DIM).index_copy_(0, slots_t, wl.k)
+        vc.view(-1, HKV, HEAD_DIM).index_copy_(0, slots_t, wl.v)
+        wl.k_cache, wl.v_cache = kc, vc
+        wl.block_table = torch.from_numpy(bt.astype(np.int32)).to(device)
+    return wl

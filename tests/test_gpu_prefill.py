@@ -1,0 +1,126 @@
+"""GPU parity of the MFMA prefill (q3a_prefill through the C ABI) against the oracle: packed varlen causal
+(engine/talker.py:169), read back from the paged pool (C4), the prefix + new bottom-right form
+(engine/arrivals.py:148), non-causal, and query rows that see no key."""
+import numpy as np
+import pytest
+import torch
+
+import q3attn
+from helpers import to_np
+from oracle import attention as ora
+from q3attn import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_varlen(wl):
+    cu = wl.cu_seqlens.cpu().numpy()
+    return ora.prefill_varlen(to_np(wl.q), to_np(wl.k), to_np(wl.v), cu, wl.scale)
+
+
+def check(out, ref, what):
+    ok, st = ora.compare(to_np(out), ref)
+    print(f"[parity] {what} {st}", flush=True)
+    assert ok, (what, st)
+
+
+def test_packed_varlen_causal(cuda_device):
+    lens = [1, 7, 16, 17, 33, 64, 65, 150, 3]
+    wl = W.make_prefill(cuda_device, lens, seed=1, paged=False)
+    out = q3attn.flash_attn_varlen_func(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len, wl.max_len,
+                                        softmax_scale=wl.scale, causal=True)
+    torch.cuda.synchronize()
+    check(out, oracle_varlen(wl), "packed varlen")
+
+
+def test_paged_c4_full(cuda_device):
+    lens = W.prefill_lengths("c4")
+    wl = W.make_prefill(cuda_device, lens, seed=0, paged=True, num_pages=4096)
+    out = q3attn.flash_attn_varlen_func(wl.q, wl.k_cache, wl.v_cache, wl.cu_seqlens, wl.cu_seqlens, wl.max_len,
+                                        wl.max_len, softmax_scale=wl.scale, causal=True, block_table=wl.block_table)
+    torch.cuda.synchronize()
+    ref = oracle_varlen(wl)
+    check(out, ref, "c4 paged")
+    packed = q3attn.flash_attn_varlen_func(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len, wl.max_len,
+                                           softmax_scale=wl.scale, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, packed), "paged and packed K/V sources must give identical results"
+
+
+def test_reference_layout_page256_identity(cuda_device):
+    wl = W.make_prefill(cuda_device, [77, 300, 5], seed=2, paged=True, page=256, identity=True)
+    out = q3attn.flash_attn_varlen_func(wl.q, wl.k_cache, wl.v_cache, wl.cu_seqlens, wl.cu_seqlens, wl.max_len,
+                                        wl.max_len, softmax_scale=wl.scale, causal=True, block_table=wl.block_table)
+    torch.cuda.synchronize()
+    check(out, oracle_varlen(wl), "page256")
+
+
+@pytest.mark.parametrize("S,R,n", [(4, 42, 77), (1, 5, 5), (8, 42, 77), (2, 70, 200)])
+def test_prefix_bottom_right(cuda_device, S, R, n):
+    """FastAdmit's dense form (engine/arrivals.py:118, 148): the k = n - R prefix keys plus R new keys."""
+    g = torch.Generator(device=cuda_device).manual_seed(S * 1000 + R)
+    q = torch.randn(S, R, 16, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    K = torch.randn(S, n, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    V = torch.randn(S, n, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    out = q3attn.flash_attn_func(q, K, V, softmax_scale=128 ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    check(out, ora.prefill_prefix(to_np(q), to_np(K), to_np(V), 128 ** -0.5), f"prefix S={S} R={R} n={n}")
+
+
+def test_non_causal(cuda_device):
+    lens = [9, 40, 129]
+    wl = W.make_prefill(cuda_device, lens, seed=3, paged=False)
+    out = q3attn.flash_attn_varlen_func(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len, wl.max_len,
+                                        softmax_scale=wl.scale, causal=False)
+    torch.cuda.synchronize()
+    q, k, v = to_np(wl.q), to_np(wl.k), to_np(wl.v)
+    cu = wl.cu_seqlens.cpu().numpy()
+    ref = np.zeros_like(q)
+    for i in range(len(lens)):
+        s = slice(cu[i], cu[i + 1])
+        ref[s] = _dense(q[s], k[s], v[s], wl.scale)
+    check(out, ref, "non-causal")
+
+
+def _dense(q, k, v, scale):
+    G = q.shape[1] // k.shape[1]
+    kk = np.repeat(k, G, axis=1).astype(np.float64)
+    vv = np.repeat(v, G, axis=1).astype(np.float64)
+    a = np.einsum("thd,shd->hts", q.astype(np.float64), kk) * scale
+    a -= a.max(-1, keepdims=True)
+    p = np.exp(a)
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("hts,shd->thd", p, vv)
+
+
+def test_query_rows_without_keys_are_zero(cuda_device):
+    """Lq > Lk with bottom-right alignment: the first Lq - Lk queries see no key."""
+    g = torch.Generator(device=cuda_device).manual_seed(5)
+    q = torch.randn(1, 20, 16, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    K = torch.randn(1, 12, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    V = torch.randn(1, 12, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    out = q3attn.flash_attn_func(q, K, V, softmax_scale=0.1, causal=True)
+    torch.cuda.synchronize()
+    assert not out[0, :8].float().abs().sum().item()
+    ref = ora.prefill_prefix(to_np(q[:, 8:]), to_np(K), to_np(V), 0.1)
+    check(out[:, 8:], ref, "rows with keys")
+
+
+def test_graph_capture_prefill(cuda_device):
+    wl = W.make_prefill(cuda_device, [33, 100], seed=4, paged=True, num_pages=64)
+    f = lambda: q3attn.flash_attn_varlen_func(wl.q, wl.k_cache, wl.v_cache, wl.cu_seqlens, wl.cu_seqlens, 100, 100,
+                                              softmax_scale=wl.scale, causal=True, block_table=wl.block_table)
+    eager = f().clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        f()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        static = f()
+    for _ in range(3):
+        torch.randn(1 << 18, device=cuda_device)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static, eager)
