@@ -101,12 +101,222 @@ def measured_traffic():
     return None
 
 
+def time_graph(dev, frame_fn, steps: int, warmup: int):
+    """Capture frame_fn once into a HIP graph (as the engine does, engine/talker.py:115-137), check a replay
+    against the eager result, then time `steps` replays with a HIP event pair around each.
+    Returns (wall ms per step, list of per-replay event ms)."""
+    import torch
+
+    stream = torch.cuda.Stream(dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        eager = [o.clone() for o in frame_fn()]
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        static_out = frame_fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    if not all(torch.equal(a, b) for a, b in zip(static_out, eager)):
+        raise RuntimeError("graph replay differs from the eager frame")
+    cur = torch.cuda.current_stream(dev)
+    for _ in range(warmup):
+        graph.replay()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(cur)
+        graph.replay()
+        ev[i][1].record(cur)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    return wall * 1e3 / steps, [a.elapsed_time(b) for a, b in ev], graph
+
+
+def base_record(metric, value, unit, args, ms_per_step, higher_is_better, config):
+    return {
+        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": higher_is_better, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": config,
+    }
+
+
+def bench_decode(args, dev, name):
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    t0 = time.time()
+    wl = W.make_decode(name, dev, layers=LAYERS, seed=args.seed)
+    torch.cuda.synchronize()
+    log(f"[bench] workload {name} built in {time.time() - t0:.1f} s: rows={wl.batch} live={(wl.ctx > 0).sum()} "
+        f"sum_ctx={int(wl.ctx.sum())} pool={tuple(wl.k_cache.shape)}")
+    nbytes = wl.algorithmic_bytes()
+
+    def layer_call(L):
+        return q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table,
+                                   wl.scale, args.split)
+
+    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [layer_call(L) for L in wl.layers], args.steps, args.warmup)
+    avg_call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
+    achieved = nbytes / (avg_call_us * 1e-6) / 1e9
+    log(f"[bench] {args.steps} graph replays of {LAYERS} calls: wall {ms_per_step:.3f} ms/step; events "
+        f"{statistics.mean(frame_ms):.3f} ms/frame (min {min(frame_ms):.3f}) = {avg_call_us:.1f} us/call; "
+        f"{achieved:.0f} GB/s = {achieved / HBM_PEAK_GBPS:.1%} of peak")
+
+    # Eager calls with an event pair around each (host launch gaps excluded): extra information.
+    cur = torch.cuda.current_stream(dev)
+    eg = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(LAYERS)]
+    for i, L in enumerate(wl.layers):
+        eg[i][0].record(cur)
+        layer_call(L)
+        eg[i][1].record(cur)
+    torch.cuda.synchronize()
+    eager_call_us = statistics.mean(a.elapsed_time(b) for a, b in eg) * 1e3
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.time()
+        cpu = cpu_baseline(wl)
+        log(f"[bench] cpu baseline {cpu['us_per_layer_call']:.0f} us/call in {time.time() - t0:.1f} s")
+
+    if name == "c5":
+        desc = ("talker paged decode attention, 576 rows (518 live, ctx log-uniform [64,1800]; 58 padded ctx=0), "
+                "GQA 16/8, head_dim 128, bf16 K/V, fp32 softmax/accumulate, 16-token pages, 131072-page pool, "
+                "28 layer calls per step with per-layer random tables")
+        metric = METRIC
+    else:
+        desc = (f"talker paged decode attention, {wl.batch} rows, ctx U[200,1200], GQA 16/8, head_dim 128, bf16, "
+                "16-token pages, 65536-page pool, 28 layer calls per step with per-layer random tables")
+        metric = f"paged decode attn µs/step and HBM GB/s (% peak) at {wl.batch} seats, 1×MI355X"
+    rec = base_record(metric, round(ms_per_step * 1e3, 2), "us/step", args, ms_per_step, False, {
+        "workload": desc, "rows": wl.batch, "sum_ctx": int(wl.ctx.sum()), "layers_per_step": LAYERS,
+        "split_tokens": args.split or "stream-K", "parallelism": "single GPU"})
+    rec.update({
+        "us_per_layer_call": round(avg_call_us, 2),
+        "us_per_layer_call_eager": round(eager_call_us, 2),
+        "hbm_gbps": round(achieved, 1),
+        "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBPS, 2),
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": measured_traffic() if name == "c5" else None,
+            "kernel": "paged decode call (stream-K decode kernel + combine kernel), per call inside the graph",
+            "bytes_per_call": nbytes,
+        },
+        "cpu_baseline": cpu,
+    })
+    return rec
+
+
+def bench_cp(args, dev):
+    """Code predictor: 512 rows, 5 layers x 16 steps (n_live = 1..16) per frame (engine/code_predictor.py:62-69)."""
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    B, L = 512, 5
+    layers = [W.make_cp(B, dev, seed=args.seed + l) for l in range(L)]
+    calls = [(qs[p], K, V, p + 1) for (qs, K, V) in layers for p in range(16)]
+    nbytes = sum(W.cp_bytes(B, n) for (_, _, _, n) in calls)
+    ms_per_step, frame_ms, _ = time_graph(
+        dev, lambda: [q3attn.cp_attn(q, K, V, n, W.HEAD_DIM ** -0.5) for (q, K, V, n) in calls], args.steps,
+        args.warmup)
+    frame_us = statistics.mean(frame_ms) * 1e3
+    achieved = nbytes / (frame_us * 1e-6) / 1e9
+    log(f"[bench] cp: {len(calls)} calls per frame, {frame_us:.1f} us/frame = {frame_us / len(calls):.2f} us/call, "
+        f"{achieved:.0f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.torch_cpu import cp_attn_rows
+        qs, K, V = layers[0]
+        qc, Kc, Vc = [t.cpu() for t in qs], K.cpu(), V.cpu()
+        times = []
+        for rep in range(3):
+            t0 = time.perf_counter()
+            for p in range(16):
+                cp_attn_rows(qc[p], Kc, Vc, p + 1, W.HEAD_DIM ** -0.5)
+            times.append(time.perf_counter() - t0)
+        us = statistics.median(times) * 1e6 * L
+        cpu = {"value": round(us, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"one layer's 16 steps at B={B} with the reference's torch bf16 ops on CPU "
+                         f"(engine/code_predictor.py:46-47), median of 3, x{L} layers"}
+    rec = base_record("code-predictor attn µs/step (5 layers x 16 steps) at 512 rows, 1×MI355X",
+                      round(ms_per_step * 1e3, 2), "us/step", args, ms_per_step, False,
+                      {"workload": "code-predictor 16-slot causal attention, 512 rows, GQA 16/8, head_dim 128, bf16, "
+                                   "n_live 1..16 per layer, 5 layers per step", "rows": B, "calls_per_step": len(calls),
+                       "parallelism": "single GPU"})
+    rec.update({"us_per_call": round(frame_us / len(calls), 3),
+                "roofline": {"bound": "latency (K/V resident in the 256 MB Infinity Cache)",
+                             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                             "bytes_per_step": nbytes},
+                "cpu_baseline": cpu})
+    return rec
+
+
+def bench_prefill(args, dev):
+    """Prompt prefill C4: 32 sequences, lengths U[150,400], K/V read from the paged pool, 28 layers per step,
+    each layer with its own q/k/v."""
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    lens = W.prefill_lengths("c4", args.seed)
+    wls = [W.make_prefill(dev, lens, seed=args.seed + l, paged=True, num_pages=4096) for l in range(LAYERS)]
+    w0 = wls[0]
+
+    def call(wl):
+        return q3attn.flash_attn_varlen_func(wl.q, wl.k_cache, wl.v_cache, wl.cu_seqlens, wl.cu_seqlens, wl.max_len,
+                                             wl.max_len, softmax_scale=wl.scale, causal=True,
+                                             block_table=wl.block_table)
+
+    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [call(wl) for wl in wls], args.steps, args.warmup)
+    call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
+    tflops = w0.flops() / (call_us * 1e-6) / 1e12
+    gbps = w0.algorithmic_bytes() / (call_us * 1e-6) / 1e9
+    log(f"[bench] c4 prefill: {call_us:.1f} us/call, {tflops:.1f} TFLOP/s, {gbps:.0f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.torch_cpu import prefill_rows
+        q, k, v = w0.q.float().cpu(), w0.k.float().cpu(), w0.v.float().cpu()
+        cu = w0.cu_seqlens.cpu()
+        times = []
+        for rep in range(3):
+            t0 = time.perf_counter()
+            prefill_rows(q, k, v, cu, w0.scale)
+            times.append(time.perf_counter() - t0)
+        us = statistics.median(times) * 1e6
+        cpu = {"value": round(us * LAYERS, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"layer 0 ({len(lens)} sequences) with the reference's fp32 per-sequence torch prefill "
+                         f"(engine/talker.py:165-167), median of 3 = {us:.0f} us, x{LAYERS} layers"}
+    rec = base_record("talker prefill attn µs/step (28 layers) at 32 sequences, 1×MI355X",
+                      round(ms_per_step * 1e3, 2), "us/step", args, ms_per_step, False,
+                      {"workload": "talker prompt prefill, 32 sequences, lengths U[150,400], causal, GQA 16/8, "
+                                   "head_dim 128, bf16, K/V read from a 16-token paged pool, 28 layers per step",
+                       "tokens": int(lens.sum()), "parallelism": "single GPU"})
+    rec.update({"us_per_layer_call": round(call_us, 2), "tflops": round(tflops, 2), "hbm_gbps": round(gbps, 1),
+                "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                             "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                             "mfma_tflops": round(tflops, 2), "mfma_peak_tflops": 2500.0,
+                             "flops_per_call": w0.flops(), "bytes_per_call": w0.algorithmic_bytes()},
+                "cpu_baseline": cpu})
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library default)")
+    ap.add_argument("--workload", default="c5", choices=["c5", "c3", "c2", "c4"],
+                    help="c5 (default, the headline metric), c3 decode, c2 code predictor, c4 prefill")
+    ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -121,9 +331,6 @@ def main() -> int:
 
     import torch
 
-    import q3attn
-    from q3attn import workloads as W
-
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.copy_probe_mib:
@@ -135,118 +342,12 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
         return 0
-    t0 = time.time()
-    wl = W.make_decode("c5", dev, layers=LAYERS, seed=args.seed)
-    torch.cuda.synchronize()
-    log(f"[bench] workload c5 built in {time.time() - t0:.1f} s: rows={wl.batch} live={(wl.ctx > 0).sum()} "
-        f"sum_ctx={int(wl.ctx.sum())} pool={tuple(wl.k_cache.shape)}")
-    nbytes = wl.algorithmic_bytes()
-
-    def layer_call(L):
-        return q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table,
-                                   wl.scale, args.split)
-
-    def frame():
-        return [layer_call(L) for L in wl.layers]
-
-    # The engine replays its 28-layer frame as one captured graph (engine/talker.py:115-137);
-    # the step here is the same: one replay of a graph holding the 28 decode-attention calls.
-    stream = torch.cuda.Stream(dev)
-    stream.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(stream):
-        eager = [o.clone() for o in frame()]
-    torch.cuda.current_stream(dev).wait_stream(stream)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        static_out = frame()
-    graph.replay()
-    torch.cuda.synchronize()
-    if not all(torch.equal(a, b) for a, b in zip(static_out, eager)):
-        raise RuntimeError("graph replay differs from the eager frame")
-
-    cur = torch.cuda.current_stream(dev)
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-
-    K = args.steps
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for i in range(K):
-        ev[i][0].record(cur)
-        graph.replay()
-        ev[i][1].record(cur)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    frame_ms = [a.elapsed_time(b) for a, b in ev]
-    avg_call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
-    ms_per_step = wall * 1e3 / K
-    us_per_step = ms_per_step * 1e3
-    achieved = nbytes / (avg_call_us * 1e-6) / 1e9
-    log(f"[bench] {K} graph replays of {LAYERS} calls: wall {ms_per_step:.3f} ms/step; events "
-        f"{statistics.mean(frame_ms):.3f} ms/frame (min {min(frame_ms):.3f}) = {avg_call_us:.1f} us/call; "
-        f"{achieved:.0f} GB/s = {achieved / HBM_PEAK_GBPS:.1%} of peak")
-
-    # Eager calls with an event pair around each (host launch gaps excluded): extra information.
-    eg = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(LAYERS * 2)]
-    i = 0
-    for _ in range(2):
-        for L in wl.layers:
-            eg[i][0].record(cur)
-            layer_call(L)
-            eg[i][1].record(cur)
-            i += 1
-    torch.cuda.synchronize()
-    eager_call_us = statistics.mean(a.elapsed_time(b) for a, b in eg) * 1e3
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        t0 = time.time()
-        cpu = cpu_baseline(wl)
-        log(f"[bench] cpu baseline {cpu['us_per_layer_call']:.0f} us/call in {time.time() - t0:.1f} s")
-
-    split = args.split or "stream-K"
-    rec = {
-        "metric": METRIC,
-        "value": round(us_per_step, 2),
-        "unit": "us/step",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": ("talker paged decode attention, 576 rows (518 live, ctx log-uniform [64,1800]; "
-                         "58 padded ctx=0), GQA 16/8, head_dim 128, bf16 K/V, fp32 softmax/accumulate, "
-                         "16-token pages, 131072-page pool, 28 layer calls per step with per-layer random tables"),
-            "rows": wl.batch,
-            "sum_ctx": int(wl.ctx.sum()),
-            "layers_per_step": LAYERS,
-            "split_tokens": split,
-            "parallelism": "single GPU",
-        },
-        "us_per_layer_call": round(avg_call_us, 2),
-        "us_per_layer_call_eager": round(eager_call_us, 2),
-        "hbm_gbps": round(achieved, 1),
-        "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBPS, 2),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic(),
-            "kernel": "paged decode call (stream-K decode kernel + combine kernel), per call inside the graph",
-            "bytes_per_call": nbytes,
-        },
-        "cpu_baseline": cpu,
-    }
+    if args.workload in ("c5", "c3"):
+        rec = bench_decode(args, dev, args.workload)
+    elif args.workload == "c2":
+        rec = bench_cp(args, dev)
+    else:
+        rec = bench_prefill(args, dev)
     print(json.dumps(rec), flush=True)
     return 0
 

@@ -32,3 +32,29 @@ def paged_decode_rows(q, k_cache, v_cache, seqlens, block_table, scale):
         a = torch.matmul(q[b].view(Hkv, G, D), k.transpose(-1, -2)) * scale
         out.append(torch.matmul(torch.softmax(a, dim=-1), v).reshape(Hq, D))
     return torch.stack(out, 0)
+
+
+def cp_attn_rows(q, K, V, n_live, scale):
+    """``CodePredictor._post``'s attention exactly as the reference writes it (engine/code_predictor.py:46-47),
+    on CPU bf16 tensors: q [B, 16, 128], K/V [B, 8, 16, 128] -> [B, 2048]."""
+    B, Hkv, S, D = K.shape
+    mask = torch.full((S, S), float("-inf")).triu(1).to(q.dtype)[n_live - 1]
+    att = torch.matmul(q.view(B, Hkv, q.shape[1] // Hkv, D), K.transpose(-1, -2)) * scale + mask
+    return torch.matmul(torch.softmax(att.float(), dim=-1).to(q.dtype), V).reshape(B, -1)
+
+
+def prefill_rows(q, k, v, cu_seqlens, scale):
+    """The fp32 single-sequence prefill of ``Talker.prefill_hidden`` (engine/talker.py:165-167), looped over
+    the packed sequences: q [T, 16, 128], k/v [T, 8, 128] fp32 -> [T, 16, 128]."""
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    out = torch.empty_like(q)
+    for i in range(len(cu_seqlens) - 1):
+        s0, s1 = int(cu_seqlens[i]), int(cu_seqlens[i + 1])
+        L = s1 - s0
+        qh = q[s0:s1].transpose(0, 1).reshape(Hkv, Hq // Hkv, L, D)
+        kh = k[s0:s1].transpose(0, 1)[:, None]
+        vh = v[s0:s1].transpose(0, 1)[:, None]
+        a = torch.matmul(qh, kh.transpose(-1, -2)) * scale + torch.full((L, L), float("-inf")).triu(1)
+        out[s0:s1] = torch.matmul(torch.softmax(a, dim=-1), vh).reshape(Hq, L, D).transpose(0, 1)
+    return out

@@ -22,6 +22,9 @@ CFLAGS = [
     "-Wall", "-Wno-unused-function",
     # no packed-fp32 instructions in generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: loop-carried accumulators that VALU code also touches are otherwise
+    # copied VGPR <-> AGPR around every MFMA block
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -42,7 +42,7 @@ struct PrefillArgs {
   const uint16_t* k;
   const uint16_t* v;
   int64_t kv_sp, kv_st, kv_sh;
-  int num_pages, page_size;
+  int num_pages, page_size, page_shift;  // paged: page_size is a power of two >= 16
   const int32_t* bt;  // nullptr: packed K/V
   int64_t bt_sb;
   int max_pages;
@@ -96,38 +96,51 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     kend = min(Lk, Lk - Lq + last + 1);
   }
   const int ntiles = kend > 0 ? (kend + kKT - 1) / kKT : 0;
+  const int jlim = a.causal ? min(Lk - 1, qpos) : Lk - 1;  // last key this lane's token sees
 
-  // Element offset of key j's row (head 0), or -1 when its page is not in the pool.
-  auto key_row = [&](int j) -> int64_t {
-    if (a.bt == nullptr) return (int64_t)(k0 + j) * a.kv_st;
-    const int pidx = j / a.page_size;
-    const int p = a.bt[(int64_t)s * a.bt_sb + pidx];
-    if ((unsigned)p >= (unsigned)a.num_pages) return -1;
-    return (int64_t)p * a.kv_sp + (int64_t)(j - pidx * a.page_size) * a.kv_st;
-  };
-
-  // Cooperative tile loads: K chunk (key (tid>>4) + 16r, dims 8*(tid&15)); V keys 4*(tid&15)+r,
-  // dims 8*(tid>>4).
+  // Cooperative tile loads: K chunk (key (tid>>4) + 16r, dims 8*(tid&15)); V keys 4*(tid&15)+r (one
+  // page: pages hold a multiple of 16 tokens), dims 8*(tid>>4).  The page indices of a tile are all
+  // fetched before any K/V load is issued, so a tile costs two memory round trips, not one per key.
+  const int64_t bt_row = (int64_t)s * a.bt_sb;
   uint4 kr[4], vr[4];
   auto load_tile = [&](int t) {
     const int kb = t * kKT;
+    const int jv = kb + 4 * (tid & 15);
+    int64_t krow[4], vrow;
+    if (a.bt != nullptr) {
+      int pk[4], pv = -1;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = kb + (tid >> 4) + 16 * r;
-      kr[r] = make_uint4(0u, 0u, 0u, 0u);
-      if (j < Lk) {
-        const int64_t row = key_row(j);
-        if (row >= 0) kr[r] = *reinterpret_cast<const uint4*>(a.k + row + g * a.kv_sh + 8 * (tid & 15));
+      for (int r = 0; r < 4; ++r) {
+        const int jk = kb + (tid >> 4) + 16 * r;
+        pk[r] = jk < Lk ? a.bt[bt_row + (jk >> a.page_shift)] : -1;
       }
+      if (jv < Lk) pv = a.bt[bt_row + (jv >> a.page_shift)];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int jk = kb + (tid >> 4) + 16 * r;
+        krow[r] = (unsigned)pk[r] < (unsigned)a.num_pages
+                      ? (int64_t)pk[r] * a.kv_sp + (int64_t)(jk & (a.page_size - 1)) * a.kv_st : -1;
+      }
+      vrow = (unsigned)pv < (unsigned)a.num_pages
+                 ? (int64_t)pv * a.kv_sp + (int64_t)(jv & (a.page_size - 1)) * a.kv_st : -1;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int jk = kb + (tid >> 4) + 16 * r;
+        krow[r] = jk < Lk ? (int64_t)(k0 + jk) * a.kv_st : -1;
+      }
+      vrow = jv < Lk ? (int64_t)(k0 + jv) * a.kv_st : -1;
     }
+    // K rows of keys outside the sequence (or on an invalid page) read row 0 of the buffer instead: their
+    // scores are masked to -inf, so the values never matter and the loads need no branch.
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      kr[r] = *reinterpret_cast<const uint4*>(a.k + (krow[r] >= 0 ? krow[r] : 0) + g * a.kv_sh + 8 * (tid & 15));
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int j = kb + 4 * (tid & 15) + r;
       vr[r] = make_uint4(0u, 0u, 0u, 0u);
-      if (j < Lk) {
-        const int64_t row = key_row(j);
-        if (row >= 0) vr[r] = *reinterpret_cast<const uint4*>(a.v + row + g * a.kv_sh + 8 * (tid >> 4));
-      }
+      if (vrow >= 0 && jv + r < Lk)
+        vr[r] = *reinterpret_cast<const uint4*>(a.v + vrow + (int64_t)r * a.kv_st + g * a.kv_sh + 8 * (tid >> 4));
     }
   };
   auto store_tile = [&]() {
@@ -176,23 +189,27 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
         st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv), qb[kk], st[kb], 0, 0, 0);
       }
     }
-    // Scale, mask, per-token max over the tile (this lane's 16 keys, then the 4 lanes of the token).
-    float x[4][4];
+    // Mask: key j is visible to this lane's token iff j <= jlim (= min(Lk - 1, qpos) when causal).
+    // Relative to the tile and this lane's key rows that is one compare per score against `lim`.
+    // Masked scores become -inf; the running max m is kept in scaled (log2) units.
+    const int lim = jlim - t * kKT - 4 * g4;
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int j = t * kKT + kb * 16 + 4 * g4 + i;
-        const bool ok = j < Lk && (!a.causal || j <= qpos);
-        x[kb][i] = ok ? st[kb][i] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, x[kb][i]);
+        st[kb][i] = (kb * 16 + i <= lim) ? st[kb][i] : -INFINITY;
+        mx = fmaxf(mx, st[kb][i]);
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m, mx);
-    if (__any(mn > m)) {
+    mx *= a.scale_log2;
+    // Lazy rescale: keep the running max while no token's tile max exceeds it by more than 8 (log2
+    // units), so p = exp2(s * scale - m) <= 256 is exact enough in bf16/fp32 and (l, acc) are rescaled
+    // only when a max grows past that margin.  The first tile always sets the max.
+    if (__any(mx > m + 8.f)) {
+      const float mn = fmaxf(m, mx);
       const float alpha = fast_exp2(m - mn);
       l *= alpha;
 #pragma unroll
@@ -212,8 +229,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       float p[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[i] = fast_exp2(x[2 * s2][i] - m);
-        p[4 + i] = fast_exp2(x[2 * s2 + 1][i] - m);
+        p[i] = fast_exp2(fmaf(st[2 * s2][i], a.scale_log2, -m));
+        p[4 + i] = fast_exp2(fmaf(st[2 * s2 + 1][i], a.scale_log2, -m));
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) l += p[i];
@@ -280,6 +297,8 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
     if (page_size <= 0 || num_pages <= 0 || max_pages_per_seq <= 0)
       return fail(Q3A_EINVAL, "prefill: paged K/V needs page_size, num_pages and max_pages_per_seq > 0");
     if (kv_stride_page % 8 != 0) return fail(Q3A_EINVAL, "prefill: page stride must be a multiple of 8 elements");
+    if (page_size < 16 || (page_size & (page_size - 1)) != 0)
+      return fail(Q3A_EINVAL, "prefill: page_size %d must be a power of two >= 16", page_size);
   }
   const int nqt = (max_seqlen_q + kQT - 1) / kQT;
   if (num_seqs > 0x7fffffff || nqt > 65535 || num_kv_heads > 65535)
@@ -297,6 +316,8 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
   a.kv_sh = kv_stride_head;
   a.num_pages = num_pages;
   a.page_size = page_size;
+  a.page_shift = 0;
+  while (block_table != nullptr && (1 << a.page_shift) < page_size) ++a.page_shift;
   a.bt = block_table;
   a.bt_sb = bt_stride_b;
   a.max_pages = max_pages_per_seq;

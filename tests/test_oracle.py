@@ -278,3 +278,25 @@ def test_rope_table_closed_form():
         ang = pos * (1.0e6 ** (-2 * i / 128))
         assert math.isclose(cos[pos, i], math.cos(ang), abs_tol=1e-6)
         assert math.isclose(sin[pos, i + 64], math.sin(ang), abs_tol=1e-6)
+
+
+def test_cpu_baseline_ports_agree_with_oracle():
+    """oracle/torch_cpu.py (timed as the CPU baseline) computes what the numpy oracle computes."""
+    from oracle import torch_cpu as tc
+    q, k, v, ctx, bt = _decode_case(B=4, Hq=16, Hkv=8, D=128, page=16, ctx=(0, 1, 40, 77), num_pages=32, seed=23)
+    got = tc.paged_decode_rows(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), ctx,
+                               torch.from_numpy(bt), 0.09).numpy()
+    np.testing.assert_allclose(got, ora.paged_decode(q, k, v, ctx, bt, 0.09), atol=2e-6)
+    qc, K, V = _cp_case(B=5, seed=29)
+    bf = lambda x: torch.from_numpy(x).to(torch.bfloat16)
+    got = tc.cp_attn_rows(bf(qc), bf(K), bf(V), 6, 128 ** -0.5).float().numpy()
+    d = np.abs(got - ora.cp_attn_torch_path(qc, K, V, 6, 128 ** -0.5))
+    assert d.max() <= 2 ** -7 * np.abs(got).max() and (d == 0).mean() > 0.95
+    r = np.random.default_rng(31)
+    lens = [3, 20]
+    cu = np.array([0, 3, 23])
+    qp = _bf16(r.standard_normal((23, 16, 32)))
+    kp = _bf16(r.standard_normal((23, 8, 32)))
+    vp = _bf16(r.standard_normal((23, 8, 32)))
+    got = tc.prefill_rows(torch.from_numpy(qp), torch.from_numpy(kp), torch.from_numpy(vp), cu, 0.2).numpy()
+    np.testing.assert_allclose(got, ora.prefill_varlen(qp, kp, vp, cu, 0.2), atol=2e-6)
