@@ -90,6 +90,23 @@ int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
                 int n_live, float softmax_scale, void* stream);
 
 /*
+ * Code-predictor slot write + attention in one launch.
+ *
+ * Replaces the pair K.index_copy_(2, p, k.unsqueeze(2)); V.index_copy_(2, p, v.unsqueeze(2)) followed by
+ * the attention of _post (engine/code_predictor.py:58 then :46-47), with p = n_live - 1: slot p of K/V[b, h]
+ * is overwritten with k_new/v_new[b, h] and the query attends over slots 0..p, slot p taken from the new rows.
+ *
+ *   k_new [B, Hkv, D] bf16, row stride kn_stride_b, head stride D
+ *   v_new [B, Hkv, D] bf16, row stride vn_stride_b, head stride D (a view into the qkv projection is fine)
+ *   q, k, v, out, strides and requirements as in q3a_cp_attn; k and v are written (slot n_live - 1 only).
+ */
+int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void* k_new, int64_t kn_stride_b,
+                       const void* v_new, int64_t vn_stride_b, void* k, void* v, int64_t kv_stride_b,
+                       int64_t kv_stride_h, int64_t kv_stride_s, void* out, int64_t o_stride_b, int batch,
+                       int num_q_heads, int num_kv_heads, int head_dim, int n_live, float softmax_scale,
+                       void* stream);
+
+/*
  * Talker prefill attention (packed variable-length, MFMA).
  *
  * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, ..., causal=True) at

@@ -5,6 +5,10 @@
 // scores and softmax in float32, probabilities rounded to bf16, P.V accumulated in float32,
 // output rounded to bf16.  Slots >= n_live are never read.
 //
+// The append form also takes this step's k/v rows: slot n_live-1 of K/V[b, g] is written from them
+// (the K.index_copy_ / V.index_copy_ of engine/code_predictor.py:58) by the same wave that attends,
+// which uses the new rows straight from registers.
+//
 // One wave per (row, KV head).  Scores: lane l takes slot l/4 and a quarter of the head
 // dimension (4 x 16 B loads; the 4 lanes of a slot read 64 contiguous bytes per instruction) and
 // reduces with two quad DPP steps.  P.V: lane l owns output dims 2l, 2l+1 of both query heads and
@@ -24,9 +28,12 @@ constexpr int kWavesPerBlock = 4;
 struct CpArgs {
   const uint16_t* q;
   int64_t q_sb;
-  const uint16_t* k;
-  const uint16_t* v;
+  uint16_t* k;  // written only at slot n_live - 1, and only when k_new != nullptr
+  uint16_t* v;
   int64_t kv_sb, kv_sh, kv_ss;
+  const uint16_t* k_new;  // optional [B, Hkv, D] rows for slot n_live - 1 (row strides kn_sb / vn_sb,
+  const uint16_t* v_new;  // head stride D)
+  int64_t kn_sb, vn_sb;
   uint16_t* out;
   int64_t o_sb;
   int pairs, hkv, n_live;
@@ -43,24 +50,42 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   const int c = lane & 3;
   const bool live = slot < a.n_live;
 
-  const uint16_t* kb = a.k + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
-  const uint16_t* vb = a.v + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
+  uint16_t* kb = a.k + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
+  uint16_t* vb = a.v + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
   const uint16_t* qb = a.q + (int64_t)b * a.q_sb + (int64_t)(kG * g) * kD;
+  // With k_new/v_new, slot n_live - 1 comes from those rows (and is stored into the scratch here);
+  // it is never read back from the scratch, so the write and the reads of this wave cannot race.
+  const bool append = a.k_new != nullptr;
+  const int last = a.n_live - 1;
+  const uint16_t* knb = append ? a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD : nullptr;
+  const uint16_t* vnb = append ? a.v_new + (int64_t)b * a.vn_sb + (int64_t)g * kD : nullptr;
 
   // Lane (slot, c) holds dims 32*i + 8*c .. +8 for i = 0..3, of K[slot] and of both query heads.
   uint4 kr[4], qr[kG][4];
+  const bool k_from_new = append && slot == last;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = 32 * i + 8 * c;
-    kr[i] = live ? *reinterpret_cast<const uint4*>(kb + (int64_t)slot * a.kv_ss + d)
-                 : make_uint4(0u, 0u, 0u, 0u);
+    kr[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (k_from_new) kr[i] = *reinterpret_cast<const uint4*>(knb + d);
+    else if (live) kr[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)slot * a.kv_ss + d);
 #pragma unroll
     for (int h = 0; h < kG; ++h) qr[h][i] = *reinterpret_cast<const uint4*>(qb + h * kD + d);
   }
   uint32_t vr[kSlots];
 #pragma unroll
-  for (int s = 0; s < kSlots; ++s)
-    vr[s] = s < a.n_live ? *reinterpret_cast<const uint32_t*>(vb + (int64_t)s * a.kv_ss + 2 * lane) : 0u;
+  for (int s = 0; s < kSlots; ++s) {
+    vr[s] = 0u;
+    if (append && s == last) vr[s] = *reinterpret_cast<const uint32_t*>(vnb + 2 * lane);
+    else if (s < a.n_live) vr[s] = *reinterpret_cast<const uint32_t*>(vb + (int64_t)s * a.kv_ss + 2 * lane);
+  }
+  if (append) {
+    if (k_from_new) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(kb + (int64_t)last * a.kv_ss + 32 * i + 8 * c) = kr[i];
+    }
+    *reinterpret_cast<uint32_t*>(vb + (int64_t)last * a.kv_ss + 2 * lane) = vr[last];
+  }
 
   float p[kG];
 #pragma unroll
@@ -112,32 +137,38 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
 
 using namespace q3a;
 
-extern "C" int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
-                           int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,
-                           int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads,
-                           int head_dim, int n_live, float softmax_scale, void* stream) {
-  if (batch < 0) return fail(Q3A_EINVAL, "cp_attn: batch %d < 0", batch);
+static int cp_launch(const void* q, int64_t q_stride_b, void* k, void* v, int64_t kv_stride_b,
+                     int64_t kv_stride_h, int64_t kv_stride_s, const void* k_new, const void* v_new,
+                     int64_t kn_stride_b, int64_t vn_stride_b, void* out, int64_t o_stride_b, int batch,
+                     int num_q_heads, int num_kv_heads, int head_dim, int n_live, float softmax_scale,
+                     void* stream, const char* who) {
+  if (batch < 0) return fail(Q3A_EINVAL, "%s: batch %d < 0", who, batch);
   if (batch == 0) return Q3A_OK;
-  if (head_dim != kD) return fail(Q3A_EINVAL, "cp_attn: head_dim %d unsupported (need %d)", head_dim, kD);
+  if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
   if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
-    return fail(Q3A_EINVAL, "cp_attn: num_q_heads %d must be %d * num_kv_heads %d", num_q_heads, kG, num_kv_heads);
-  if (n_live < 1 || n_live > kSlots) return fail(Q3A_EINVAL, "cp_attn: n_live %d outside [1, %d]", n_live, kSlots);
-  if (!q || !k || !v || !out) return fail(Q3A_EINVAL, "cp_attn: null pointer argument");
-  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;
-  if (align % 16 != 0) return fail(Q3A_EINVAL, "cp_attn: q/K/V/out must be 16-byte aligned");
-  if ((q_stride_b | kv_stride_b | kv_stride_h | kv_stride_s | o_stride_b) % 8 != 0)
-    return fail(Q3A_EINVAL, "cp_attn: strides must be multiples of 8 elements (16 bytes)");
+    return fail(Q3A_EINVAL, "%s: num_q_heads %d must be %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
+  if (n_live < 1 || n_live > kSlots) return fail(Q3A_EINVAL, "%s: n_live %d outside [1, %d]", who, n_live, kSlots);
+  if (!q || !k || !v || !out) return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)k_new |
+                          (uintptr_t)v_new;
+  if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: q/K/V/out/k_new/v_new must be 16-byte aligned", who);
+  if ((q_stride_b | kv_stride_b | kv_stride_h | kv_stride_s | o_stride_b | kn_stride_b | vn_stride_b) % 8 != 0)
+    return fail(Q3A_EINVAL, "%s: strides must be multiples of 8 elements (16 bytes)", who);
   const int64_t pairs = (int64_t)batch * num_kv_heads;
-  if (pairs > ((int64_t)1 << 30)) return fail(Q3A_EINVAL, "cp_attn: batch too large");
+  if (pairs > ((int64_t)1 << 30)) return fail(Q3A_EINVAL, "%s: batch too large", who);
 
   CpArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_stride_b;
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
+  a.k = static_cast<uint16_t*>(k);
+  a.v = static_cast<uint16_t*>(v);
   a.kv_sb = kv_stride_b;
   a.kv_sh = kv_stride_h;
   a.kv_ss = kv_stride_s;
+  a.k_new = static_cast<const uint16_t*>(k_new);
+  a.v_new = static_cast<const uint16_t*>(v_new);
+  a.kn_sb = kn_stride_b;
+  a.vn_sb = vn_stride_b;
   a.out = static_cast<uint16_t*>(out);
   a.o_sb = o_stride_b;
   a.pairs = (int)pairs;
@@ -148,6 +179,26 @@ extern "C" int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, con
   hipLaunchKernelGGL(cp_attn_kernel, dim3(blocks), dim3(64 * kWavesPerBlock), 0,
                      static_cast<hipStream_t>(stream), a);
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "cp_attn: launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   return Q3A_OK;
+}
+
+extern "C" int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
+                           int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,
+                           int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads,
+                           int head_dim, int n_live, float softmax_scale, void* stream) {
+  return cp_launch(q, q_stride_b, const_cast<void*>(k), const_cast<void*>(v), kv_stride_b, kv_stride_h,
+                   kv_stride_s, nullptr, nullptr, 0, 0, out, o_stride_b, batch, num_q_heads, num_kv_heads,
+                   head_dim, n_live, softmax_scale, stream, "cp_attn");
+}
+
+extern "C" int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void* k_new, int64_t kn_stride_b,
+                                  const void* v_new, int64_t vn_stride_b, void* k, void* v, int64_t kv_stride_b,
+                                  int64_t kv_stride_h, int64_t kv_stride_s, void* out, int64_t o_stride_b,
+                                  int batch, int num_q_heads, int num_kv_heads, int head_dim, int n_live,
+                                  float softmax_scale, void* stream) {
+  if (!k_new || !v_new) return fail(Q3A_EINVAL, "cp_attn_append: null k_new/v_new");
+  return cp_launch(q, q_stride_b, k, v, kv_stride_b, kv_stride_h, kv_stride_s, k_new, v_new, kn_stride_b,
+                   vn_stride_b, out, o_stride_b, batch, num_q_heads, num_kv_heads, head_dim, n_live,
+                   softmax_scale, stream, "cp_attn_append");
 }

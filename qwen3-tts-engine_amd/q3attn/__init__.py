@@ -2,12 +2,13 @@
 
 Entry points (each a drop-in for the reference call it names):
   * ``flash_attn_with_kvcache`` / ``paged_decode``  -- talker decode attention (engine/talker.py:77)
-  * ``cp_attn``                                     -- code-predictor attention (engine/cp_attn.py:33-39)
+  * ``cp_attn`` / ``cp_attn_append``                 -- code-predictor attention (engine/cp_attn.py:33-39;
+                                                       slot write fused: engine/code_predictor.py:58)
   * ``flash_attn_varlen_func`` / ``flash_attn_func``  -- prefill (engine/talker.py:169, engine/arrivals.py:148)
 """
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 from ._lib import LIB_PATH, Q3AttnError, lib  # noqa: F401
-from .cp_attn import cp_attn, cp_attn_op  # noqa: F401
+from .cp_attn import cp_attn, cp_attn_append, cp_attn_append_op, cp_attn_op  # noqa: F401
 from .ops import flash_attn_with_kvcache, paged_decode  # noqa: F401
 from .prefill import flash_attn_func, flash_attn_varlen_func, prefill  # noqa: F401

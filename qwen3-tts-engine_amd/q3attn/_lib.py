@@ -43,6 +43,13 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int,                # batch, Hq, Hkv, D, n_live
         _c_float, _c_vp,                                       # softmax_scale, stream
     ]),
+    "q3a_cp_attn_append": (_c_int, [
+        _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,           # q, q_sb, k_new, kn_sb, v_new, vn_sb
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k, v, kv strides (b, h, s)
+        _c_vp, _c_i64,                                         # out, o_stride_b
+        _c_int, _c_int, _c_int, _c_int, _c_int,                # batch, Hq, Hkv, D, n_live
+        _c_float, _c_vp,                                       # softmax_scale, stream
+    ]),
     "q3a_prefill": (_c_int, [
         _c_vp, _c_i64, _c_i64, _c_vp,                          # q, q_stride_t, q_stride_h, cu_seqlens_q
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k, v, kv strides (page, tok, head)

@@ -5,6 +5,10 @@
 [B, 2048], K/V [B, 8, 16, 128] bf16 whose batch stride may exceed the live batch, ``n_live`` =
 p + 1 live slots -> o [B, 2048] bf16.  Scores and softmax are float32, probabilities are rounded
 to bf16 before P.V, P.V accumulates in float32.  GPU only.
+
+``cp_attn_append(q, k, v, K, V, p, scale)`` is the slot write of engine/code_predictor.py:58
+(``K.index_copy_(2, p, k.unsqueeze(2))`` and the same for V) fused with that attention over
+n_live = p + 1 slots: one launch instead of three.
 """
 from __future__ import annotations
 
@@ -20,19 +24,7 @@ def _req(cond: bool, msg: str) -> None:
 
 @torch.library.custom_op("q3attn::cp_attn", mutates_args=())
 def cp_attn_op(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, n_live: int, scale: float) -> torch.Tensor:
-    _req(q.is_cuda, "q3attn.cp_attn: tensors must be on a GPU (there is no CPU path)")
-    _req(K.device == q.device and V.device == q.device, "q3attn.cp_attn: q, K, V must share a device")
-    _req(q.dtype == torch.bfloat16 and K.dtype == torch.bfloat16 and V.dtype == torch.bfloat16,
-         "q3attn.cp_attn: q, K, V must be bfloat16")
-    _req(K.dim() == 4 and K.shape == V.shape and K.stride() == V.stride(),
-         "q3attn.cp_attn: K and V must be [B, kv_heads, slots, head_dim] with equal strides")
-    B, Hkv, S, D = K.shape
-    _req(K.stride(3) == 1, "q3attn.cp_attn: K/V head_dim must be contiguous")
-    _req(1 <= n_live <= S, f"q3attn.cp_attn: n_live {n_live} outside [1, {S}]")
-    q2 = q.reshape(q.shape[0], -1)
-    _req(q2.shape[0] == B and q2.shape[1] % D == 0, "q3attn.cp_attn: q and K batch/head_dim mismatch")
-    _req(q2.stride(1) == 1, "q3attn.cp_attn: q rows must be contiguous")
-    Hq = q2.shape[1] // D
+    q2, B, Hkv, D, Hq = _check_common(q, K, V, n_live, "cp_attn")
     out = torch.empty((B, Hq * D), dtype=q.dtype, device=q.device)
     if B == 0:
         return out
@@ -42,6 +34,55 @@ def cp_attn_op(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, n_live: int, s
         torch.cuda.current_stream(q.device).cuda_stream)
     check(rc, "q3a_cp_attn")
     return out
+
+
+def _check_common(q, K, V, n_live, who):
+    _req(q.is_cuda, f"q3attn.{who}: tensors must be on a GPU (there is no CPU path)")
+    _req(K.device == q.device and V.device == q.device, f"q3attn.{who}: q, K, V must share a device")
+    _req(q.dtype == torch.bfloat16 and K.dtype == torch.bfloat16 and V.dtype == torch.bfloat16,
+         f"q3attn.{who}: q, K, V must be bfloat16")
+    _req(K.dim() == 4 and K.shape == V.shape and K.stride() == V.stride(),
+         f"q3attn.{who}: K and V must be [B, kv_heads, slots, head_dim] with equal strides")
+    B, Hkv, S, D = K.shape
+    _req(K.stride(3) == 1, f"q3attn.{who}: K/V head_dim must be contiguous")
+    _req(1 <= n_live <= S, f"q3attn.{who}: n_live {n_live} outside [1, {S}]")
+    q2 = q.reshape(q.shape[0], -1)
+    _req(q2.shape[0] == B and q2.shape[1] % D == 0, f"q3attn.{who}: q and K batch/head_dim mismatch")
+    _req(q2.stride(1) == 1, f"q3attn.{who}: q rows must be contiguous")
+    return q2, B, Hkv, D, q2.shape[1] // D
+
+
+def _new_rows(x, B, Hkv, D, name):
+    if x.dim() == 2:
+        x = x.view(x.shape[0], Hkv, D)
+    _req(x.dtype == torch.bfloat16, f"q3attn.cp_attn_append: {name} must be bfloat16")
+    _req(tuple(x.shape) == (B, Hkv, D), f"q3attn.cp_attn_append: {name} must be [B, {Hkv}, {D}]")
+    _req(x.stride(2) == 1 and x.stride(1) == D, f"q3attn.cp_attn_append: {name} heads must be packed rows")
+    return x
+
+
+@torch.library.custom_op("q3attn::cp_attn_append", mutates_args=("K", "V"))
+def cp_attn_append_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
+                      p: int, scale: float) -> torch.Tensor:
+    q2, B, Hkv, D, Hq = _check_common(q, K, V, int(p) + 1, "cp_attn_append")
+    _req(k.device == q.device and v.device == q.device, "q3attn.cp_attn_append: k, v must share q's device")
+    k3 = _new_rows(k, B, Hkv, D, "k")
+    v3 = _new_rows(v, B, Hkv, D, "v")
+    out = torch.empty((B, Hq * D), dtype=q.dtype, device=q.device)
+    if B == 0:
+        return out
+    rc = lib().q3a_cp_attn_append(
+        q2.data_ptr(), q2.stride(0), k3.data_ptr(), k3.stride(0), v3.data_ptr(), v3.stride(0),
+        K.data_ptr(), V.data_ptr(), K.stride(0), K.stride(1), K.stride(2),
+        out.data_ptr(), out.stride(0), B, Hq, Hkv, D, int(p) + 1, float(scale),
+        torch.cuda.current_stream(q.device).cuda_stream)
+    check(rc, "q3a_cp_attn_append")
+    return out
+
+
+@cp_attn_append_op.register_fake
+def _cp_attn_append_fake(q, k, v, K, V, p, scale):
+    return q.new_empty((q.shape[0], K.shape[1] * 2 * K.shape[3]))
 
 
 @cp_attn_op.register_fake
@@ -54,3 +95,10 @@ def cp_attn(q, K, V, n_live, scale):
     """q [B,16,128] (or [B,2048]), K/V [B,8,16,128] (row stride may exceed the live batch),
     n_live = p + 1 -> o [B,2048].  engine/cp_attn.py:33-39."""
     return cp_attn_op(q, K, V, int(n_live), float(scale))
+
+
+def cp_attn_append(q, k, v, K, V, p, scale):
+    """Slot write + attention of one code-predictor step (engine/code_predictor.py:58 then :46-47):
+    K[:, :, p] = k, V[:, :, p] = v (k, v [B, 8, 128], v may be a view into the qkv projection), then
+    attention over slots 0..p -> o [B, 2048]."""
+    return cp_attn_append_op(q, k, v, K, V, int(p), float(scale))

@@ -10,7 +10,8 @@ Decode workloads (16 query heads over 8 KV heads, head_dim 128, pages of 16 toke
   * ``c3``: 256 rows, ctx ~ U[200, 1200], random table over a 65,536-page pool;
   * ``c5``: 576 rows, 518 live with ctx = round(exp(U[ln 64, ln 1800])) and 58 padded rows with
     ctx = 0 at the tail, random table over a 131,072-page pool.
-The code-predictor workload ``cp`` is 512 rows with dense 16-slot K/V buffers.
+The code-predictor workload ``c2`` is 512 rows with dense 16-slot K/V buffers (5 layers x 16 steps).
+Prefill workload ``c4``: 32 sequences of U[150, 400] tokens packed, causal, K/V through the page pool.
 """
 from __future__ import annotations
 
@@ -149,14 +150,6 @@ def make_decode(name: str, device, layers: int = 1, seed: int = 0, ctx: np.ndarr
                           layers=out_layers, ctx=ctx)
 
 
-@dataclasses.dataclass
-class CpWorkload:
-    q: torch.Tensor      # [B, Hq, D] bf16, one per AR step (list)
-    K: torch.Tensor      # [B, Hkv, 16, D] bf16
-    V: torch.Tensor
-    scale: float = HEAD_DIM ** -0.5
-
-
 def make_cp(batch: int, device, seed: int = 0, steps: int = 16, kv_pad: int = 0) -> tuple:
     """Dense 16-slot K/V scratch (engine/code_predictor.py:20-21) filled for all 16 slots and one
     query per step p (RoPE at position p).  ``kv_pad`` > 0 allocates the slot rows wider than
@@ -178,9 +171,10 @@ def make_cp(batch: int, device, seed: int = 0, steps: int = 16, kv_pad: int = 0)
     return qs, Kb[..., :HEAD_DIM], Vb[..., :HEAD_DIM]
 
 
-def cp_bytes(batch: int, n_live: int, hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM) -> int:
-    """Bytes of one cp_attn call: K+V of the live slots, q in, o out."""
-    return batch * (2 * hkv * n_live * d * 2 + 2 * hq * d * 2)
+def cp_bytes(batch: int, n_live: int, hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM, append: bool = False) -> int:
+    """Bytes of one cp_attn call: K+V of the live slots, q in, o out; with ``append`` also the write of
+    the new slot's K+V (its reads are already counted as live slots)."""
+    return batch * (2 * hkv * n_live * d * 2 + 2 * hq * d * 2 + (2 * hkv * d * 2 if append else 0))
 
 
 @dataclasses.dataclass

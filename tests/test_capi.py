@@ -95,6 +95,20 @@ def test_cp_attn_rejects_bad_arguments(kw, frag):
     assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
 
 
+@pytest.mark.parametrize("kw,frag", [
+    (dict(kn=None), "k_new"), (dict(vn=None), "k_new"), (dict(kn=18), "aligned"), (dict(vn_sb=1030), "strides"),
+    (dict(n_live=0), "n_live"), (dict(Hq=8), "num_q_heads"),
+])
+def test_cp_attn_append_rejects_bad_arguments(kw, frag):
+    a = dict(q=16, q_sb=2048, kn=16, kn_sb=1024, vn=16, vn_sb=4096, k=16, v=16, kv_sb=16384, kv_sh=2048,
+             kv_ss=128, out=16, o_sb=2048, B=4, Hq=16, Hkv=8, D=128, n_live=3, scale=0.088)
+    a.update(kw)
+    rc = _lib.lib().q3a_cp_attn_append(a["q"], a["q_sb"], a["kn"], a["kn_sb"], a["vn"], a["vn_sb"], a["k"], a["v"],
+                                       a["kv_sb"], a["kv_sh"], a["kv_ss"], a["out"], a["o_sb"], a["B"], a["Hq"],
+                                       a["Hkv"], a["D"], a["n_live"], a["scale"], None)
+    assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
+
+
 def test_python_entry_points_refuse_cpu_tensors():
     q = torch.zeros(2, 1, 16, 128, dtype=torch.bfloat16)
     kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16)
@@ -105,6 +119,10 @@ def test_python_entry_points_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         q3attn.cp_attn(torch.zeros(2, 16, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16),
                        torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16), 3, 0.1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        q3attn.cp_attn_append(torch.zeros(2, 16, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 128, dtype=torch.bfloat16),
+                              torch.zeros(2, 8, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16),
+                              torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16), 2, 0.1)
 
 
 def test_unsupported_flash_attn_arguments_raise():
@@ -127,4 +145,8 @@ def test_fake_impl_traces_shapes():
         assert o.shape == (3, 16, 128) and o.dtype == torch.bfloat16
         c = torch.ops.q3attn.cp_attn(q, torch.empty(3, 8, 16, 128, dtype=torch.bfloat16),
                                      torch.empty(3, 8, 16, 128, dtype=torch.bfloat16), 4, 0.1)
+        assert c.shape == (3, 2048)
+        kv = torch.empty(3, 8, 128, dtype=torch.bfloat16)
+        c = torch.ops.q3attn.cp_attn_append(q, kv, kv, torch.empty(3, 8, 16, 128, dtype=torch.bfloat16),
+                                            torch.empty(3, 8, 16, 128, dtype=torch.bfloat16), 4, 0.1)
         assert c.shape == (3, 2048)

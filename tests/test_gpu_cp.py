@@ -83,3 +83,68 @@ def test_odd_batch_sizes(cuda_device):
         torch.cuda.synchronize()
         ok, st = ora.compare(to_np(o), ora.cp_attn_triton_path(to_np(qs[3]), to_np(K), to_np(V), 4, 0.088))
         assert ok, (B, st)
+
+
+def _step_rows(B, device, seed):
+    """This step's k (contiguous [B, 8, 128]) and v as a view into a [B, 4096] qkv projection, the layouts
+    engine/code_predictor.py:38-42 hands to the slot write."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    k = torch.randn(B, 8, 128, generator=g, device=device).to(torch.bfloat16)
+    qkv = torch.randn(B, 4096, generator=g, device=device).to(torch.bfloat16)
+    return k, qkv[:, 3072:].view(B, 8, 128)
+
+
+@pytest.mark.parametrize("kv_pad", [0, 8])
+def test_append_matches_index_copy_then_attn(cuda_device, kv_pad):
+    """cp_attn_append == K.index_copy_ + V.index_copy_ + cp_attn, bit for bit, for every slot p, and leaves
+    the scratch exactly as the index_copy_ pair does (engine/code_predictor.py:58)."""
+    B = 300
+    qs, K, V = W.make_cp(B, cuda_device, seed=11, kv_pad=kv_pad)
+    _, K2, V2 = W.make_cp(B, cuda_device, seed=11, kv_pad=kv_pad, steps=0)
+    for t in (K, V, K2, V2):
+        t.zero_()
+    scale = W.HEAD_DIM ** -0.5
+    for p in range(16):
+        k, v = _step_rows(B, cuda_device, 100 + p)
+        pidx = torch.tensor([p], device=cuda_device)
+        K.index_copy_(2, pidx, k.unsqueeze(2))
+        V.index_copy_(2, pidx, v.unsqueeze(2))
+        ref = q3attn.cp_attn(qs[p], K, V, p + 1, scale)
+        got = q3attn.cp_attn_append(qs[p], k, v, K2, V2, p, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), p
+        assert torch.equal(K2, K) and torch.equal(V2, V), p
+        if p in (0, 7, 15):
+            ok, st = ora.compare(to_np(got), ora.cp_attn_triton_path(to_np(qs[p]), to_np(K), to_np(V), p + 1, scale))
+            print(f"[parity] cp_append p={p} pad={kv_pad} vs triton_path {st}", flush=True)
+            assert ok, (p, st)
+
+
+def test_append_writes_only_slot_p(cuda_device):
+    B = 64
+    qs, K, V = W.make_cp(B, cuda_device, seed=12)
+    k, v = _step_rows(B, cuda_device, 7)
+    K0, V0 = K.clone(), V.clone()
+    q3attn.cp_attn_append(qs[5], k, v, K, V, 5, 0.088)
+    torch.cuda.synchronize()
+    keep = [s for s in range(16) if s != 5]
+    assert torch.equal(K[:, :, keep], K0[:, :, keep]) and torch.equal(V[:, :, keep], V0[:, :, keep])
+    assert torch.equal(K[:, :, 5], k) and torch.equal(V[:, :, 5], v)
+
+
+def test_append_batch_slice_of_wider_scratch(cuda_device):
+    """K/V are [l, :B] slices of the [layers, max_bs, 8, 16, 128] scratch: rows >= B stay untouched."""
+    max_bs, B, p = 96, 40, 3
+    qs, K, V = W.make_cp(max_bs, cuda_device, seed=13)
+    Kbig, Vbig = torch.stack([K.clone(), K.clone()]), torch.stack([V.clone(), V.clone()])
+    before = Kbig.clone(), Vbig.clone()
+    k, v = _step_rows(B, cuda_device, 8)
+    got = q3attn.cp_attn_append(qs[p][:B], k, v, Kbig[1, :B], Vbig[1, :B], p, 0.088)
+    K[:B, :, p] = k
+    V[:B, :, p] = v
+    ref = q3attn.cp_attn(qs[p][:B], K[:B], V[:B], p + 1, 0.088)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(Kbig[0], before[0][0]) and torch.equal(Vbig[0], before[1][0])
+    assert torch.equal(Kbig[1, B:], before[0][1, B:]) and torch.equal(Vbig[1, B:], before[1][1, B:])
+    assert torch.equal(Kbig[1, :B], K[:B]) and torch.equal(Vbig[1, :B], V[:B])
