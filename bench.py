@@ -177,6 +177,10 @@ def bench_decode(args, dev, name):
     torch.cuda.synchronize()
     eager_call_us = statistics.mean(a.elapsed_time(b) for a, b in eg) * 1e3
 
+    append = None
+    if not args.no_append:
+        append = bench_decode_append(args, dev, wl)
+
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
@@ -209,7 +213,56 @@ def bench_decode(args, dev, name):
         },
         "cpu_baseline": cpu,
     })
+    if append is not None:
+        rec["append_form"] = append
     return rec
+
+
+def bench_decode_append(args, dev, wl):
+    """Extra information beside the headline: the same frame with this step's K/V append included, once as the
+    engine does it (two index_copy_ scatters per layer, engine/talker.py:72-73, then the decode call) and once
+    fused (paged_decode_append).  Each layer's new token is its row's last context token; the step's k/v rows
+    are that slot's current contents, so the frame rewrites identical values and stays replayable."""
+    import numpy as np
+    import torch
+
+    import q3attn
+
+    page = wl.page_size
+    live = wl.ctx > 0
+    pos = np.where(live, wl.ctx - 1, 0)
+    old = torch.from_numpy(wl.ctx - 1).to(torch.int32).to(dev)
+    kflat = wl.k_cache.view(-1, wl.k_cache.shape[2], wl.k_cache.shape[3])
+    vflat = wl.v_cache.view(-1, wl.v_cache.shape[2], wl.v_cache.shape[3])
+    steps = []
+    for L in wl.layers:
+        bt = L.block_table.cpu().numpy().astype(np.int64)
+        slot = bt[np.arange(wl.batch), pos // page] * page + pos % page
+        # padded rows (ctx 0) write nothing in the fused form; the scatter form writes them to a scratch slot
+        # (the reference sends padded rows to a scratch seat) -- here slot 0 with its own value
+        slot = torch.from_numpy(np.where(live, slot, 0)).to(dev)
+        steps.append((L, slot, kflat.index_select(0, slot), vflat.index_select(0, slot)))
+
+    def fused():
+        return [q3attn.paged_decode_append(L.q, k, v, wl.k_cache, wl.v_cache, old, L.block_table, wl.scale,
+                                           args.split) for (L, _, k, v) in steps]
+
+    def scatter_then_decode():
+        out = []
+        for (L, slot, k, v) in steps:
+            kflat.index_copy_(0, slot, k)
+            vflat.index_copy_(0, slot, v)
+            out.append(q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale,
+                                           args.split))
+        return out
+
+    _, fr_split, _ = time_graph(dev, scatter_then_decode, args.steps, args.warmup)
+    _, fr_fused, _ = time_graph(dev, fused, args.steps, args.warmup)
+    a = statistics.mean(fr_fused) * 1e3 / LAYERS
+    b = statistics.mean(fr_split) * 1e3 / LAYERS
+    log(f"[bench] append form: fused {a:.1f} us/layer call; index_copy_ x2 + decode {b:.1f} us/layer call")
+    return {"fused_us_per_layer_call": round(a, 2), "index_copy_then_decode_us_per_layer_call": round(b, 2),
+            "fused_us_per_step": round(a * LAYERS, 1), "index_copy_then_decode_us_per_step": round(b * LAYERS, 1)}
 
 
 def bench_cp(args, dev):
@@ -347,6 +400,7 @@ def main() -> int:
                     help="c5 (default, the headline metric), c3 decode, c2 code predictor, c4 prefill")
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-append", action="store_true", help="skip the KV-append comparison of the decode bench")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates rocprof byte counters)")

@@ -64,6 +64,34 @@ int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      int num_kv_heads, int head_dim, float softmax_scale, int split_tokens,
                      void* stream);
 
+/*
+ * Talker decode attention with this step's K/V append fused in.
+ *
+ * Replaces the pair kc[l].view(-1,8,128).index_copy_(0, slot, k); vc[l]...index_copy_(0, slot, v)
+ * (engine/talker.py:72-73) and the attention call after it (engine/talker.py:77), i.e. the
+ * flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v, cache_seqlens=pos, block_table=bt, ...) form.
+ *
+ *   k_new, v_new [B, Hkv, D] bf16, row strides kn_stride_b / vn_stride_b, head stride D
+ *   cache_seqlens[B] int32   tokens ALREADY in the cache (= the new token's position)
+ *   everything else as in q3a_paged_decode (k_cache/v_cache are written)
+ *
+ * Row b writes k_new[b], v_new[b] into page block_table[b][p / page_size], offset p % page_size with
+ * p = cache_seqlens[b], then attends over the p + 1 tokens 0..p; the new token is taken from k_new/v_new
+ * directly (the slot's previous contents are never read).  Rows with cache_seqlens < 0, or whose new token
+ * would fall past max_pages_per_seq*page_size, are skipped: zero output, nothing written.  A page index
+ * outside [0, num_pages) is neither written nor attended.  The page that receives a row's new token must not
+ * be read by another row of the same call.  Workspace: q3a_paged_decode_workspace_bytes() as for
+ * q3a_paged_decode.
+ */
+int q3a_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                            int64_t kn_stride_b, const void* v_new, int64_t vn_stride_b, void* k_cache,
+                            void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head,
+                            int num_pages, int page_size, const int32_t* cache_seqlens,
+                            const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq, void* out,
+                            int64_t o_stride_b, int64_t o_stride_h, void* workspace, size_t workspace_bytes,
+                            int batch, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                            int split_tokens, void* stream);
+
 /* Bytes of workspace q3a_paged_decode needs for this shape and split (0 if none is needed). */
 size_t q3a_paged_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                         int max_pages_per_seq, int page_size, int split_tokens);

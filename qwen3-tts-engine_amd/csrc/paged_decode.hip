@@ -21,6 +21,12 @@
 // workgroup; the combine kernel merges them and writes zeros for ctx == 0 rows.
 // Alternative (split_tokens > 0): one workgroup per (row, fixed-size split), partials merged by
 // the same kind of combine.
+//
+// Append form (flash_attn_with_kvcache with k=, v=; replaces the index_copy_ pair of
+// engine/talker.py:72-73 before the call at :77): cache_seqlens counts the tokens already cached,
+// the row attends over cache_seqlens + 1 tokens, and the last one is this step's k/v row.  The wave
+// that consumes a row's last tile swaps that token's registers for the k_new/v_new row, writes the
+// row into the page slot, and attends with the registers; the slot's old contents are never used.
 #include "q3a_common.h"
 #include "../../include/q3attn.h"
 
@@ -43,6 +49,9 @@ struct DecodeArgs {
   const uint16_t* kc;
   const uint16_t* vc;
   int64_t kv_sp, kv_st, kv_sh;
+  const uint16_t* k_new;  // append form: [batch, hkv, kD] rows (head stride kD), else unused
+  const uint16_t* v_new;
+  int64_t kn_sb, vn_sb;
   int num_pages, page_size;
   uint32_t page_bytes;  // byte extent of one page's tokens (bounds of the buffer loads)
   const int32_t* seqlens;
@@ -75,6 +84,19 @@ __device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int c) {
   return c < 0 ? 0 : (c > cap ? cap : c);
 }
 
+// Tokens row b attends over.  Append form: the cached tokens plus the new one; a row whose new
+// token would not fit the table (or with cache_seqlens < 0) is skipped: zero output, nothing written.
+template <bool kAppend>
+__device__ __forceinline__ int row_ctx(const DecodeArgs& a, int b) {
+  const int c = a.seqlens[b];
+  if constexpr (kAppend) {
+    const int cap = a.max_pages * a.page_size;
+    return (c < 0 || c >= cap) ? 0 : c + 1;
+  } else {
+    return clamp_ctx(a, c);
+  }
+}
+
 __device__ __forceinline__ int readlane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
 // Issues the 8 loads of tile j.  A tile past the list or with an invalid page issues loads against a
@@ -98,6 +120,46 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, const TileList& 
     T.k[i] = buffer_load16_stream(rk, o);
     T.v[i] = buffer_load16_stream(rv, o);
   }
+}
+
+// Append form, the last tile of a row, once its loads have landed: token nvalid-1 is the new one.  The
+// 16 lanes holding it take this step's k/v row instead of the stale slot (its old contents are never
+// used) and store that row into the slot; an invalid page is neither written nor attended (tile_update
+// masks it).  The two row loads are issued here, at consume time, so they never sit in a register across
+// the tile pipeline; the wave waits once per row for them.
+__device__ __forceinline__ void take_new_token(const DecodeArgs& a, const TileList& L, uint32_t lane_off,
+                                               int grp, int g, int j, int row, KVTile& T) {
+  const int page = readlane(L.page, j);
+  const int off = readlane(L.off, j);
+  const int tn = readlane(L.nvalid, j) - 1;
+  const int i_new = tn >> 2;
+  const bool mine = grp == (tn & 3);
+  const bool ok = (unsigned)page < (unsigned)a.num_pages;
+  // Uniform bases in SGPRs: the new rows of (row, g), and the slot's page (lane_off already holds the
+  // lane's token-in-quad, head and dim offset, so the slot adds only (off + 4*i_new) tokens).
+  const uint32_t dim_off = (uint32_t)(threadIdx.x & 15) * 16;
+  const __amdgpu_buffer_rsrc_t rkn = make_rsrc(a.k_new + (int64_t)row * a.kn_sb + g * kD, kD * 2);
+  const __amdgpu_buffer_rsrc_t rvn = make_rsrc(a.v_new + (int64_t)row * a.vn_sb + g * kD, kD * 2);
+  const int64_t pbase = ok ? (int64_t)page * a.kv_sp : 0;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kc + pbase, ok ? a.page_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + pbase, ok ? a.page_bytes : 0u);
+  const uint32_t slot_off = (uint32_t)((off + 4 * i_new) * a.kv_st * 2);
+  // K, then V: one 4-register row live at a time (the other tile of the pipeline is in flight).
+  const uint4 kn = buffer_load16_s(rkn, dim_off, 0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i == i_new && mine) T.k[i] = kn;
+  if (mine) buffer_store16_s(kn, rk, lane_off, slot_off);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint4 vn = buffer_load16_s(rvn, dim_off, 0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i == i_new && mine) T.v[i] = vn;
+  if (mine) buffer_store16_s(vn, rv, lane_off, slot_off);
+  // Drain here (vmcnt(0); expcnt, lgkmcnt untouched) so this once-per-row path rejoins the tile loop
+  // with nothing outstanding: the loop's own waits then stay at "this tile only" on every tile.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 __device__ __forceinline__ uint32_t u4get(const uint4& v, int c) {
@@ -222,10 +284,13 @@ __device__ __forceinline__ void store_row8(uint16_t* dst, const float (&x)[8], f
   *reinterpret_cast<uint4*>(dst) = v;
 }
 
+// The (row, head pair) base is uniform, so it lives in the descriptor (SGPRs); the lane adds only its
+// 16 B of dims, keeping 64-bit per-lane address pairs out of the kernels' register budget.
 __device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int g, int dl, uint4 (&q)[kG]) {
+  const __amdgpu_buffer_rsrc_t rq =
+      make_rsrc(a.q + (int64_t)b * a.q_sb + (int64_t)(kG * g) * a.q_sh, (uint32_t)(((kG - 1) * a.q_sh + kD) * 2));
 #pragma unroll
-  for (int h = 0; h < kG; ++h)
-    q[h] = *reinterpret_cast<const uint4*>(a.q + b * a.q_sb + (kG * g + h) * a.q_sh + dl);
+  for (int h = 0; h < kG; ++h) q[h] = buffer_load16_s(rq, (uint32_t)dl * 2, (uint32_t)(h * a.q_sh * 2));
 }
 
 // Lanes 0..15 hold the merged state: the normalised output row of both query heads.
@@ -346,13 +411,14 @@ constexpr int kLast = 2;      // tile closes a segment
 constexpr int kRowStart = 4;  // tile is tile 0 of its row
 constexpr int kRowEnd = 8;    // tile is the last tile of its row
 
+template <bool kAppend>
 __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs a) {
   __shared__ int s_ctx[kSkMaxRows];
   __shared__ int s_prefix[kSkMaxRows + 1];
   __shared__ int s_wsum[16];
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
-  const int g = tid >> 6;
+  const int g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform KV head
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int dl = (lane & 15) * 8;
@@ -363,7 +429,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   const int r0 = min(B, tid * per), r1 = min(B, r0 + per);
   int sum = 0;
   for (int r = r0; r < r1; ++r) {
-    const int c = clamp_ctx(a, a.seqlens[r]);
+    const int c = row_ctx<kAppend>(a, r);
     s_ctx[r] = c;
     sum += (c + kTile - 1) / kTile;
   }
@@ -431,7 +497,9 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
                (mt == 0 ? kRowStart : 0) | (mt == ntr - 1 ? kRowEnd : 0);
     }
 
-    auto process = [&](const KVTile& T, int j) {
+    // Segment bookkeeping for tile j, run before tile j+1 is issued: the q loads of a new segment then
+    // precede that prefetch, so consuming tile j waits for tile j's loads and q only, never for j+1's.
+    auto open_segment = [&](int j) {
       const int fl = readlane(vflags, j);
       if (fl & kFirst) {
         seg_row = readlane(vrow, j);
@@ -439,6 +507,12 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         seg_slot = (cb + j == lo) ? 0 : 1;
         reset_state(m, l, acc);
         load_q(a, seg_row, g, dl, q);
+      }
+    };
+    auto process = [&](KVTile& T, int j) {
+      const int fl = readlane(vflags, j);
+      if constexpr (kAppend) {
+        if (fl & kRowEnd) take_new_token(a, L, lane_off, grp, g, j, seg_row, T);
       }
       tile_update(a, L, q, T, j, grp, m, l, acc);
       if (fl & kLast) {
@@ -452,12 +526,21 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       }
     };
 
+    auto issue = [&](int j, KVTile& T) {
+      issue_tile(a, L, lane_off, grp, j, T);
+      // Keep the whole tile's loads ahead of the consumer: no instruction of the next tile_update may
+      // be scheduled between them (that would wait for the current tile in the middle of the issue).
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
     KVTile A, Bt;
-    issue_tile(a, L, lane_off, grp, 0, A);
+    issue(0, A);
     for (int j = 0; j < L.n; j += 2) {
-      issue_tile(a, L, lane_off, grp, j + 1, Bt);
+      open_segment(j);
+      issue(j + 1, Bt);
       process(A, j);
-      issue_tile(a, L, lane_off, grp, j + 2, A);
+      if (j + 1 < L.n) open_segment(j + 1);
+      issue(j + 2, A);
       if (j + 1 < L.n) process(Bt, j + 1);
     }
   }
@@ -467,7 +550,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
 // writes zeros for rows with no context.
 __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
-  const int g = threadIdx.x >> 6;
+  const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
   const int lane = threadIdx.x & 63;
   const int p0 = a.prefix[b];
   const int p1 = a.prefix[b + 1];
@@ -489,15 +572,16 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const Dec
 }
 
 // ------------------------------------------------------------------------------ fixed-split path
+template <bool kAppend>
 __global__ __launch_bounds__(1024) void paged_decode_split_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
   const int s = blockIdx.y;
-  const int g = threadIdx.x >> 6;
+  const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
   const int lane = threadIdx.x & 63;
   const int grp = lane >> 4;
   const int dl = (lane & 15) * 8;
 
-  const int ctx = clamp_ctx(a, a.seqlens[b]);
+  const int ctx = row_ctx<kAppend>(a, b);
   if (ctx == 0) {
     if (s == 0) write_zero_row(a, b, g, lane);
     return;
@@ -526,13 +610,24 @@ __global__ __launch_bounds__(1024) void paged_decode_split_kernel(const DecodeAr
   float m[kG], l[kG], acc[kG][8];
   reset_state(m, l, acc);
 
+  // Append form: the last tile of the last split holds the new token.
+  const int tail = (kAppend && s == ns - 1) ? L.n - 1 : -1;
+  auto issue = [&](int j, KVTile& T) {
+    issue_tile(a, L, lane_off, grp, j, T);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto consume = [&](KVTile& T, int j) {
+    if (kAppend && j == tail) take_new_token(a, L, lane_off, grp, g, j, b, T);
+    tile_update(a, L, q, T, j, grp, m, l, acc);
+  };
+
   KVTile A, Bt;
-  issue_tile(a, L, lane_off, grp, 0, A);
+  issue(0, A);
   for (int j = 0; j < L.n; j += 2) {
-    issue_tile(a, L, lane_off, grp, j + 1, Bt);
-    tile_update(a, L, q, A, j, grp, m, l, acc);
-    issue_tile(a, L, lane_off, grp, j + 2, A);
-    if (j + 1 < L.n) tile_update(a, L, q, Bt, j + 1, grp, m, l, acc);
+    issue(j + 1, Bt);
+    consume(A, j);
+    issue(j + 2, A);
+    if (j + 1 < L.n) consume(Bt, j + 1);
   }
 
   merge_lanes(16, m, l, acc);
@@ -544,11 +639,12 @@ __global__ __launch_bounds__(1024) void paged_decode_split_kernel(const DecodeAr
   }
 }
 
+template <bool kAppend>
 __global__ __launch_bounds__(1024) void paged_decode_split_combine_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
-  const int g = threadIdx.x >> 6;
+  const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
   const int lane = threadIdx.x & 63;
-  const int ctx = clamp_ctx(a, a.seqlens[b]);
+  const int ctx = row_ctx<kAppend>(a, b);
   if (ctx == 0) return;
   const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
   if (ns <= 1) return;
@@ -571,20 +667,28 @@ int default_split(int batch, int hkv, int max_pages, int page_size) {
 }
 
 // Workgroups of the stream-K kernel the current device holds at once (cached per device).
-int sk_grid(int hkv) {
-  static int cache[64][17];
+// The workspace is sized for the larger of the two forms, so one buffer serves both.
+int sk_grid_of(int hkv, bool append) {
+  static int cache[64][17][2];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kSkMaxGrid;
-  int& c = cache[dev][hkv];
+  int& c = cache[dev][hkv][append ? 1 : 0];
   if (c > 0) return c;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return kSkMaxGrid;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel, 64 * hkv, 0) != hipSuccess)
-    return kSkMaxGrid;
+  const hipError_t e =
+      append ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true>, 64 * hkv, 0)
+             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<false>, 64 * hkv, 0);
+  if (e != hipSuccess) return kSkMaxGrid;
   int g = cus * (per_cu > 0 ? per_cu : 1);
   g = g < 1 ? 1 : (g > kSkMaxGrid ? kSkMaxGrid : g);
   c = g;
   return g;
+}
+
+int sk_grid(int hkv) {
+  const int g0 = sk_grid_of(hkv, false), g1 = sk_grid_of(hkv, true);
+  return g0 > g1 ? g0 : g1;
 }
 
 bool use_sk(int batch, int split_tokens) { return split_tokens == 0 && batch <= kSkMaxRows; }
@@ -621,53 +725,55 @@ extern "C" size_t q3a_paged_decode_workspace_bytes(int batch, int num_q_heads, i
   return workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, split_tokens);
 }
 
-extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                                const void* k_cache, const void* v_cache, int64_t kv_stride_page,
-                                int64_t kv_stride_tok, int64_t kv_stride_head, int num_pages,
-                                int page_size, const int32_t* cache_seqlens,
-                                const int32_t* block_table, int64_t bt_stride_b,
-                                int max_pages_per_seq, void* out, int64_t o_stride_b,
-                                int64_t o_stride_h, void* workspace, size_t workspace_bytes_,
-                                int batch, int num_q_heads, int num_kv_heads, int head_dim,
-                                float softmax_scale, int split_tokens, void* stream) {
-  if (batch < 0) return fail(Q3A_EINVAL, "paged_decode: batch %d < 0", batch);
+static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                         int64_t kn_stride_b, const void* v_new, int64_t vn_stride_b, const void* k_cache,
+                         const void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head,
+                         int num_pages, int page_size, const int32_t* cache_seqlens, const int32_t* block_table,
+                         int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_b,
+                         int64_t o_stride_h, void* workspace, size_t workspace_bytes_, int batch, int num_q_heads,
+                         int num_kv_heads, int head_dim, float softmax_scale, int split_tokens, void* stream,
+                         const char* who) {
+  const bool append = k_new != nullptr;
+  if (batch < 0) return fail(Q3A_EINVAL, "%s: batch %d < 0", who, batch);
   if (batch == 0) return Q3A_OK;
-  if (head_dim != kD) return fail(Q3A_EINVAL, "paged_decode: head_dim %d unsupported (need %d)", head_dim, kD);
+  if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
   if (num_kv_heads < 1 || num_kv_heads > 16)
-    return fail(Q3A_EINVAL, "paged_decode: num_kv_heads %d outside [1, 16]", num_kv_heads);
+    return fail(Q3A_EINVAL, "%s: num_kv_heads %d outside [1, 16]", who, num_kv_heads);
   if (num_q_heads != kG * num_kv_heads)
-    return fail(Q3A_EINVAL, "paged_decode: num_q_heads %d != %d * num_kv_heads %d", num_q_heads, kG, num_kv_heads);
+    return fail(Q3A_EINVAL, "%s: num_q_heads %d != %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
   if (page_size <= 0 || page_size % kTile != 0)
-    return fail(Q3A_EINVAL, "paged_decode: page_size %d is not a positive multiple of %d", page_size, kTile);
+    return fail(Q3A_EINVAL, "%s: page_size %d is not a positive multiple of %d", who, page_size, kTile);
   if (num_pages <= 0 || max_pages_per_seq <= 0)
-    return fail(Q3A_EINVAL, "paged_decode: num_pages %d / max_pages_per_seq %d must be > 0", num_pages, max_pages_per_seq);
+    return fail(Q3A_EINVAL, "%s: num_pages %d / max_pages_per_seq %d must be > 0", who, num_pages, max_pages_per_seq);
   if (!q || !k_cache || !v_cache || !cache_seqlens || !block_table || !out)
-    return fail(Q3A_EINVAL, "paged_decode: null pointer argument");
-  const uintptr_t align = (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out;
-  if (align % 16 != 0) return fail(Q3A_EINVAL, "paged_decode: q/k_cache/v_cache/out must be 16-byte aligned");
-  if ((q_stride_b | q_stride_h | kv_stride_page | kv_stride_tok | kv_stride_head | o_stride_b | o_stride_h) % 8 != 0)
-    return fail(Q3A_EINVAL, "paged_decode: strides must be multiples of 8 elements (16 bytes)");
+    return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out |
+                          (uintptr_t)k_new | (uintptr_t)v_new;
+  if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: q/k_cache/v_cache/out/k_new/v_new must be 16-byte aligned", who);
+  if ((q_stride_b | q_stride_h | kv_stride_page | kv_stride_tok | kv_stride_head | o_stride_b | o_stride_h |
+       kn_stride_b | vn_stride_b) % 8 != 0)
+    return fail(Q3A_EINVAL, "%s: strides must be multiples of 8 elements (16 bytes)", who);
   if (split_tokens < 0 || split_tokens % kTile != 0)
-    return fail(Q3A_EINVAL, "paged_decode: split_tokens %d is not 0 or a positive multiple of %d", split_tokens, kTile);
+    return fail(Q3A_EINVAL, "%s: split_tokens %d is not 0 or a positive multiple of %d", who, split_tokens, kTile);
   if (split_tokens > kMaxSplitTokens)
-    return fail(Q3A_EINVAL, "paged_decode: split_tokens %d exceeds %d", split_tokens, kMaxSplitTokens);
+    return fail(Q3A_EINVAL, "%s: split_tokens %d exceeds %d", who, split_tokens, kMaxSplitTokens);
   const int64_t page_extent =
       ((int64_t)(page_size - 1) * kv_stride_tok + (int64_t)(num_kv_heads - 1) * kv_stride_head + head_dim) * 2;
   if (kv_stride_tok <= 0 || kv_stride_head <= 0 || page_extent >= ((int64_t)1 << 31))
-    return fail(Q3A_EINVAL, "paged_decode: page extent %lld bytes unsupported (need positive strides, < 2 GiB)",
+    return fail(Q3A_EINVAL, "%s: page extent %lld bytes unsupported (need positive strides, < 2 GiB)", who,
                 (long long)page_extent);
   const int64_t max_ctx = (int64_t)max_pages_per_seq * page_size;
-  if (max_ctx > (int64_t)1 << 30) return fail(Q3A_EINVAL, "paged_decode: context capacity too large");
+  if (max_ctx > (int64_t)1 << 30) return fail(Q3A_EINVAL, "%s: context capacity too large", who);
   const bool sk = use_sk(batch, split_tokens);
   if (!sk && split_tokens == 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
   const int max_splits = sk ? 0 : ceil_div(max_ctx, split_tokens);
   if (!sk && max_splits > kMaxSplits)
-    return fail(Q3A_EINVAL, "paged_decode: %d splits exceed %d (raise split_tokens)", max_splits, kMaxSplits);
+    return fail(Q3A_EINVAL, "%s: %d splits exceed %d (raise split_tokens)", who, max_splits, kMaxSplits);
   const size_t need = workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, sk ? 0 : split_tokens);
   if (need > 0 && (workspace == nullptr || workspace_bytes_ < need))
-    return fail(Q3A_ESPACE, "paged_decode: workspace %zu bytes < %zu needed", workspace_bytes_, need);
+    return fail(Q3A_ESPACE, "%s: workspace %zu bytes < %zu needed", who, workspace_bytes_, need);
   if (need > 0 && (uintptr_t)workspace % 16 != 0)
-    return fail(Q3A_EINVAL, "paged_decode: workspace must be 16-byte aligned");
+    return fail(Q3A_EINVAL, "%s: workspace must be 16-byte aligned", who);
 
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -678,6 +784,10 @@ extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   a.kv_sp = kv_stride_page;
   a.kv_st = kv_stride_tok;
   a.kv_sh = kv_stride_head;
+  a.k_new = static_cast<const uint16_t*>(k_new);
+  a.v_new = static_cast<const uint16_t*>(v_new);
+  a.kn_sb = kn_stride_b;
+  a.vn_sb = vn_stride_b;
   a.num_pages = num_pages;
   a.page_size = page_size;
   a.page_bytes = (uint32_t)page_extent;
@@ -698,27 +808,68 @@ extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   const dim3 block(64 * num_kv_heads);
   hipError_t e;
   if (sk) {
-    a.grid = sk_grid(num_kv_heads);
+    a.grid = sk_grid_of(num_kv_heads, append);
     a.prefix = static_cast<int*>(workspace);
     a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256((size_t)(batch + 1) * sizeof(int)));
-    hipLaunchKernelGGL(paged_decode_sk_kernel, dim3(a.grid), block, 0, st, a);
+    if (append)
+      hipLaunchKernelGGL(paged_decode_sk_kernel<true>, dim3(a.grid), block, 0, st, a);
+    else
+      hipLaunchKernelGGL(paged_decode_sk_kernel<false>, dim3(a.grid), block, 0, st, a);
     e = hipGetLastError();
-    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: stream-K launch failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: stream-K launch failed: %s", who, hipGetErrorString(e));
     hipLaunchKernelGGL(paged_decode_sk_combine_kernel, dim3(batch), block, 0, st, a);
     e = hipGetLastError();
-    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: combine launch failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: combine launch failed: %s", who, hipGetErrorString(e));
     return Q3A_OK;
   }
   a.grid = 0;
   a.prefix = nullptr;
   a.ws = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(paged_decode_split_kernel, dim3(batch, max_splits), block, 0, st, a);
+  if (append)
+    hipLaunchKernelGGL(paged_decode_split_kernel<true>, dim3(batch, max_splits), block, 0, st, a);
+  else
+    hipLaunchKernelGGL(paged_decode_split_kernel<false>, dim3(batch, max_splits), block, 0, st, a);
   e = hipGetLastError();
-  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: split launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: split launch failed: %s", who, hipGetErrorString(e));
   if (max_splits > 1) {
-    hipLaunchKernelGGL(paged_decode_split_combine_kernel, dim3(batch), block, 0, st, a);
+    if (append)
+      hipLaunchKernelGGL(paged_decode_split_combine_kernel<true>, dim3(batch), block, 0, st, a);
+    else
+      hipLaunchKernelGGL(paged_decode_split_combine_kernel<false>, dim3(batch), block, 0, st, a);
     e = hipGetLastError();
-    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "paged_decode: combine launch failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: combine launch failed: %s", who, hipGetErrorString(e));
   }
   return Q3A_OK;
+}
+
+extern "C" int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_cache, const void* v_cache, int64_t kv_stride_page,
+                                int64_t kv_stride_tok, int64_t kv_stride_head, int num_pages,
+                                int page_size, const int32_t* cache_seqlens,
+                                const int32_t* block_table, int64_t bt_stride_b,
+                                int max_pages_per_seq, void* out, int64_t o_stride_b,
+                                int64_t o_stride_h, void* workspace, size_t workspace_bytes_,
+                                int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                float softmax_scale, int split_tokens, void* stream) {
+  return launch_decode(q, q_stride_b, q_stride_h, nullptr, 0, nullptr, 0, k_cache, v_cache, kv_stride_page,
+                       kv_stride_tok, kv_stride_head, num_pages, page_size, cache_seqlens, block_table, bt_stride_b,
+                       max_pages_per_seq, out, o_stride_b, o_stride_h, workspace, workspace_bytes_, batch,
+                       num_q_heads, num_kv_heads, head_dim, softmax_scale, split_tokens, stream, "paged_decode");
+}
+
+extern "C" int q3a_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                       const void* k_new, int64_t kn_stride_b, const void* v_new,
+                                       int64_t vn_stride_b, void* k_cache, void* v_cache,
+                                       int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head,
+                                       int num_pages, int page_size, const int32_t* cache_seqlens,
+                                       const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq,
+                                       void* out, int64_t o_stride_b, int64_t o_stride_h, void* workspace,
+                                       size_t workspace_bytes_, int batch, int num_q_heads, int num_kv_heads,
+                                       int head_dim, float softmax_scale, int split_tokens, void* stream) {
+  if (!k_new || !v_new) return fail(Q3A_EINVAL, "paged_decode_append: null k_new/v_new");
+  return launch_decode(q, q_stride_b, q_stride_h, k_new, kn_stride_b, v_new, vn_stride_b, k_cache, v_cache,
+                       kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, cache_seqlens,
+                       block_table, bt_stride_b, max_pages_per_seq, out, o_stride_b, o_stride_h, workspace,
+                       workspace_bytes_, batch, num_q_heads, num_kv_heads, head_dim, softmax_scale, split_tokens,
+                       stream, "paged_decode_append");
 }

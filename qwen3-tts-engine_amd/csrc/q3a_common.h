@@ -57,6 +57,17 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
 }
 
+// Uniform part of the offset in an SGPR (soffset), per-lane part in a VGPR.
+__device__ __forceinline__ uint4 buffer_load16_s(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint32_t s_off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, (int)s_off, 0));
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void buffer_store16_s(uint4 v, __amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                                 uint32_t s_off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)byte_off, (int)s_off, 0);
+}
+
 // Streaming variant with the non-temporal hint (`nt`): data read exactly once (the K/V pages of a
 // decode call) bypasses cache retention, which measured ~12% more HBM read bandwidth on MI355X
 // than plain loads for the same access pattern.

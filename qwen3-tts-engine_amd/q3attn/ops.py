@@ -88,6 +88,60 @@ def _paged_decode_fake(q, k_cache, v_cache, cache_seqlens, block_table, softmax_
     return q.new_empty(q.shape)
 
 
+def _new_rows(x, B, Hkv, D, name):
+    """k/v of this step as [B, Hkv, D] with packed heads: accepts [B, Hkv, D], [B, 1, Hkv, D] or [B, Hkv*D]
+    views (e.g. the v slice of a fused qkv projection)."""
+    if x.dim() == 4:
+        _req(x.shape[1] == 1, f"q3attn.paged_decode_append: {name} must hold one new token per row")
+        x = x[:, 0]
+    elif x.dim() == 2:
+        x = x.view(x.shape[0], Hkv, D)
+    _req(x.dtype == torch.bfloat16, f"q3attn.paged_decode_append: {name} must be bfloat16")
+    _req(tuple(x.shape) == (B, Hkv, D), f"q3attn.paged_decode_append: {name} must be [B, {Hkv}, {D}]")
+    _req(x.stride(2) == 1 and x.stride(1) == D, f"q3attn.paged_decode_append: {name} heads must be packed")
+    return x
+
+
+@torch.library.custom_op("q3attn::paged_decode_append", mutates_args=("k_cache", "v_cache"))
+def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                        v_cache: torch.Tensor, cache_seqlens: torch.Tensor, block_table: torch.Tensor,
+                        softmax_scale: float, split_tokens: int = 0) -> torch.Tensor:
+    """Append + attend in one pass: writes k[b], v[b] at position p = cache_seqlens[b] of row b (page
+    block_table[b][p // page], offset p % page) and returns the attention of q[b] over tokens 0..p
+    (engine/talker.py:72-73 then :77).  Rows with cache_seqlens < 0 give zeros and write nothing."""
+    _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table)
+    B, Hq, D = q.shape
+    num_pages, page, Hkv, _ = k_cache.shape
+    _req(k.device == q.device and v.device == q.device, "q3attn.paged_decode_append: k, v must be on q's device")
+    k3 = _new_rows(k, B, Hkv, D, "k")
+    v3 = _new_rows(v, B, Hkv, D, "v")
+    max_pages = block_table.shape[1]
+    out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    if B == 0:
+        return out
+    L = lib()
+    split = int(split_tokens)
+    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    rc = L.q3a_paged_decode_append(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k3.data_ptr(), k3.stride(0), v3.data_ptr(), v3.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        num_pages, page,
+        cache_seqlens.data_ptr(), block_table.data_ptr(), block_table.stride(0), max_pages,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), ws_bytes,
+        B, Hq, Hkv, D, float(softmax_scale), split, _stream(q.device))
+    check(rc, "q3a_paged_decode_append")
+    return out
+
+
+@paged_decode_append.register_fake
+def _paged_decode_append_fake(q, k, v, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
+                              split_tokens=0):
+    return q.new_empty(q.shape)
+
+
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
                             cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None,
                             block_table=None, softmax_scale=None, causal=False, window_size=(-1, -1),
@@ -96,8 +150,15 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
     """Drop-in for the paged-decode subset of ``flash_attn.flash_attn_with_kvcache`` that the talker
     calls (engine/talker.py:77): q [B, 1, Hq, D], paged caches, int32 ``cache_seqlens`` and
     ``block_table``, ``softmax_scale``, ``causal`` (a no-op for one query token).  Returns
-    [B, 1, Hq, D].  Arguments the talker does not use raise NotImplementedError."""
-    unsupported = {"k": k, "v": v, "rotary_cos": rotary_cos, "rotary_sin": rotary_sin,
+    [B, 1, Hq, D].
+
+    With ``k``/``v`` ([B, 1, Hkv, D], one new token per row) the flash-attn append semantics apply:
+    the new token is written into the caches at position ``cache_seqlens[b]`` and attention runs over
+    ``cache_seqlens[b] + 1`` tokens, in one pass (replacing engine/talker.py:72-73 + :77);
+    ``cache_seqlens`` itself is not updated.  Arguments the talker does not use raise
+    NotImplementedError."""
+    _req((k is None) == (v is None), "q3attn.flash_attn_with_kvcache: pass both k and v, or neither")
+    unsupported = {"rotary_cos": rotary_cos, "rotary_sin": rotary_sin,
                    "cache_batch_idx": cache_batch_idx, "cache_leftpad": cache_leftpad,
                    "alibi_slopes": alibi_slopes}
     for name, val in unsupported.items():
@@ -116,5 +177,11 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
     if num_splits and num_splits > 0:
         max_ctx = block_table.shape[1] * k_cache.shape[1]
         split = max(16, 16 * math.ceil(math.ceil(max_ctx / num_splits) / 16))
-    o = paged_decode(q[:, 0], k_cache, v_cache, cache_seqlens, block_table, float(scale), split)
+    if k is not None:
+        _req(k.dim() == 4 and k.shape[1] == 1 and v.dim() == 4 and v.shape[1] == 1,
+             "q3attn.flash_attn_with_kvcache: k/v must be [batch, 1, kv_heads, head_dim]")
+        o = paged_decode_append(q[:, 0], k[:, 0], v[:, 0], k_cache, v_cache, cache_seqlens, block_table,
+                                float(scale), split)
+    else:
+        o = paged_decode(q[:, 0], k_cache, v_cache, cache_seqlens, block_table, float(scale), split)
     return o.unsqueeze(1)

@@ -128,9 +128,32 @@ def test_python_entry_points_refuse_cpu_tensors():
 def test_unsupported_flash_attn_arguments_raise():
     q = torch.zeros(2, 1, 16, 128, dtype=torch.bfloat16)
     kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16)
+    kw = dict(cache_seqlens=torch.ones(2, dtype=torch.int32), block_table=torch.zeros(2, 2, dtype=torch.int32))
     with pytest.raises(NotImplementedError):
-        q3attn.flash_attn_with_kvcache(q, kc, kc, k=q, cache_seqlens=torch.ones(2, dtype=torch.int32),
-                                       block_table=torch.zeros(2, 2, dtype=torch.int32))
+        q3attn.flash_attn_with_kvcache(q, kc, kc, rotary_cos=q, **kw)
+    with pytest.raises(NotImplementedError):
+        q3attn.flash_attn_with_kvcache(q, kc, kc, window_size=(8, 0), **kw)
+    with pytest.raises(RuntimeError, match="both k and v"):
+        q3attn.flash_attn_with_kvcache(q, kc, kc, k=q, **kw)
+    with pytest.raises(RuntimeError, match="GPU"):
+        q3attn.flash_attn_with_kvcache(q, kc, kc, k=torch.zeros(2, 1, 8, 128, dtype=torch.bfloat16),
+                                       v=torch.zeros(2, 1, 8, 128, dtype=torch.bfloat16), **kw)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(kn=None), "k_new"), (dict(vn=None), "k_new"), (dict(kn=18), "aligned"), (dict(vn_sb=1030), "strides"),
+    (dict(page=24), "page_size"), (dict(Hq=8), "num_q_heads"),
+])
+def test_paged_decode_append_rejects_bad_arguments(kw, frag):
+    a = dict(q=16, q_sb=2048, q_sh=128, kn=16, kn_sb=1024, vn=16, vn_sb=4096, k=16, v=16, sp=16384, st=1024,
+             sh=128, num_pages=8, page=16, seqlens=16, bt=16, bt_sb=4, max_pages=4, out=16, o_sb=2048, o_sh=128,
+             ws=16, ws_bytes=1 << 30, B=2, Hq=16, Hkv=8, D=128, scale=0.088, split=0)
+    a.update(kw)
+    rc = _lib.lib().q3a_paged_decode_append(
+        a["q"], a["q_sb"], a["q_sh"], a["kn"], a["kn_sb"], a["vn"], a["vn_sb"], a["k"], a["v"], a["sp"], a["st"],
+        a["sh"], a["num_pages"], a["page"], a["seqlens"], a["bt"], a["bt_sb"], a["max_pages"], a["out"], a["o_sb"],
+        a["o_sh"], a["ws"], a["ws_bytes"], a["B"], a["Hq"], a["Hkv"], a["D"], a["scale"], a["split"], None)
+    assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
 
 
 def test_fake_impl_traces_shapes():
@@ -143,6 +166,10 @@ def test_fake_impl_traces_shapes():
         o = torch.ops.q3attn.paged_decode(q, kc, kc, torch.empty(3, dtype=torch.int32),
                                           torch.empty(3, 4, dtype=torch.int32), 0.1, 0)
         assert o.shape == (3, 16, 128) and o.dtype == torch.bfloat16
+        kv = torch.empty(3, 8, 128, dtype=torch.bfloat16)
+        o = torch.ops.q3attn.paged_decode_append(q, kv, kv, kc, kc, torch.empty(3, dtype=torch.int32),
+                                                 torch.empty(3, 4, dtype=torch.int32), 0.1, 0)
+        assert o.shape == (3, 16, 128)
         c = torch.ops.q3attn.cp_attn(q, torch.empty(3, 8, 16, 128, dtype=torch.bfloat16),
                                      torch.empty(3, 8, 16, 128, dtype=torch.bfloat16), 4, 0.1)
         assert c.shape == (3, 2048)
