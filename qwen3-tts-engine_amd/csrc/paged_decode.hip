@@ -464,11 +464,11 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
   float* part = a.ws + (int64_t)blockIdx.x * kSkSlots * a.hkv * kPartFloats;
 
-  uint4 q[kG];
+  uint4 q[kG], q_next[kG];
   float m[kG], l[kG], acc[kG][8];
   reset_state(m, l, acc);
   int seg_row = 0, seg_flags = 0, seg_slot = 0;
-  q[0] = q[1] = make_uint4(0u, 0u, 0u, 0u);
+  q[0] = q[1] = q_next[0] = q_next[1] = make_uint4(0u, 0u, 0u, 0u);
 
   for (int cb = lo; cb < hi; cb += 64) {
     TileList L;
@@ -497,8 +497,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
                (mt == 0 ? kRowStart : 0) | (mt == ntr - 1 ? kRowEnd : 0);
     }
 
-    // Segment bookkeeping for tile j, run before tile j+1 is issued: the q loads of a new segment then
-    // precede that prefetch, so consuming tile j waits for tile j's loads and q only, never for j+1's.
+    // Segment bookkeeping for tile j, run before tile j+1 is issued.  A segment's q was loaded into
+    // q_next together with its first tile (see issue), so opening it costs no extra wait.
     auto open_segment = [&](int j) {
       const int fl = readlane(vflags, j);
       if (fl & kFirst) {
@@ -506,7 +506,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         seg_flags = fl;
         seg_slot = (cb + j == lo) ? 0 : 1;
         reset_state(m, l, acc);
-        load_q(a, seg_row, g, dl, q);
+        q[0] = q_next[0];
+        q[1] = q_next[1];
       }
     };
     auto process = [&](KVTile& T, int j) {
@@ -528,6 +529,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
 
     auto issue = [&](int j, KVTile& T) {
       issue_tile(a, L, lane_off, grp, j, T);
+      if (j < L.n && (readlane(vflags, j) & kFirst)) load_q(a, readlane(vrow, j), g, dl, q_next);
       // Keep the whole tile's loads ahead of the consumer: no instruction of the next tile_update may
       // be scheduled between them (that would wait for the current tile in the middle of the issue).
       __builtin_amdgcn_sched_barrier(0);
