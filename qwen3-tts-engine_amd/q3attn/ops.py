@@ -178,8 +178,9 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
         max_ctx = block_table.shape[1] * k_cache.shape[1]
         split = max(16, 16 * math.ceil(math.ceil(max_ctx / num_splits) / 16))
     if k is not None:
-        _req(k.dim() == 4 and k.shape[1] == 1 and v.dim() == 4 and v.shape[1] == 1,
-             "q3attn.flash_attn_with_kvcache: k/v must be [batch, 1, kv_heads, head_dim]")
+        _req(k.dim() == 4 and v.dim() == 4, "q3attn.flash_attn_with_kvcache: k/v must be [batch, new, kv_heads, head_dim]")
+        if k.shape[1] != 1 or v.shape[1] != 1:
+            raise NotImplementedError("q3attn.flash_attn_with_kvcache: one new token per row is supported")
         o = paged_decode_append(q[:, 0], k[:, 0], v[:, 0], k_cache, v_cache, cache_seqlens, block_table,
                                 float(scale), split)
     else:
