@@ -54,6 +54,12 @@ struct PrefillArgs {
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+__device__ __forceinline__ int readlane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+// V^T tile swizzle: key k of dim row r is stored at column k ^ vswz(r).  It moves whole 4-key quads (bits 2-5
+// of k), so 8-byte reads of 4 consecutive keys stay contiguous; with the 72-element row stride it makes both
+// the transposed stores (16 rows x 4 quads per wave) and the MFMA operand reads free of LDS bank conflicts.
+__device__ __forceinline__ int vswz(int r) { return (((r >> 3) & 3) << 2) ^ (((r >> 5) & 3) << 4); }
 
 __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   __shared__ __align__(16) uint16_t Ks[kKT * kKs];
@@ -63,7 +69,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int qt = gridDim.y - 1 - blockIdx.y;  // longest query tiles dispatch first
   const int g = blockIdx.z;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int col = lane & 15;
   const int g4 = lane >> 4;
@@ -86,7 +92,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     uint4 x = make_uint4(0u, 0u, 0u, 0u);
-    if (qvalid) x = *reinterpret_cast<const uint4*>(a.q + (int64_t)(q0 + tq) * a.q_st + h * a.q_sh + 32 * kk + 8 * g4);
+    if (qvalid) x = ld16(a.q + (int64_t)(q0 + tq) * a.q_st + h * a.q_sh + 32 * kk + 8 * g4);
     qb[kk] = as_bf16x8(x);
   }
 
@@ -98,58 +104,62 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int ntiles = kend > 0 ? (kend + kKT - 1) / kKT : 0;
   const int jlim = a.causal ? min(Lk - 1, qpos) : Lk - 1;  // last key this lane's token sees
 
-  // Cooperative tile loads: K chunk (key (tid>>4) + 16r, dims 8*(tid&15)); V keys 4*(tid&15)+r (one
-  // page: pages hold a multiple of 16 tokens), dims 8*(tid>>4).  The page indices of a tile are all
-  // fetched before any K/V load is issued, so a tile costs two memory round trips, not one per key.
+  // Tile loads.  A 64-key tile is 4 groups of 16 keys and a group never straddles a page (page sizes are
+  // powers of two >= 16), so each group has one uniform base address: all K/V loads are raw buffer loads
+  // against a descriptor covering exactly the group's valid rows of head g (rows past the sequence, and
+  // groups on an invalid page, read as zeros without touching memory).  No per-lane address math.
+  //   K: thread t loads key 16r + (t >> 4), dims 8 (t & 15), for r = 0..3.
+  //   V: wave w loads group w: keys 16w + 4((t >> 4) & 3) + b, b = 0..3, dims 8 (t & 15): each thread
+  //      holds 4 consecutive keys x 8 dims, the shape of its transposed LDS store.
+  // Page ids come from a lane-wise window (lane i = table entry pwin_base + i), read with v_readlane, so
+  // a tile costs one memory round trip; the window is refilled once per 64 pages.
+  const bool paged = a.bt != nullptr;
   const int64_t bt_row = (int64_t)s * a.bt_sb;
-  uint4 kr[4], vr[4];
-  auto load_tile = [&](int t) {
-    const int kb = t * kKT;
-    const int jv = kb + 4 * (tid & 15);
-    int64_t krow[4], vrow;
-    if (a.bt != nullptr) {
-      int pk[4], pv = -1;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int jk = kb + (tid >> 4) + 16 * r;
-        pk[r] = jk < Lk ? a.bt[bt_row + (jk >> a.page_shift)] : -1;
-      }
-      if (jv < Lk) pv = a.bt[bt_row + (jv >> a.page_shift)];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int jk = kb + (tid >> 4) + 16 * r;
-        krow[r] = (unsigned)pk[r] < (unsigned)a.num_pages
-                      ? (int64_t)pk[r] * a.kv_sp + (int64_t)(jk & (a.page_size - 1)) * a.kv_st : -1;
-      }
-      vrow = (unsigned)pv < (unsigned)a.num_pages
-                 ? (int64_t)pv * a.kv_sp + (int64_t)(jv & (a.page_size - 1)) * a.kv_st : -1;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int jk = kb + (tid >> 4) + 16 * r;
-        krow[r] = jk < Lk ? (int64_t)(k0 + jk) * a.kv_st : -1;
-      }
-      vrow = jv < Lk ? (int64_t)(k0 + jv) * a.kv_st : -1;
-    }
-    // K rows of keys outside the sequence (or on an invalid page) read row 0 of the buffer instead: their
-    // scores are masked to -inf, so the values never matter and the loads need no branch.
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      kr[r] = *reinterpret_cast<const uint4*>(a.k + (krow[r] >= 0 ? krow[r] : 0) + g * a.kv_sh + 8 * (tid & 15));
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      vr[r] = make_uint4(0u, 0u, 0u, 0u);
-      if (vrow >= 0 && jv + r < Lk)
-        vr[r] = *reinterpret_cast<const uint4*>(a.v + vrow + (int64_t)r * a.kv_st + g * a.kv_sh + 8 * (tid >> 4));
-    }
+  int pwin = -1, pwin_base = 0;
+  auto load_window = [&](int base) __attribute__((always_inline)) {
+    pwin_base = base;
+    const int i = base + lane;
+    pwin = (paged && i < a.max_pages) ? a.bt[bt_row + i] : -1;
   };
-  auto store_tile = [&]() {
+  if (paged) load_window(0);
+
+  auto group_rsrc = [&](const uint16_t* base, int t, int r) __attribute__((always_inline)) {
+    const int j0 = t * kKT + 16 * r;
+    const int nv = min(16, Lk - j0);
+    bool ok = nv > 0;
+    int64_t off = 0;
+    if (paged) {
+      const int page = readlane(pwin, (j0 >> a.page_shift) - pwin_base);
+      ok = ok && (unsigned)page < (unsigned)a.num_pages;
+      off = (int64_t)page * a.kv_sp + (int64_t)(j0 & (a.page_size - 1)) * a.kv_st;
+    } else {
+      off = (int64_t)(k0 + j0) * a.kv_st;
+    }
+    return make_rsrc(base + (ok ? off : 0) + (int64_t)g * a.kv_sh, ok ? (uint32_t)(((nv - 1) * a.kv_st + kD) * 2) : 0u);
+  };
+
+  const uint32_t k_off = (uint32_t)(((tid >> 4) * a.kv_st + 8 * (tid & 15)) * 2);
+  const uint32_t v_off = (uint32_t)((4 * ((tid >> 4) & 3) * a.kv_st + 8 * (tid & 15)) * 2);
+  const uint32_t tok_bytes = (uint32_t)(a.kv_st * 2);
+  uint4 kr[4], vr[4];
+  auto load_tile = [&](int t) __attribute__((always_inline)) {
+    if (paged) {
+      const int pf = (t * kKT) >> a.page_shift;
+      const int pl = (t * kKT + kKT - 1) >> a.page_shift;
+      if (pf < pwin_base || pl >= pwin_base + 64) load_window(pf);
+    }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<uint4*>(&Ks[((tid >> 4) + 16 * r) * kKs + 8 * (tid & 15)]) = kr[r];
+    for (int r = 0; r < 4; ++r) kr[r] = buffer_load16(group_rsrc(a.k, t, r), k_off);
+    const __amdgpu_buffer_rsrc_t rv = group_rsrc(a.v, t, wave);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) vr[b] = buffer_load16(rv, v_off + b * tok_bytes);
+  };
+  auto store_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) st16(&Ks[((tid >> 4) + 16 * r) * kKs + 8 * (tid & 15)], kr[r]);
     // V transposed: for each of this thread's 8 dims, its 4 keys as one 8-byte row segment.
-    const int kq = 4 * (tid & 15);
-    const int d0 = 8 * (tid >> 4);
+    const int kq = 16 * wave + 4 * ((tid >> 4) & 3);
+    const int d0 = 8 * (tid & 15);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const uint32_t w0 = c == 0 ? vr[0].x : c == 1 ? vr[0].y : c == 2 ? vr[0].z : vr[0].w;
@@ -161,8 +171,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       lo.y = perm_b32(w3, w2, kPermLoLo);
       hi.x = perm_b32(w1, w0, kPermHiHi);
       hi.y = perm_b32(w3, w2, kPermHiHi);
-      *reinterpret_cast<uint2*>(&Vt[(d0 + 2 * c) * kVs + kq]) = lo;
-      *reinterpret_cast<uint2*>(&Vt[(d0 + 2 * c + 1) * kVs + kq]) = hi;
+      const int r0 = d0 + 2 * c;
+      *reinterpret_cast<uint2*>(&Vt[r0 * kVs + (kq ^ vswz(r0))]) = lo;
+      *reinterpret_cast<uint2*>(&Vt[(r0 + 1) * kVs + (kq ^ vswz(r0 + 1))]) = hi;
     }
   };
 
@@ -185,7 +196,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       st[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const uint4 kv = *reinterpret_cast<const uint4*>(&Ks[(kb * 16 + col) * kKs + 32 * kk + 8 * g4]);
+        const uint4 kv = ld16(&Ks[(kb * 16 + col) * kKs + 32 * kk + 8 * g4]);
         st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv), qb[kk], st[kb], 0, 0, 0);
       }
     }
@@ -246,9 +257,11 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     for (int db = 0; db < 8; ++db) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const uint16_t* vrow = &Vt[(db * 16 + col) * kVs + 32 * s2 + 4 * g4];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
+        const int vr_row = db * 16 + col;
+        const uint16_t* vrow = &Vt[vr_row * kVs];
+        const int sw = vswz(vr_row);
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + ((32 * s2 + 4 * g4) ^ sw));
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + ((32 * s2 + 4 * g4 + 16) ^ sw));
         acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb[s2],
                                                           acc[db], 0, 0, 0);
       }
@@ -293,6 +306,9 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
   if (align % 16 != 0) return fail(Q3A_EINVAL, "prefill: q/k/v/out must be 16-byte aligned");
   if ((q_stride_t | q_stride_h | kv_stride_tok | kv_stride_head | o_stride_t | o_stride_h) % 8 != 0)
     return fail(Q3A_EINVAL, "prefill: strides must be multiples of 8 elements (16 bytes)");
+  if (kv_stride_tok < head_dim || kv_stride_head < 0 || kv_stride_tok > ((int64_t)1 << 26))
+    return fail(Q3A_EINVAL, "prefill: token stride %lld must be in [head_dim, 2^26] and head stride >= 0",
+                (long long)kv_stride_tok);
   if (block_table != nullptr) {
     if (page_size <= 0 || num_pages <= 0 || max_pages_per_seq <= 0)
       return fail(Q3A_EINVAL, "prefill: paged K/V needs page_size, num_pages and max_pages_per_seq > 0");
