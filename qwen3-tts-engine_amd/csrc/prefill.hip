@@ -9,12 +9,12 @@
 // of flash_attn_func at engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131), and both
 // read from the pool after the K/V append (engine/talker.py:161-162, engine/arrivals.py:144-145).
 //
-// Work: one workgroup (4 waves) per (sequence, 32-query tile, KV head); wave w takes query head
-// 2g + (w & 1) and tokens 16*(w >> 1)..+16 of the tile, so the workgroup's 64 MFMA rows are the two
-// query heads of the GQA pair over 32 tokens and every K/V tile staged in LDS serves both heads.
-// Key tiles of 64 are staged in LDS (K row-major, V transposed); the next tile is prefetched into
-// registers while the current one is consumed.  v_mfma_f32_16x16x32_bf16 layouts: A lane l = row
-// l%16, k 8*(l/16)..+8; B lane l = column l%16, same k; C lane l = column l%16, rows 4*(l/16)..+4.
+// Work: one workgroup (4 waves) per (sequence, 64-query tile, KV head); wave w takes tokens 16w..16w+15 of
+// the tile for BOTH query heads 2g, 2g+1 of the GQA pair, so every K or V^T operand read from LDS feeds two
+// MFMAs.  Key tiles of 64 are staged in LDS (K row-major with padding, V transposed and swizzled); the next
+// tile is prefetched into registers while the current one is consumed.  v_mfma_f32_16x16x32_bf16 layouts:
+// A lane l = row l%16, k 8*(l/16)..+8; B lane l = column l%16, same k; C lane l = column l%16, rows
+// 4*(l/16)..+4.
 //   S^T = K Q^T  : A = K (rows = keys), B = Q^T (columns = this lane's query token)
 //   O^T = V^T P^T: A = V^T from LDS, B = P^T taken straight from S^T's C registers
 // so the softmax statistics, P and the O accumulators of a query token all live on the lanes with
@@ -27,7 +27,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kG = 2;
-constexpr int kQT = 32;        // query tokens per workgroup
+constexpr int kQT = 64;        // query tokens per workgroup (16 per wave, both heads)
 constexpr int kKT = 64;        // keys per LDS tile
 constexpr int kKs = kD + 8;    // K tile row stride in LDS (bf16 elements, padded)
 constexpr int kVs = kKT + 8;   // V^T tile row stride in LDS (bf16 elements, padded)
@@ -65,14 +65,28 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   __shared__ __align__(16) uint16_t Ks[kKT * kKs];
   __shared__ __align__(16) uint16_t Vt[kD * kVs];
 
+  // Grid (sequence, KV head, query tile) with the query tile slowest and reversed: the tiles with the most
+  // key tiles (the last ones of each sequence) dispatch first for every head, the short ones fill in last.
   const int s = blockIdx.x;
-  const int qt = gridDim.y - 1 - blockIdx.y;  // longest query tiles dispatch first
-  const int g = blockIdx.z;
+  const int g = blockIdx.y;
+  const int qt = gridDim.z - 1 - blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int col = lane & 15;
   const int g4 = lane >> 4;
+
+  // The sequence's first 64 page ids depend only on s: fetch them before cu_seqlens so the first tile's
+  // loads wait for one memory round trip, not two.
+  const bool paged = a.bt != nullptr;
+  const int64_t bt_row = (int64_t)s * a.bt_sb;
+  int pwin = -1, pwin_base = 0;
+  auto load_window = [&](int base) __attribute__((always_inline)) {
+    pwin_base = base;
+    const int i = base + lane;
+    pwin = (paged && i < a.max_pages) ? a.bt[bt_row + i] : -1;
+  };
+  if (paged) load_window(0);
 
   const int q0 = a.cu_q[s];
   const int Lq = a.cu_q[s + 1] - q0;
@@ -82,18 +96,20 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   if (a.bt != nullptr) Lk = min(Lk, a.max_pages * a.page_size);
   Lk = max(Lk, 0);
 
-  const int h = kG * g + (wave & 1);
-  const int tq = qt * kQT + (wave >> 1) * 16 + col;  // this lane's query token
+  const int tq = qt * kQT + wave * 16 + col;  // this lane's query token
   const bool qvalid = tq < Lq;
-  const int qpos = Lk - Lq + tq;                       // last key this token may see when causal
+  const int qpos = Lk - Lq + tq;              // last key this token may see when causal
 
-  // Q^T as the B operand of S^T = K Q^T: 4 chunks of 32 dims.
-  bf16x8_t qb[4];
+  // Q^T of both heads as B operands of S^T = K Q^T: 4 chunks of 32 dims each.
+  bf16x8_t qb[kG][4];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    uint4 x = make_uint4(0u, 0u, 0u, 0u);
-    if (qvalid) x = ld16(a.q + (int64_t)(q0 + tq) * a.q_st + h * a.q_sh + 32 * kk + 8 * g4);
-    qb[kk] = as_bf16x8(x);
+  for (int hh = 0; hh < kG; ++hh) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint4 x = make_uint4(0u, 0u, 0u, 0u);
+      if (qvalid) x = ld16(a.q + (int64_t)(q0 + tq) * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
+      qb[hh][kk] = as_bf16x8(x);
+    }
   }
 
   int kend = Lk;
@@ -113,16 +129,6 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   //      holds 4 consecutive keys x 8 dims, the shape of its transposed LDS store.
   // Page ids come from a lane-wise window (lane i = table entry pwin_base + i), read with v_readlane, so
   // a tile costs one memory round trip; the window is refilled once per 64 pages.
-  const bool paged = a.bt != nullptr;
-  const int64_t bt_row = (int64_t)s * a.bt_sb;
-  int pwin = -1, pwin_base = 0;
-  auto load_window = [&](int base) __attribute__((always_inline)) {
-    pwin_base = base;
-    const int i = base + lane;
-    pwin = (paged && i < a.max_pages) ? a.bt[bt_row + i] : -1;
-  };
-  if (paged) load_window(0);
-
   auto group_rsrc = [&](const uint16_t* base, int t, int r) __attribute__((always_inline)) {
     const int j0 = t * kKT + 16 * r;
     const int nv = min(16, Lk - j0);
@@ -177,10 +183,12 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     }
   };
 
-  f32x4_t acc[8];
+  f32x4_t acc[kG][8];
 #pragma unroll
-  for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m = kMaxSeed, l = 0.f;
+  for (int hh = 0; hh < kG; ++hh)
+#pragma unroll
+    for (int db = 0; db < 8; ++db) acc[hh][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m[kG] = {kMaxSeed, kMaxSeed}, l[kG] = {0.f, 0.f};
 
   if (ntiles > 0) load_tile(0);
   for (int t = 0; t < ntiles; ++t) {
@@ -189,97 +197,110 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     __syncthreads();
     if (t + 1 < ntiles) load_tile(t + 1);
 
-    // S^T for the tile's 4 blocks of 16 keys.
-    f32x4_t st[4];
+    // S^T for the tile's 4 blocks of 16 keys, both heads; each K operand is read once.
+    f32x4_t st[kG][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      st[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int hh = 0; hh < kG; ++hh) st[hh][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const uint4 kv = ld16(&Ks[(kb * 16 + col) * kKs + 32 * kk + 8 * g4]);
-        st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv), qb[kk], st[kb], 0, 0, 0);
+        const bf16x8_t kv = as_bf16x8(ld16(&Ks[(kb * 16 + col) * kKs + 32 * kk + 8 * g4]));
+#pragma unroll
+        for (int hh = 0; hh < kG; ++hh)
+          st[hh][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qb[hh][kk], st[hh][kb], 0, 0, 0);
       }
     }
     // Mask: key j is visible to this lane's token iff j <= jlim (= min(Lk - 1, qpos) when causal).
     // Relative to the tile and this lane's key rows that is one compare per score against `lim`.
     // Masked scores become -inf; the running max m is kept in scaled (log2) units.
     const int lim = jlim - t * kKT - 4 * g4;
-    float mx = -INFINITY;
+    bf16x8_t pb[kG][2];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int hh = 0; hh < kG; ++hh) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        st[kb][i] = (kb * 16 + i <= lim) ? st[kb][i] : -INFINITY;
-        mx = fmaxf(mx, st[kb][i]);
+      for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          st[hh][kb][i] = (kb * 16 + i <= lim) ? st[hh][kb][i] : -INFINITY;
+          mx = fmaxf(mx, st[hh][kb][i]);
+        }
       }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    mx *= a.scale_log2;
-    // Lazy rescale: keep the running max while no token's tile max exceeds it by more than 8 (log2
-    // units), so p = exp2(s * scale - m) <= 256 is exact enough in bf16/fp32 and (l, acc) are rescaled
-    // only when a max grows past that margin.  The first tile always sets the max.
-    if (__any(mx > m + 8.f)) {
-      const float mn = fmaxf(m, mx);
-      const float alpha = fast_exp2(m - mn);
-      l *= alpha;
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx *= a.scale_log2;
+      // Lazy rescale: keep the running max while no token's tile max exceeds it by more than 8 (log2
+      // units), so p = exp2(s * scale - m) <= 256 is exact enough in bf16/fp32 and (l, acc) are rescaled
+      // only when a max grows past that margin.  The first tile always sets the max.
+      if (__any(mx > m[hh] + 8.f)) {
+        const float mn = fmaxf(m[hh], mx);
+        const float alpha = fast_exp2(m[hh] - mn);
+        l[hh] *= alpha;
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        acc[db][0] *= alpha;
-        acc[db][1] *= alpha;
-        acc[db][2] *= alpha;
-        acc[db][3] *= alpha;
+        for (int db = 0; db < 8; ++db) {
+          acc[hh][db][0] *= alpha;
+          acc[hh][db][1] *= alpha;
+          acc[hh][db][2] *= alpha;
+          acc[hh][db][3] *= alpha;
+        }
+        m[hh] = mn;
       }
-      m = mn;
-    }
-    // P^T as the B operand: k slot 8*g4 + i <- key 32*s2 + 4*g4 + i, slot 8*g4 + 4 + i <- key
-    // 32*s2 + 16 + 4*g4 + i (blocks 2*s2 and 2*s2+1 of this lane's C registers).
-    bf16x8_t pb[2];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      float p[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[i] = fast_exp2(fmaf(st[2 * s2][i], a.scale_log2, -m));
-        p[4 + i] = fast_exp2(fmaf(st[2 * s2 + 1][i], a.scale_log2, -m));
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) l += p[i];
-      uint4 w;
-      w.x = pack_bf16x2(p[0], p[1]);
-      w.y = pack_bf16x2(p[2], p[3]);
-      w.z = pack_bf16x2(p[4], p[5]);
-      w.w = pack_bf16x2(p[6], p[7]);
-      pb[s2] = as_bf16x8(w);
-    }
-    // O^T += V^T P^T; V^T rows are dims, the same key order as the B operand.
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
+      // P^T as the B operand: k slot 8*g4 + i <- key 32*s2 + 4*g4 + i, slot 8*g4 + 4 + i <- key
+      // 32*s2 + 16 + 4*g4 + i (blocks 2*s2 and 2*s2+1 of this lane's C registers).
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const int vr_row = db * 16 + col;
-        const uint16_t* vrow = &Vt[vr_row * kVs];
-        const int sw = vswz(vr_row);
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = fast_exp2(fmaf(st[hh][2 * s2][i], a.scale_log2, -m[hh]));
+          p[4 + i] = fast_exp2(fmaf(st[hh][2 * s2 + 1][i], a.scale_log2, -m[hh]));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) l[hh] += p[i];
+        uint4 w;
+        w.x = pack_bf16x2(p[0], p[1]);
+        w.y = pack_bf16x2(p[2], p[3]);
+        w.z = pack_bf16x2(p[4], p[5]);
+        w.w = pack_bf16x2(p[6], p[7]);
+        pb[hh][s2] = as_bf16x8(w);
+      }
+    }
+    // O^T += V^T P^T; V^T rows are dims, the same key order as the B operand; each V^T operand is
+    // read once for both heads.
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int vr_row = db * 16 + col;
+      const uint16_t* vrow = &Vt[vr_row * kVs];
+      const int sw = vswz(vr_row);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
         const uint2 lo = *reinterpret_cast<const uint2*>(vrow + ((32 * s2 + 4 * g4) ^ sw));
         const uint2 hi = *reinterpret_cast<const uint2*>(vrow + ((32 * s2 + 4 * g4 + 16) ^ sw));
-        acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb[s2],
-                                                          acc[db], 0, 0, 0);
+        const bf16x8_t va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+        for (int hh = 0; hh < kG; ++hh)
+          acc[hh][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[hh][s2], acc[hh][db], 0, 0, 0);
       }
     }
   }
 
   // The 4 lanes of a token hold partial sums over disjoint keys.
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (qvalid) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* o = a.out + (int64_t)(q0 + tq) * a.o_st + h * a.o_sh + 4 * g4;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      uint2 w;
-      w.x = pack_bf16x2(acc[db][0] * inv, acc[db][1] * inv);
-      w.y = pack_bf16x2(acc[db][2] * inv, acc[db][3] * inv);
-      *reinterpret_cast<uint2*>(o + db * 16) = w;
+  for (int hh = 0; hh < kG; ++hh) {
+    float lt = l[hh];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    if (qvalid) {
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      uint16_t* o = a.out + (int64_t)(q0 + tq) * a.o_st + (kG * g + hh) * a.o_sh + 4 * g4;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        uint2 w;
+        w.x = pack_bf16x2(acc[hh][db][0] * inv, acc[hh][db][1] * inv);
+        w.y = pack_bf16x2(acc[hh][db][2] * inv, acc[hh][db][3] * inv);
+        *reinterpret_cast<uint2*>(o + db * 16) = w;
+      }
     }
   }
 }
@@ -343,7 +364,7 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
   a.o_sh = o_stride_h;
   a.causal = causal ? 1 : 0;
   a.scale_log2 = softmax_scale * kLog2e;
-  hipLaunchKernelGGL(prefill_kernel, dim3(num_seqs, nqt, num_kv_heads), dim3(256), 0,
+  hipLaunchKernelGGL(prefill_kernel, dim3(num_seqs, num_kv_heads, nqt), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(Q3A_ELAUNCH, "prefill: launch failed: %s", hipGetErrorString(e));
