@@ -129,13 +129,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   //      holds 4 consecutive keys x 8 dims, the shape of its transposed LDS store.
   // Page ids come from a lane-wise window (lane i = table entry pwin_base + i), read with v_readlane, so
   // a tile costs one memory round trip; the window is refilled once per 64 pages.
-  auto group_rsrc = [&](const uint16_t* base, int t, int r) __attribute__((always_inline)) {
+  // Descriptor of group r of tile t given the group's page id (uniform).
+  auto group_rsrc = [&](const uint16_t* base, int t, int r, int page) __attribute__((always_inline)) {
     const int j0 = t * kKT + 16 * r;
     const int nv = min(16, Lk - j0);
     bool ok = nv > 0;
     int64_t off = 0;
     if (paged) {
-      const int page = readlane(pwin, (j0 >> a.page_shift) - pwin_base);
       ok = ok && (unsigned)page < (unsigned)a.num_pages;
       off = (int64_t)page * a.kv_sp + (int64_t)(j0 & (a.page_size - 1)) * a.kv_st;
     } else {
@@ -149,14 +149,21 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const uint32_t tok_bytes = (uint32_t)(a.kv_st * 2);
   uint4 kr[4], vr[4];
   auto load_tile = [&](int t) __attribute__((always_inline)) {
+    // All page ids first: reading the window register waits for its load, and a wait placed between the
+    // K/V loads would also wait for the loads issued before it.
+    int pg[4] = {0, 0, 0, 0};
+    int pgv = 0;
     if (paged) {
       const int pf = (t * kKT) >> a.page_shift;
       const int pl = (t * kKT + kKT - 1) >> a.page_shift;
       if (pf < pwin_base || pl >= pwin_base + 64) load_window(pf);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pg[r] = readlane(pwin, ((t * kKT + 16 * r) >> a.page_shift) - pwin_base);
+      pgv = readlane(pwin, ((t * kKT + 16 * wave) >> a.page_shift) - pwin_base);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) kr[r] = buffer_load16(group_rsrc(a.k, t, r), k_off);
-    const __amdgpu_buffer_rsrc_t rv = group_rsrc(a.v, t, wave);
+    for (int r = 0; r < 4; ++r) kr[r] = buffer_load16(group_rsrc(a.k, t, r, pg[r]), k_off);
+    const __amdgpu_buffer_rsrc_t rv = group_rsrc(a.v, t, wave, pgv);
 #pragma unroll
     for (int b = 0; b < 4; ++b) vr[b] = buffer_load16(rv, v_off + b * tok_bytes);
   };
