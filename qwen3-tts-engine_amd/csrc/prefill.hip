@@ -9,16 +9,18 @@
 // of flash_attn_func at engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131), and both
 // read from the pool after the K/V append (engine/talker.py:161-162, engine/arrivals.py:144-145).
 //
-// Work: one workgroup (4 waves) per (sequence, 64-query tile, KV head); wave w takes tokens 16w..16w+15 of
-// the tile for BOTH query heads 2g, 2g+1 of the GQA pair, so every K or V^T operand read from LDS feeds two
-// MFMAs.  Key tiles of 64 are staged in LDS (K row-major with padding, V transposed and swizzled); the next
-// tile is prefetched into registers while the current one is consumed.  v_mfma_f32_16x16x32_bf16 layouts:
-// A lane l = row l%16, k 8*(l/16)..+8; B lane l = column l%16, same k; C lane l = column l%16, rows
-// 4*(l/16)..+4.
-//   S^T = K Q^T  : A = K (rows = keys), B = Q^T (columns = this lane's query token)
-//   O^T = V^T P^T: A = V^T from LDS, B = P^T taken straight from S^T's C registers
-// so the softmax statistics, P and the O accumulators of a query token all live on the lanes with
-// that token in column l%16; a row's max over a tile needs only two cross-lane steps.
+// Work: one workgroup (4 waves) per (sequence, KV head, 64-query tile); wave w takes tokens 16w..16w+15 of the
+// tile for BOTH query heads 2g, 2g+1 of the GQA pair, so every K or V^T operand read from LDS feeds two MFMAs.
+// K/V tiles of 64 keys are copied global -> LDS by direct-to-LDS buffer loads (no register staging) into two
+// stages, tile t+1 in flight while tile t is consumed, one barrier per tile.  LDS tiles are row-major
+// [64 keys][128 dims] with the 16-byte chunks of key k XOR-swizzled by k & 15 (bank-conflict free for both the
+// DMA writes and the operand reads).  v_mfma_f32_16x16x32_bf16 layouts: A lane l = row l%16, k 8*(l/16)..+8;
+// B lane l = column l%16, same k; C lane l = column l%16, rows 4*(l/16)..+4.
+//   S^T = K Q^T  : A = K rows from LDS, B = Q^T (columns = this lane's query token)
+//   O^T = V^T P^T: A = V^T from the row-major V tile through ds_read_b64_tr_b16 (a 16-lane transpose read),
+//                  B = P^T taken straight from S^T's C registers
+// so the softmax statistics, P and the O accumulators of a query token all live on the lanes with that token
+// in column l%16; a row's max over a tile needs only two cross-lane steps.
 #include "q3a_common.h"
 #include "../../include/q3attn.h"
 
@@ -29,11 +31,12 @@ constexpr int kD = 128;
 constexpr int kG = 2;
 constexpr int kQT = 64;        // query tokens per workgroup (16 per wave, both heads)
 constexpr int kKT = 64;        // keys per LDS tile
-constexpr int kKs = kD + 8;    // K tile row stride in LDS (bf16 elements, padded)
-constexpr int kVs = kKT + 8;   // V^T tile row stride in LDS (bf16 elements, padded)
+constexpr int kRowB = kD * 2;  // bytes of one key row in an LDS tile
+constexpr int kTileB = kKT * kRowB;
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -56,14 +59,30 @@ struct PrefillArgs {
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 __device__ __forceinline__ int readlane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
-// V^T tile swizzle: key k of dim row r is stored at column k ^ vswz(r).  It moves whole 4-key quads (bits 2-5
-// of k), so 8-byte reads of 4 consecutive keys stay contiguous; with the 72-element row stride it makes both
-// the transposed stores (16 rows x 4 quads per wave) and the MFMA operand reads free of LDS bank conflicts.
-__device__ __forceinline__ int vswz(int r) { return (((r >> 3) & 3) << 2) ^ (((r >> 5) & 3) << 4); }
+// 16 bytes per lane from the descriptor straight into LDS at lds + 16 * lane (lanes failing the descriptor's
+// bounds write zeros).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, (int)voff, 0, 0, 0);
+}
+
+// Transpose read: within each 16-lane group, lane i receives element i & 3 of the 8-byte words addressed by
+// lanes 4k + (i >> 2), k = 0..3.
+__device__ __forceinline__ uint2 ldtr(const uint8_t* lds) {
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)lds);
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Waits for this wave's outstanding vector-memory operations (the direct-to-LDS copies); vmcnt(0), the other
+// counters untouched.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
-  __shared__ __align__(16) uint16_t Ks[kKT * kKs];
-  __shared__ __align__(16) uint16_t Vt[kD * kVs];
+  // Two stages of K and V tiles; separate arrays so the compiler can tell the stage being filled from the one
+  // being read.
+  __shared__ __align__(16) uint8_t sK0[kTileB];
+  __shared__ __align__(16) uint8_t sV0[kTileB];
+  __shared__ __align__(16) uint8_t sK1[kTileB];
+  __shared__ __align__(16) uint8_t sV1[kTileB];
 
   // Grid (sequence, KV head, query tile) with the query tile slowest and reversed: the tiles with the most
   // key tiles (the last ones of each sequence) dispatch first for every head, the short ones fill in last.
@@ -120,18 +139,15 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int ntiles = kend > 0 ? (kend + kKT - 1) / kKT : 0;
   const int jlim = a.causal ? min(Lk - 1, qpos) : Lk - 1;  // last key this lane's token sees
 
-  // Tile loads.  A 64-key tile is 4 groups of 16 keys and a group never straddles a page (page sizes are
-  // powers of two >= 16), so each group has one uniform base address: all K/V loads are raw buffer loads
-  // against a descriptor covering exactly the group's valid rows of head g (rows past the sequence, and
-  // groups on an invalid page, read as zeros without touching memory).  No per-lane address math.
-  //   K: thread t loads key 16r + (t >> 4), dims 8 (t & 15), for r = 0..3.
-  //   V: wave w loads group w: keys 16w + 4((t >> 4) & 3) + b, b = 0..3, dims 8 (t & 15): each thread
-  //      holds 4 consecutive keys x 8 dims, the shape of its transposed LDS store.
-  // Page ids come from a lane-wise window (lane i = table entry pwin_base + i), read with v_readlane, so
-  // a tile costs one memory round trip; the window is refilled once per 64 pages.
-  // Descriptor of group r of tile t given the group's page id (uniform).
-  auto group_rsrc = [&](const uint16_t* base, int t, int r, int page) __attribute__((always_inline)) {
-    const int j0 = t * kKT + 16 * r;
+  // Tile copies.  A 64-key tile is 4 groups of 16 keys and a group never straddles a page (page sizes are
+  // powers of two >= 16), so each group has one uniform base address; wave w copies group w of K and of V with
+  // four direct-to-LDS loads each (instruction i: rows 4i..4i+3 of the group, 1 KiB).  The descriptor covers
+  // exactly the group's valid rows of head g: rows past the sequence and groups on an invalid page arrive as
+  // zeros.  Lane l of instruction i lands at LDS chunk slot l & 15 of row rr = 4i + (l >> 4), so it fetches
+  // global chunk (l & 15) ^ rr: the swizzle is applied on the global side.  Page ids come from a lane-wise
+  // window (lane i = table entry pwin_base + i), read with v_readlane; it is refilled once per 64 pages.
+  auto group_rsrc = [&](const uint16_t* base, int t, int page) __attribute__((always_inline)) {
+    const int j0 = t * kKT + 16 * wave;
     const int nv = min(16, Lk - j0);
     bool ok = nv > 0;
     int64_t off = 0;
@@ -143,52 +159,38 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     }
     return make_rsrc(base + (ok ? off : 0) + (int64_t)g * a.kv_sh, ok ? (uint32_t)(((nv - 1) * a.kv_st + kD) * 2) : 0u);
   };
-
-  const uint32_t k_off = (uint32_t)(((tid >> 4) * a.kv_st + 8 * (tid & 15)) * 2);
-  const uint32_t v_off = (uint32_t)((4 * ((tid >> 4) & 3) * a.kv_st + 8 * (tid & 15)) * 2);
-  const uint32_t tok_bytes = (uint32_t)(a.kv_st * 2);
-  uint4 kr[4], vr[4];
-  auto load_tile = [&](int t) __attribute__((always_inline)) {
-    // All page ids first: reading the window register waits for its load, and a wait placed between the
-    // K/V loads would also wait for the loads issued before it.
-    int pg[4] = {0, 0, 0, 0};
-    int pgv = 0;
+  uint32_t dma_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rr = 4 * i + (lane >> 4);
+    dma_off[i] = (uint32_t)((rr * a.kv_st + 8 * ((lane & 15) ^ rr)) * 2);
+  }
+  auto issue = [&](int t, uint8_t* Kst, uint8_t* Vst) __attribute__((always_inline)) {
+    int page = 0;
     if (paged) {
-      const int pf = (t * kKT) >> a.page_shift;
-      const int pl = (t * kKT + kKT - 1) >> a.page_shift;
-      if (pf < pwin_base || pl >= pwin_base + 64) load_window(pf);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pg[r] = readlane(pwin, ((t * kKT + 16 * r) >> a.page_shift) - pwin_base);
-      pgv = readlane(pwin, ((t * kKT + 16 * wave) >> a.page_shift) - pwin_base);
+      const int pi = (t * kKT + 16 * wave) >> a.page_shift;
+      if (pi < pwin_base || pi >= pwin_base + 64) load_window(pi & ~63);
+      page = readlane(pwin, pi - pwin_base);
     }
+    const __amdgpu_buffer_rsrc_t rk = group_rsrc(a.k, t, page);
+    const __amdgpu_buffer_rsrc_t rv = group_rsrc(a.v, t, page);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) kr[r] = buffer_load16(group_rsrc(a.k, t, r, pg[r]), k_off);
-    const __amdgpu_buffer_rsrc_t rv = group_rsrc(a.v, t, wave, pgv);
-#pragma unroll
-    for (int b = 0; b < 4; ++b) vr[b] = buffer_load16(rv, v_off + b * tok_bytes);
-  };
-  auto store_tile = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) st16(&Ks[((tid >> 4) + 16 * r) * kKs + 8 * (tid & 15)], kr[r]);
-    // V transposed: for each of this thread's 8 dims, its 4 keys as one 8-byte row segment.
-    const int kq = 16 * wave + 4 * ((tid >> 4) & 3);
-    const int d0 = 8 * (tid & 15);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t w0 = c == 0 ? vr[0].x : c == 1 ? vr[0].y : c == 2 ? vr[0].z : vr[0].w;
-      const uint32_t w1 = c == 0 ? vr[1].x : c == 1 ? vr[1].y : c == 2 ? vr[1].z : vr[1].w;
-      const uint32_t w2 = c == 0 ? vr[2].x : c == 1 ? vr[2].y : c == 2 ? vr[2].z : vr[2].w;
-      const uint32_t w3 = c == 0 ? vr[3].x : c == 1 ? vr[3].y : c == 2 ? vr[3].z : vr[3].w;
-      uint2 lo, hi;
-      lo.x = perm_b32(w1, w0, kPermLoLo);
-      lo.y = perm_b32(w3, w2, kPermLoLo);
-      hi.x = perm_b32(w1, w0, kPermHiHi);
-      hi.y = perm_b32(w3, w2, kPermHiHi);
-      const int r0 = d0 + 2 * c;
-      *reinterpret_cast<uint2*>(&Vt[r0 * kVs + (kq ^ vswz(r0))]) = lo;
-      *reinterpret_cast<uint2*>(&Vt[(r0 + 1) * kVs + (kq ^ vswz(r0 + 1))]) = hi;
+    for (int i = 0; i < 4; ++i) {
+      dma16(rk, Kst + (16 * wave + 4 * i) * kRowB, dma_off[i]);
+      dma16(rv, Vst + (16 * wave + 4 * i) * kRowB, dma_off[i]);
     }
   };
+
+  // Operand read offsets.  K (A of S^T): lane (col, g4) reads key kb*16 + col, logical chunk 4kk + g4, stored at
+  // slot (4kk + g4) ^ col.  V^T (A of O^T, transpose read): lane L = lane & 15 of group g4 addresses key
+  // key0 + (L >> 2) (key0 = 32 s2 + 16 p + 4 g4), dims 16 db + 4 (L & 3): chunk 2 db + ((L & 3) >> 1), byte
+  // (L & 1) * 8, with key & 15 = 4 g4 + (L >> 2) =: rsw.
+  uint32_t k_rd[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) k_rd[kk] = (uint32_t)(col * kRowB + (((4 * kk + g4) ^ col) << 4));
+  const int rsw = 4 * g4 + ((lane & 15) >> 2);
+  const int c_lo = ((lane & 15) & 3) >> 1;
+  const uint32_t v_rd = (uint32_t)(rsw * kRowB + (lane & 1) * 8);
 
   f32x4_t acc[kG][8];
 #pragma unroll
@@ -197,13 +199,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     for (int db = 0; db < 8; ++db) acc[hh][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m[kG] = {kMaxSeed, kMaxSeed}, l[kG] = {0.f, 0.f};
 
-  if (ntiles > 0) load_tile(0);
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (t + 1 < ntiles) load_tile(t + 1);
-
+  auto compute = [&](int t, const uint8_t* Ks, const uint8_t* Vs) __attribute__((always_inline)) {
     // S^T for the tile's 4 blocks of 16 keys, both heads; each K operand is read once.
     f32x4_t st[kG][4];
 #pragma unroll
@@ -212,7 +208,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       for (int hh = 0; hh < kG; ++hh) st[hh][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8_t kv = as_bf16x8(ld16(&Ks[(kb * 16 + col) * kKs + 32 * kk + 8 * g4]));
+        const bf16x8_t kv = as_bf16x8(ld16(Ks + kb * 16 * kRowB + k_rd[kk]));
 #pragma unroll
         for (int hh = 0; hh < kG; ++hh)
           st[hh][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qb[hh][kk], st[hh][kb], 0, 0, 0);
@@ -273,23 +269,40 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
         pb[hh][s2] = as_bf16x8(w);
       }
     }
-    // O^T += V^T P^T; V^T rows are dims, the same key order as the B operand; each V^T operand is
-    // read once for both heads.
+    // O^T += V^T P^T: the V^T operand of keys 32 s2 + 4 g4 + (0..3) and 32 s2 + 16 + 4 g4 + (0..3) (the B
+    // operand's key order) comes from two transpose reads; each is used for both heads.
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
-      const int vr_row = db * 16 + col;
-      const uint16_t* vrow = &Vt[vr_row * kVs];
-      const int sw = vswz(vr_row);
+      const uint32_t chunk = (uint32_t)((((2 * db) + c_lo) ^ rsw) << 4);
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + ((32 * s2 + 4 * g4) ^ sw));
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + ((32 * s2 + 4 * g4 + 16) ^ sw));
+        const uint2 lo = ldtr(Vs + v_rd + chunk + (32 * s2) * kRowB);
+        const uint2 hi = ldtr(Vs + v_rd + chunk + (32 * s2 + 16) * kRowB);
         const bf16x8_t va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
         for (int hh = 0; hh < kG; ++hh)
           acc[hh][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[hh][s2], acc[hh][db], 0, 0, 0);
       }
     }
+  };
+
+  // Stage (t+1) & 1 is filled while tile t is read from stage t & 1; the barrier at the end of each tile both
+  // publishes the next tile (every wave has waited for its own copies) and frees the stage just read.
+  // The wait is unconditional so that no path into the loop carries outstanding loads (the q fragments): a
+  // pending load on any entry path makes the compiler drain every copy before the first MFMA of each tile.
+  if (ntiles > 0) issue(0, sK0, sV0);
+  wait_vmem();
+  __syncthreads();
+  for (int t = 0; t < ntiles; t += 2) {
+    if (t + 1 < ntiles) issue(t + 1, sK1, sV1);
+    compute(t, sK0, sV0);
+    wait_vmem();
+    __syncthreads();
+    if (t + 1 >= ntiles) break;
+    if (t + 2 < ntiles) issue(t + 2, sK0, sV0);
+    compute(t + 1, sK1, sV1);
+    wait_vmem();
+    __syncthreads();
   }
 
   // The 4 lanes of a token hold partial sums over disjoint keys.
