@@ -72,6 +72,19 @@ __device__ __forceinline__ uint2 ldtr(const uint8_t* lds) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// max(x, x of lane l ^ 32) and max(x, x of lane l ^ 16) with the gfx950 lane-swap instructions (plain VALU
+// operations, unlike a shuffle through the LDS crossbar): v_permlane32_swap exchanges lanes 32..63 of its first
+// operand with lanes 0..31 of its second, v_permlane16_swap the odd 16-lane rows of the first with the even rows
+// of the second, so with x in both operands the two results hold x and its partner lane's x.
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Waits for this wave's outstanding vector-memory operations (the direct-to-LDS copies); vmcnt(0), the other
 // counters untouched.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -230,8 +243,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
           mx = fmaxf(mx, st[hh][kb][i]);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = max_xor16(max_xor32(mx));
       mx *= a.scale_log2;
       // Lazy rescale: keep the running max while no token's tile max exceeds it by more than 8 (log2
       // units), so p = exp2(s * scale - m) <= 256 is exact enough in bf16/fp32 and (l, acc) are rescaled
