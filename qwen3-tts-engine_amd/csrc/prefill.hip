@@ -253,12 +253,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
         const float alpha = fast_exp2(m[hh] - mn);
         l[hh] *= alpha;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-          acc[hh][db][0] *= alpha;
-          acc[hh][db][1] *= alpha;
-          acc[hh][db][2] *= alpha;
-          acc[hh][db][3] *= alpha;
-        }
+        for (int db = 0; db < 8; ++db) acc[hh][db] = acc[hh][db] * alpha;
         m[hh] = mn;
       }
       // P^T as the B operand: k slot 8*g4 + i <- key 32*s2 + 4*g4 + i, slot 8*g4 + 4 + i <- key
