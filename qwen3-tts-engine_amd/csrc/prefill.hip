@@ -28,7 +28,7 @@ namespace q3a {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kG = 2;
+constexpr int kG = 2;  // query heads per KV head (the softmax below is written for exactly two)
 constexpr int kQT = 64;        // query tokens per workgroup (16 per wave, both heads)
 constexpr int kKT = 64;        // keys per LDS tile
 constexpr int kRowB = kD * 2;  // bytes of one key row in an LDS tile
@@ -232,30 +232,38 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     // Masked scores become -inf; the running max m is kept in scaled (log2) units.
     const int lim = jlim - t * kKT - 4 * g4;
     bf16x8_t pb[kG][2];
+    float mx[kG];
 #pragma unroll
     for (int hh = 0; hh < kG; ++hh) {
-      float mx = -INFINITY;
+      mx[hh] = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           st[hh][kb][i] = (kb * 16 + i <= lim) ? st[hh][kb][i] : -INFINITY;
-          mx = fmaxf(mx, st[hh][kb][i]);
+          mx[hh] = fmaxf(mx[hh], st[hh][kb][i]);
         }
       }
-      mx = max_xor16(max_xor32(mx));
-      mx *= a.scale_log2;
-      // Lazy rescale: keep the running max while no token's tile max exceeds it by more than 8 (log2
-      // units), so p = exp2(s * scale - m) <= 256 is exact enough in bf16/fp32 and (l, acc) are rescaled
-      // only when a max grows past that margin.  The first tile always sets the max.
-      if (__any(mx > m[hh] + 8.f)) {
-        const float mn = fmaxf(m[hh], mx);
+    }
+#pragma unroll
+    for (int hh = 0; hh < kG; ++hh) mx[hh] = max_xor16(max_xor32(mx[hh])) * a.scale_log2;
+    // Lazy rescale: keep the running max while no token's tile max exceeds it by more than 8 (log2 units), so
+    // p = exp2(s * scale - m) <= 256 is exact enough in bf16/fp32 and (l, acc) are rescaled only when a max grows
+    // past that margin; one wave vote covers both heads (a head whose max did not grow gets alpha = 1 or a
+    // smaller exact shift).  The first tile always sets the max.
+    if (__any(mx[0] > m[0] + 8.f || mx[1] > m[1] + 8.f)) {
+#pragma unroll
+      for (int hh = 0; hh < kG; ++hh) {
+        const float mn = fmaxf(m[hh], mx[hh]);
         const float alpha = fast_exp2(m[hh] - mn);
         l[hh] *= alpha;
 #pragma unroll
         for (int db = 0; db < 8; ++db) acc[hh][db] = acc[hh][db] * alpha;
         m[hh] = mn;
       }
+    }
+#pragma unroll
+    for (int hh = 0; hh < kG; ++hh) {
       // P^T as the B operand: k slot 8*g4 + i <- key 32*s2 + 4*g4 + i, slot 8*g4 + 4 + i <- key
       // 32*s2 + 16 + 4*g4 + i (blocks 2*s2 and 2*s2+1 of this lane's C registers).
 #pragma unroll
