@@ -16,6 +16,11 @@ import torch
 from ._lib import check, lib
 
 
+# Fixed-split limits of q3a_paged_decode (split_tokens <= 1024, at most 64 splits per row).
+_MAX_SPLIT_TOKENS = 1024
+_MAX_SPLITS = 64
+
+
 def _req(cond: bool, msg: str) -> None:
     if not cond:
         raise RuntimeError(msg)
@@ -175,8 +180,14 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
     scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
     split = 0
     if num_splits and num_splits > 0:
+        # flash-attn's split count maps to a fixed split length, kept inside the library's limits: at most
+        # _MAX_SPLITS splits per row and _MAX_SPLIT_TOKENS tokens per split (beyond both: stream-K).
         max_ctx = block_table.shape[1] * k_cache.shape[1]
-        split = max(16, 16 * math.ceil(math.ceil(max_ctx / num_splits) / 16))
+        ceil16 = lambda n: 16 * math.ceil(n / 16)
+        lo = max(16, ceil16(math.ceil(max_ctx / _MAX_SPLITS)))
+        split = min(max(lo, ceil16(math.ceil(max_ctx / num_splits))), _MAX_SPLIT_TOKENS)
+        if lo > _MAX_SPLIT_TOKENS:
+            split = 0
     if k is not None:
         _req(k.dim() == 4 and v.dim() == 4, "q3attn.flash_attn_with_kvcache: k/v must be [batch, new, kv_heads, head_dim]")
         if k.shape[1] != 1 or v.shape[1] != 1:

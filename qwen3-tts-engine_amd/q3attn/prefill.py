@@ -89,6 +89,10 @@ _CU_CACHE: dict = {}
 
 
 def _cu(n: int, length: int, device) -> torch.Tensor:
+    """Cumulative lengths 0, L, 2L, ... nL.  Cached outside graph capture only: a tensor made during a capture
+    lives in that graph's memory pool and must not outlive it or be shared with another graph."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.arange(0, (n + 1) * length, length, dtype=torch.int32, device=device)
     key = (n, length, str(device))
     t = _CU_CACHE.get(key)
     if t is None:

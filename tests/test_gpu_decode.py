@@ -191,3 +191,16 @@ def test_stream_k_matches_fixed_split(cuda_device):
     b = run(wl, split=128)
     ok, st = ora.compare(to_np(a), to_np(b), max_abs=8e-3, mean_abs=2e-4)
     assert ok, st
+
+
+@pytest.mark.parametrize("num_splits", [1, 3, 200])
+def test_flash_attn_num_splits(cuda_device, num_splits):
+    """flash-attn's num_splits maps to a fixed split length inside the library's limits (1 split over a
+    1,800-token table is clamped to 1,024-token splits; 200 splits to the 64-split minimum length)."""
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=5)
+    L = wl.layers[0]
+    out = q3attn.flash_attn_with_kvcache(L.q.unsqueeze(1), wl.k_cache, wl.v_cache, cache_seqlens=wl.cache_seqlens,
+                                         block_table=L.block_table, softmax_scale=wl.scale, causal=True,
+                                         num_splits=num_splits)
+    torch.cuda.synchronize()
+    assert_parity(out[:, 0], decode_oracle(wl), f"num_splits={num_splits}")
