@@ -17,8 +17,8 @@
 // Work decomposition (default): stream-K.  The grid is exactly the number of workgroups the GPU
 // holds at once; the flattened sequence of (row, tile) pairs is cut into equal contiguous ranges,
 // one per workgroup, and every wave of a workgroup streams its KV head over that range.  Rows that
-// straddle a range boundary leave fp32 partials (m, l, unnormalised o) in at most two slots per
-// workgroup; the combine kernel merges them and writes zeros for ctx == 0 rows.
+// straddle a range boundary leave partial records (fp32 m, l and the normalised o in 16 bits) in at
+// most two slots per workgroup; the combine kernel merges them and writes zeros for ctx == 0 rows.
 // Alternative (split_tokens > 0): one workgroup per (row, fixed-size split), partials merged by
 // the same kind of combine.
 //
@@ -35,7 +35,10 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kG = 2;                              // query heads per KV head
-constexpr int kPartFloats = kG * kD + 2 * kG;      // acc[G][D], m[G], l[G]
+// Partial record of one (segment, KV head): o = acc / l of both query heads as 16-bit values (fp16; bf16 when
+// some |o| would overflow fp16, flagged by negative l), then m[G], l[G] in fp32: 528 bytes, addressed in floats.
+constexpr int kPartFloats = kG * kD / 2 + 2 * kG;
+constexpr int kPartML = kG * kD / 2;               // float index of m[0]; l[h] at kPartML + kG + h
 constexpr int kMaxSplits = 64;
 constexpr int kTile = 16;                          // tokens per pipeline stage
 constexpr int kMaxSplitTokens = 64 * kTile;        // one VGPR lane per tile of a split
@@ -303,23 +306,52 @@ __device__ __forceinline__ void write_output(const DecodeArgs& a, int b, int g, 
   }
 }
 
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const _Float16 a = (_Float16)lo, b = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+__device__ __forceinline__ float f16_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu)); }
+__device__ __forceinline__ float f16_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+
+// Writes the segment's record (layout at kPartFloats).  The partial records are the decode kernel's only
+// sizeable writes and, interleaved with the K/V read stream, cost ~1 us per MB at C5, so o is stored
+// normalised in 16 bits: fp16 keeps 11 significant bits (relative error 2^-12 against the bf16 output's
+// 2^-9) while the record's largest |o| lies in [2^-6, 2^15]; outside that range (fp16 overflow, or values
+// small enough for fp16's fixed absolute resolution to matter) the record is stored in bf16, flagged by
+// negative l.
+// Every lane holds the merged (m, l, acc) after merge_lanes; lanes 0..15 write o, lane 0 writes (m, l).
 __device__ __forceinline__ void write_partial(float* P, int lane, int grp, int dl, const float (&m)[kG],
                                               const float (&l)[kG], const float (&acc)[kG][8]) {
+  float inv[kG], big = 0.f;
+#pragma unroll
+  for (int h = 0; h < kG; ++h) {
+    inv[h] = l[h] > 0.f ? 1.f / l[h] : 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) big = fmaxf(big, fabsf(acc[h][d] * inv[h]));
+  }
+  const bool wide = __any(big > 32768.f || big < 0.015625f);
   if (grp == 0) {
 #pragma unroll
     for (int h = 0; h < kG; ++h) {
-      float4* dst = reinterpret_cast<float4*>(P + h * kD + dl);
-      dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-      dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+      const float* x = acc[h];
+      const float s = inv[h];
+      uint4 w;
+      if (wide) {
+        w.x = pack_bf16x2(x[0] * s, x[1] * s);
+        w.y = pack_bf16x2(x[2] * s, x[3] * s);
+        w.z = pack_bf16x2(x[4] * s, x[5] * s);
+        w.w = pack_bf16x2(x[6] * s, x[7] * s);
+      } else {
+        w.x = pack_f16x2(x[0] * s, x[1] * s);
+        w.y = pack_f16x2(x[2] * s, x[3] * s);
+        w.z = pack_f16x2(x[4] * s, x[5] * s);
+        w.w = pack_f16x2(x[6] * s, x[7] * s);
+      }
+      st16(reinterpret_cast<char*>(P) + h * kD * 2 + dl * 2, w);
     }
   }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < kG; ++h) {
-      P[kG * kD + h] = m[h];
-      P[kG * kD + kG + h] = l[h];
-    }
-  }
+  if (lane == 0)
+    st16(P + kPartML, __builtin_bit_cast(uint4, make_float4(m[0], m[1], wide ? -l[0] : l[0], wide ? -l[1] : l[1])));
 }
 
 // Merges `count` partial records (rec(i) -> record i) of one (row, KV head) into the output row.
@@ -345,8 +377,8 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int b, int g,
       const float* P = rec(c0 + lane);
 #pragma unroll
       for (int h = 0; h < kG; ++h) {
-        mj[h] = P[kG * kD + h];
-        lj[h] = P[kG * kD + kG + h];
+        mj[h] = P[kPartML + h];
+        lj[h] = fabsf(P[kPartML + kG + h]);
       }
     }
 #pragma unroll
@@ -362,7 +394,7 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int b, int g,
       M[h] = mn;
     }
   }
-  // Pass 2: weighted sum of the unnormalised partial outputs, 8 independent loads in flight.
+  // Pass 2: sum of the records' o weighted by l * 2^(m - M), 8 independent loads in flight.
   const int h = lane >> 5;
   const int d0 = (lane & 31) * 4;
   const float Mh = h == 0 ? M[0] : M[1];
@@ -374,8 +406,14 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int b, int g,
     for (int u = 0; u < 8; ++u) {
       if (s0 + u < count) {
         const float* P = rec(s0 + u);
-        v[u] = *reinterpret_cast<const float4*>(P + h * kD + d0);
-        w[u] = fast_exp2(P[kG * kD + h] - Mh);
+        const uint2 raw = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(P) + (h * kD + d0) * 2);
+        const float lr = P[kPartML + kG + h];
+        if (__builtin_signbit(lr)) {
+          v[u] = make_float4(bf16_lo(raw.x), bf16_hi(raw.x), bf16_lo(raw.y), bf16_hi(raw.y));
+        } else {
+          v[u] = make_float4(f16_lo(raw.x), f16_hi(raw.x), f16_lo(raw.y), f16_hi(raw.y));
+        }
+        w[u] = fabsf(lr) * fast_exp2(P[kPartML + h] - Mh);
       } else {
         v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         w[u] = 0.f;

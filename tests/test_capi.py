@@ -75,7 +75,8 @@ def test_workspace_and_default_split():
     assert split % 16 == 0 and split >= 16
     n_splits = -(-113 * 16 // split)
     assert n_splits <= 64
-    assert L.q3a_paged_decode_workspace_bytes(576, 16, 8, 128, 113, 16, split) == 576 * n_splits * 8 * 260 * 4
+    # one 528-byte partial record (2 x 128 16-bit o values, m[2], l[2] in fp32) per (row, split, KV head)
+    assert L.q3a_paged_decode_workspace_bytes(576, 16, 8, 128, 113, 16, split) == 576 * n_splits * 8 * 528
     # one split: no workspace
     assert L.q3a_paged_decode_workspace_bytes(4, 16, 8, 128, 4, 16, 64) == 0
     # small batches get smaller splits (more workgroups)

@@ -204,3 +204,20 @@ def test_flash_attn_num_splits(cuda_device, num_splits):
                                          num_splits=num_splits)
     torch.cuda.synchronize()
     assert_parity(out[:, 0], decode_oracle(wl), f"num_splits={num_splits}")
+
+
+@pytest.mark.parametrize("split", [0, 32])
+@pytest.mark.parametrize("v_scale", [1.0 / 4096, 1.0, 3.0e5])
+def test_partial_records_keep_precision_at_extreme_v(cuda_device, split, v_scale):
+    """Rows cut into several segments are merged from 16-bit partial records: fp16 o for ordinary values, bf16
+    when a record's largest |o| is below 2^-6 (V ~ 2.4e-4) or above 2^15 (V ~ 3e5).  Either way the result stays
+    within the bf16 output's own rounding of the oracle (relative to the largest |o|)."""
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=8)
+    v = (wl.v_cache.float() * v_scale).to(torch.bfloat16)
+    wl.v_cache = v
+    out = run(wl, split=split, v=v).float().cpu().numpy()
+    ref = decode_oracle(wl)
+    scale = float(np.abs(ref).max())
+    err = np.abs(out - ref) / scale
+    print(f"[parity] v_scale={v_scale} split={split} max_rel={err.max():.2e} mean_rel={err.mean():.2e}", flush=True)
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3
