@@ -355,80 +355,56 @@ __device__ __forceinline__ void write_partial(float* P, int lane, int grp, int d
 }
 
 // Merges `count` partial records (rec(i) -> record i) of one (row, KV head) into the output row.
-// The whole wave participates; lane l owns query head l/32 and dims 4*(l%32)..+4.
+// The whole wave participates; lane l owns query head l/32 and dims 4*(l%32)..+4.  Each lane reads every
+// record's (m, l) of its head itself (the 32 lanes of a head read the same words), so the merge needs no
+// cross-lane step, and the o, m and l loads of up to 8 records are all in flight at once; records are folded
+// in with an online rescale (running max M, running weight L).
 template <typename RecFn>
 __device__ __forceinline__ void merge_records(const DecodeArgs& a, int b, int g, int lane, int count,
                                               RecFn rec) {
-  // Pass 1: global max and weighted sum of l over all records, 64 records per step.
-  float M[kG], L[kG];
-#pragma unroll
-  for (int h = 0; h < kG; ++h) {
-    M[h] = kMaxSeed;
-    L[h] = 0.f;
-  }
-  for (int c0 = 0; c0 < count; c0 += 64) {
-    float mj[kG], lj[kG];
-#pragma unroll
-    for (int h = 0; h < kG; ++h) {
-      mj[h] = kMaxSeed;
-      lj[h] = 0.f;
-    }
-    if (c0 + lane < count) {
-      const float* P = rec(c0 + lane);
-#pragma unroll
-      for (int h = 0; h < kG; ++h) {
-        mj[h] = P[kPartML + h];
-        lj[h] = fabsf(P[kPartML + kG + h]);
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < kG; ++h) {
-      float x = mj[h];
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-      const float mn = fmaxf(M[h], x);
-      float y = lj[h] * fast_exp2(mj[h] - mn);
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) y += __shfl_xor(y, o);
-      L[h] = L[h] * fast_exp2(M[h] - mn) + y;
-      M[h] = mn;
-    }
-  }
-  // Pass 2: sum of the records' o weighted by l * 2^(m - M), 8 independent loads in flight.
   const int h = lane >> 5;
   const int d0 = (lane & 31) * 4;
-  const float Mh = h == 0 ? M[0] : M[1];
+  float M = kMaxSeed, L = 0.f;
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = 0; s0 < count; s0 += 8) {
-    float4 v[8];
-    float w[8];
+    uint2 raw[8];
+    float mr[8], lr[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
+      raw[u] = make_uint2(0u, 0u);
+      mr[u] = kMaxSeed;
+      lr[u] = 0.f;
       if (s0 + u < count) {
         const float* P = rec(s0 + u);
-        const uint2 raw = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(P) + (h * kD + d0) * 2);
-        const float lr = P[kPartML + kG + h];
-        if (__builtin_signbit(lr)) {
-          v[u] = make_float4(bf16_lo(raw.x), bf16_hi(raw.x), bf16_lo(raw.y), bf16_hi(raw.y));
-        } else {
-          v[u] = make_float4(f16_lo(raw.x), f16_hi(raw.x), f16_lo(raw.y), f16_hi(raw.y));
-        }
-        w[u] = fabsf(lr) * fast_exp2(P[kPartML + h] - Mh);
-      } else {
-        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        w[u] = 0.f;
+        raw[u] = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(P) + (h * kD + d0) * 2);
+        mr[u] = P[kPartML + h];
+        lr[u] = P[kPartML + kG + h];
       }
     }
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mc = fmaxf(mc, mr[u]);
+    const float alpha = fast_exp2(M - mc);
+    L *= alpha;
+    A.x *= alpha;
+    A.y *= alpha;
+    A.z *= alpha;
+    A.w *= alpha;
+    M = mc;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      A.x = fmaf(v[u].x, w[u], A.x);
-      A.y = fmaf(v[u].y, w[u], A.y);
-      A.z = fmaf(v[u].z, w[u], A.z);
-      A.w = fmaf(v[u].w, w[u], A.w);
+      const bool wide = __builtin_signbit(lr[u]);
+      const float w = fabsf(lr[u]) * fast_exp2(mr[u] - M);
+      const float4 v = wide ? make_float4(bf16_lo(raw[u].x), bf16_hi(raw[u].x), bf16_lo(raw[u].y), bf16_hi(raw[u].y))
+                            : make_float4(f16_lo(raw[u].x), f16_hi(raw[u].x), f16_lo(raw[u].y), f16_hi(raw[u].y));
+      L += w;
+      A.x = fmaf(v.x, w, A.x);
+      A.y = fmaf(v.y, w, A.y);
+      A.z = fmaf(v.z, w, A.z);
+      A.w = fmaf(v.w, w, A.w);
     }
   }
-  const float lsel = h == 0 ? L[0] : L[1];
-  const float inv = lsel > 0.f ? 1.f / lsel : 0.f;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
   uint2 o;
   o.x = pack_bf16x2(A.x * inv, A.y * inv);
   o.y = pack_bf16x2(A.z * inv, A.w * inv);
