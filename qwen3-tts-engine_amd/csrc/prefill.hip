@@ -155,6 +155,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   }
   const int ntiles = kend > 0 ? (kend + kKT - 1) / kKT : 0;
   const int jlim = a.causal ? min(Lk - 1, qpos) : Lk - 1;  // last key this lane's token sees
+  // Last key that every token of this wave sees (wave-uniform).
+  const int wlim = a.causal ? min(Lk - 1, Lk - Lq + qt * kQT + wave * 16) : Lk - 1;
 
   // Tile copies.  A 64-key tile is 4 groups of 16 keys and a group never straddles a page (page sizes are
   // powers of two >= 16), so each group has one uniform base address; wave w copies group w of K and of V with
@@ -234,20 +236,25 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     // Mask: key j is visible to this lane's token iff j <= jlim (= min(Lk - 1, qpos) when causal).
     // Relative to the tile and this lane's key rows that is one compare per score against `lim`.
     // Masked scores become -inf; the running max m is kept in scaled (log2) units.
-    const int lim = jlim - t * kKT - 4 * g4;
+    // Tiles that every token of the wave sees whole (all but the diagonal one and the sequence's last) skip it.
+    if (t * kKT + kKT - 1 > wlim) {
+      const int lim = jlim - t * kKT - 4 * g4;
+#pragma unroll
+      for (int hh = 0; hh < kG; ++hh)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[hh][kb][i] = (kb * 16 + i <= lim) ? st[hh][kb][i] : -INFINITY;
+    }
     bf16x8_t pb[kG][2];
     float mx[kG];
 #pragma unroll
     for (int hh = 0; hh < kG; ++hh) {
       mx[hh] = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          st[hh][kb][i] = (kb * 16 + i <= lim) ? st[hh][kb][i] : -INFINITY;
-          mx[hh] = fmaxf(mx[hh], st[hh][kb][i]);
-        }
-      }
+        for (int i = 0; i < 4; ++i) mx[hh] = fmaxf(mx[hh], st[hh][kb][i]);
     }
 #pragma unroll
     for (int hh = 0; hh < kG; ++hh) mx[hh] = max_xor16(max_xor32(mx[hh])) * a.scale_log2;
