@@ -13,7 +13,10 @@
 // dimension (4 x 16 B loads; the 4 lanes of a slot read 64 contiguous bytes per instruction) and
 // reduces with two quad DPP steps.  P.V: lane l owns output dims 2l, 2l+1 of both query heads and
 // walks the slots; each slot is one 256 B coalesced load and the slot's probability is broadcast
-// with v_readlane.  All loads of the wave are issued before the first use.
+// with v_readlane.  All loads of the wave are issued before the first use, without branches: the
+// scratch rows go through a buffer descriptor whose extent ends at the last row read, so the loads
+// of dead slots return zeros without touching memory.  Cross-row reductions use the gfx950 lane
+// swaps.
 #include "q3a_common.h"
 #include "../../include/q3attn.h"
 
@@ -40,11 +43,27 @@ struct CpArgs {
   float scale_log2;
 };
 
+// x + (x of lane l ^ 32) and x + (x of lane l ^ 16), and the same for max, with the gfx950 lane swaps (VALU
+// operations, not the LDS crossbar): with x in both operands, one result holds x and the other the partner's x.
+__device__ __forceinline__ float2 swap32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 swap16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) { const float2 r = swap32(x); return r.x + r.y; }
+__device__ __forceinline__ float sum_xor16(float x) { const float2 r = swap16(x); return r.x + r.y; }
+__device__ __forceinline__ float max_xor32(float x) { const float2 r = swap32(x); return fmaxf(r.x, r.y); }
+__device__ __forceinline__ float max_xor16(float x) { const float2 r = swap16(x); return fmaxf(r.x, r.y); }
+
+template <bool kAppend>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpArgs a) {
   const int wave = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (wave >= a.pairs) return;
-  const int b = wave / a.hkv;
-  const int g = wave - b * a.hkv;
+  const int b = __builtin_amdgcn_readfirstlane(wave / a.hkv);
+  const int g = __builtin_amdgcn_readfirstlane(wave - b * a.hkv);
   const int lane = threadIdx.x & 63;
   const int slot = lane >> 2;
   const int c = lane & 3;
@@ -53,38 +72,60 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   uint16_t* kb = a.k + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
   uint16_t* vb = a.v + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
   const uint16_t* qb = a.q + (int64_t)b * a.q_sb + (int64_t)(kG * g) * kD;
-  // With k_new/v_new, slot n_live - 1 comes from those rows (and is stored into the scratch here);
-  // it is never read back from the scratch, so the write and the reads of this wave cannot race.
-  const bool append = a.k_new != nullptr;
+  // The scratch rows read are 0..n_read-1: all live slots, or in the append form all but the last, which
+  // comes from this step's k/v rows (and is stored into the scratch here; it is never read back from the
+  // scratch, so the write and the reads of this wave cannot race).  Every load is unconditional: rows past
+  // n_read fail the descriptor's bounds and read as zeros without touching memory, so slots >= n_live are
+  // never read and no branch or early wait sits between the loads.
   const int last = a.n_live - 1;
-  const uint16_t* knb = append ? a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD : nullptr;
-  const uint16_t* vnb = append ? a.v_new + (int64_t)b * a.vn_sb + (int64_t)g * kD : nullptr;
+  const int n_read = kAppend ? last : a.n_live;
+  const uint32_t row_b = (uint32_t)a.kv_ss * 2;
+  const uint32_t span = n_read > 0 ? (uint32_t)(n_read - 1) * row_b + kD * 2 : 0u;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, span);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, span);
 
   // Lane (slot, c) holds dims 32*i + 8*c .. +8 for i = 0..3, of K[slot] and of both query heads.
-  uint4 kr[4], qr[kG][4];
-  const bool k_from_new = append && slot == last;
+  uint4 kr[4], qr[kG][4], kn[4];
+  uint32_t vr[kSlots], vn = 0u;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int d = 32 * i + 8 * c;
-    kr[i] = make_uint4(0u, 0u, 0u, 0u);
-    if (k_from_new) kr[i] = *reinterpret_cast<const uint4*>(knb + d);
-    else if (live) kr[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)slot * a.kv_ss + d);
+  for (int h = 0; h < kG; ++h)
 #pragma unroll
-    for (int h = 0; h < kG; ++h) qr[h][i] = *reinterpret_cast<const uint4*>(qb + h * kD + d);
+    for (int i = 0; i < 4; ++i) qr[h][i] = ld16(qb + h * kD + 32 * i + 8 * c);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kr[i] = buffer_load16(rk, (uint32_t)slot * row_b + (32 * i + 8 * c) * 2);
+  // In the append form the new k row goes to the lanes of slot `last` (the other lanes' offsets are out of
+  // bounds: zeros).
+  const bool mine = kAppend && slot == last;
+  __amdgpu_buffer_rsrc_t rkn = rk, rvn = rv;
+  if constexpr (kAppend) {
+    rkn = make_rsrc(a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD, kD * 2);
+    rvn = make_rsrc(a.v_new + (int64_t)b * a.vn_sb + (int64_t)g * kD, kD * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kn[i] = buffer_load16(rkn, mine ? (uint32_t)(32 * i + 8 * c) * 2 : 0x80000000u);
   }
-  uint32_t vr[kSlots];
 #pragma unroll
-  for (int s = 0; s < kSlots; ++s) {
-    vr[s] = 0u;
-    if (append && s == last) vr[s] = *reinterpret_cast<const uint32_t*>(vnb + 2 * lane);
-    else if (s < a.n_live) vr[s] = *reinterpret_cast<const uint32_t*>(vb + (int64_t)s * a.kv_ss + 2 * lane);
-  }
-  if (append) {
-    if (k_from_new) {
+  for (int s = 0; s < kSlots; ++s)
+    vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, (int)((uint32_t)s * row_b + lane * 4), 0, 0);
+  if constexpr (kAppend) vn = __builtin_amdgcn_raw_buffer_load_b32(rvn, lane * 4, 0, 0);
+  // Every load is in flight before any is waited for.
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kAppend) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(kb + (int64_t)last * a.kv_ss + 32 * i + 8 * c) = kr[i];
+    for (int i = 0; i < 4; ++i) {
+      kr[i].x |= kn[i].x;
+      kr[i].y |= kn[i].y;
+      kr[i].z |= kn[i].z;
+      kr[i].w |= kn[i].w;
     }
-    *reinterpret_cast<uint32_t*>(vb + (int64_t)last * a.kv_ss + 2 * lane) = vr[last];
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s)
+      if (s == last) vr[s] = vn;
+    // Slot `last` of the scratch, written with vector buffer stores (lanes of other slots are out of bounds).
+    const __amdgpu_buffer_rsrc_t wk = make_rsrc(kb + (int64_t)last * a.kv_ss, kD * 2);
+    const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.kv_ss, kD * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buffer_store16_s(kn[i], wk, mine ? (uint32_t)(32 * i + 8 * c) * 2 : 0x80000000u, 0u);
+    __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, 0);
   }
 
   float p[kG];
@@ -101,13 +142,9 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
     x = quad_sum(x);
     x = live ? x * a.scale_log2 : -INFINITY;
     // Max and sum over the 16 slots: quad-uniform values, 4 quads per row, 4 rows per wave.
-    float mx = quads_max(x);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mx = max_xor32(max_xor16(quads_max(x)));
     const float e = fast_exp2(x - mx);
-    float z = quads_sum(e);
-    z += __shfl_xor(z, 16);
-    z += __shfl_xor(z, 32);
+    const float z = sum_xor32(sum_xor16(quads_sum(e)));
     p[h] = round_bf16(e / z);
   }
 
@@ -156,6 +193,8 @@ static int cp_launch(const void* q, int64_t q_stride_b, void* k, void* v, int64_
     return fail(Q3A_EINVAL, "%s: strides must be multiples of 8 elements (16 bytes)", who);
   const int64_t pairs = (int64_t)batch * num_kv_heads;
   if (pairs > ((int64_t)1 << 30)) return fail(Q3A_EINVAL, "%s: batch too large", who);
+  if (kv_stride_s < head_dim || kv_stride_s > ((int64_t)1 << 26))
+    return fail(Q3A_EINVAL, "%s: slot stride %lld must be in [head_dim, 2^26] elements", who, (long long)kv_stride_s);
 
   CpArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -176,8 +215,12 @@ static int cp_launch(const void* q, int64_t q_stride_b, void* k, void* v, int64_
   a.n_live = n_live;
   a.scale_log2 = softmax_scale * kLog2e;
   const int blocks = (int)((pairs + kWavesPerBlock - 1) / kWavesPerBlock);
-  hipLaunchKernelGGL(cp_attn_kernel, dim3(blocks), dim3(64 * kWavesPerBlock), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (k_new != nullptr)
+    hipLaunchKernelGGL(cp_attn_kernel<true>, dim3(blocks), dim3(64 * kWavesPerBlock), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(cp_attn_kernel<false>, dim3(blocks), dim3(64 * kWavesPerBlock), 0,
+                       static_cast<hipStream_t>(stream), a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   return Q3A_OK;
