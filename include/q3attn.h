@@ -110,7 +110,8 @@ int q3a_paged_decode_default_split(int batch, int num_kv_heads, int max_pages_pe
  *   q   [B, Hq, D] bf16 with row stride q_stride_b (head stride D)
  *   k,v [B, Hkv, S, D] bf16 with strides kv_stride_b / kv_stride_h / kv_stride_s (dim stride 1)
  *   out [B, Hq*D] bf16 with row stride o_stride_b
- * Requirements: D == 128, Hq == 2*Hkv, 1 <= n_live <= 16.
+ * Requirements: D == 128, Hq == 2*Hkv, 1 <= n_live <= 16, 16-byte aligned pointers and strides,
+ * D <= kv_stride_s <= 2^26 elements.
  */
 int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
                 int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,

@@ -86,6 +86,7 @@ def test_workspace_and_default_split():
 @pytest.mark.parametrize("kw,frag", [
     (dict(n_live=0), "n_live"), (dict(n_live=17), "n_live"), (dict(D=64), "head_dim"),
     (dict(Hq=12), "num_q_heads"), (dict(q=None), "null"), (dict(kv_ss=100), "strides"),
+    (dict(kv_ss=64), "slot stride"), (dict(kv_ss=(1 << 26) + 8), "slot stride"),
 ])
 def test_cp_attn_rejects_bad_arguments(kw, frag):
     a = dict(q=16, q_sb=2048, k=16, v=16, kv_sb=16384, kv_sh=2048, kv_ss=128, out=16, o_sb=2048,
