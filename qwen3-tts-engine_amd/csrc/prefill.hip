@@ -11,9 +11,10 @@
 //
 // Work: one workgroup (4 waves) per (sequence, KV head, 64-query tile); wave w takes tokens 16w..16w+15 of the
 // tile for BOTH query heads 2g, 2g+1 of the GQA pair, so every K or V^T operand read from LDS feeds two MFMAs.
-// K/V tiles of 64 keys are copied global -> LDS by direct-to-LDS buffer loads (no register staging) into two
-// stages, tile t+1 in flight while tile t is consumed, one barrier per tile.  LDS tiles are row-major
-// [64 keys][128 dims] with the 16-byte chunks of key k XOR-swizzled by k & 15 (bank-conflict free for both the
+// K/V tiles of 32 keys are copied global -> LDS by direct-to-LDS buffer loads (no register staging) into two
+// stages, tile t+1 in flight while tile t is consumed, one barrier per tile.  32-key tiles keep the LDS at 32 KiB
+// and the registers under 168 per lane, so three workgroups share a CU (64-key tiles: two).  LDS tiles are
+// row-major [32 keys][128 dims] with the 16-byte chunks of key k XOR-swizzled by k & 15 (bank-conflict free for both the
 // DMA writes and the operand reads).  v_mfma_f32_16x16x32_bf16 layouts: A lane l = row l%16, k 8*(l/16)..+8;
 // B lane l = column l%16, same k; C lane l = column l%16, rows 4*(l/16)..+4.
 //   S^T = K Q^T  : A = K rows from LDS, B = Q^T (columns = this lane's query token)
@@ -30,7 +31,7 @@ namespace {
 constexpr int kD = 128;
 constexpr int kG = 2;  // query heads per KV head (the softmax below is written for exactly two)
 constexpr int kQT = 64;        // query tokens per workgroup (16 per wave, both heads)
-constexpr int kKT = 64;        // keys per LDS tile
+constexpr int kKT = 32;        // keys per LDS tile
 constexpr int kRowB = kD * 2;  // bytes of one key row in an LDS tile
 constexpr int kTileB = kKT * kRowB;
 
@@ -90,7 +91,8 @@ __device__ __forceinline__ float max_xor16(float x) {
 // counters untouched.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
+// Three waves per SIMD (<= 168 VGPRs): three workgroups per CU hide each other's prologues and barriers.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void prefill_kernel(const PrefillArgs a) {
   // Two stages of K and V tiles; separate arrays so the compiler can tell the stage being filled from the one
   // being read.
   __shared__ __align__(16) uint8_t sK0[kTileB];
@@ -158,15 +160,19 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   // Last key that every token of this wave sees (wave-uniform).
   const int wlim = a.causal ? min(Lk - 1, Lk - Lq + qt * kQT + wave * 16) : Lk - 1;
 
-  // Tile copies.  A 64-key tile is 4 groups of 16 keys and a group never straddles a page (page sizes are
-  // powers of two >= 16), so each group has one uniform base address; wave w copies group w of K and of V with
-  // four direct-to-LDS loads each (instruction i: rows 4i..4i+3 of the group, 1 KiB).  The descriptor covers
+  // Tile copies.  A 32-key tile is 2 groups of 16 keys and a group never straddles a page (page sizes are
+  // powers of two >= 16), so each group has one uniform base address; waves 0 and 1 copy K groups 0 and 1,
+  // waves 2 and 3 the V groups, with four direct-to-LDS loads each (instruction i: rows 4i..4i+3 of the group,
+  // 1 KiB).  The descriptor covers
   // exactly the group's valid rows of head g: rows past the sequence and groups on an invalid page arrive as
   // zeros.  Lane l of instruction i lands at LDS chunk slot l & 15 of row rr = 4i + (l >> 4), so it fetches
   // global chunk (l & 15) ^ rr: the swizzle is applied on the global side.  Page ids come from a lane-wise
   // window (lane i = table entry pwin_base + i), read with v_readlane; it is refilled once per 64 pages.
+  static_assert(kKT == 32 && kQT == 64, "the copy assignment below is for 4 waves and 2 groups per tile");
+  const int cgrp = wave & 1;                     // the 16-key group of a tile this wave copies
+  const uint16_t* cbase = wave < 2 ? a.k : a.v;  // waves 0, 1 copy K; waves 2, 3 copy V
   auto group_rsrc = [&](const uint16_t* base, int t, int page) __attribute__((always_inline)) {
-    const int j0 = t * kKT + 16 * wave;
+    const int j0 = t * kKT + 16 * cgrp;
     const int nv = min(16, Lk - j0);
     bool ok = nv > 0;
     int64_t off = 0;
@@ -187,17 +193,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   auto issue = [&](int t, uint8_t* Kst, uint8_t* Vst) __attribute__((always_inline)) {
     int page = 0;
     if (paged) {
-      const int pi = (t * kKT + 16 * wave) >> a.page_shift;
+      const int pi = (t * kKT + 16 * cgrp) >> a.page_shift;
       if (pi < pwin_base || pi >= pwin_base + 64) load_window(pi & ~63);
       page = readlane(pwin, pi - pwin_base);
     }
-    const __amdgpu_buffer_rsrc_t rk = group_rsrc(a.k, t, page);
-    const __amdgpu_buffer_rsrc_t rv = group_rsrc(a.v, t, page);
+    const __amdgpu_buffer_rsrc_t rc = group_rsrc(cbase, t, page);
+    uint8_t* dst = wave < 2 ? Kst : Vst;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      dma16(rk, Kst + (16 * wave + 4 * i) * kRowB, dma_off[i]);
-      dma16(rv, Vst + (16 * wave + 4 * i) * kRowB, dma_off[i]);
-    }
+    for (int i = 0; i < 4; ++i) dma16(rc, dst + (16 * cgrp + 4 * i) * kRowB, dma_off[i]);
   };
 
   // Operand read offsets.  K (A of S^T): lane (col, g4) reads key kb*16 + col, logical chunk 4kk + g4, stored at
@@ -219,10 +222,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   float m[kG] = {kMaxSeed, kMaxSeed}, l[kG] = {0.f, 0.f};
 
   auto compute = [&](int t, const uint8_t* Ks, const uint8_t* Vs) __attribute__((always_inline)) {
-    // S^T for the tile's 4 blocks of 16 keys, both heads; each K operand is read once.
-    f32x4_t st[kG][4];
+    // S^T for the tile's 2 blocks of 16 keys, both heads; each K operand is read once.
+    f32x4_t st[kG][kKT / 16];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < kKT / 16; ++kb) {
 #pragma unroll
       for (int hh = 0; hh < kG; ++hh) st[hh][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -242,17 +245,17 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
       for (int hh = 0; hh < kG; ++hh)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < kKT / 16; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) st[hh][kb][i] = (kb * 16 + i <= lim) ? st[hh][kb][i] : -INFINITY;
     }
-    bf16x8_t pb[kG][2];
+    bf16x8_t pb[kG][kKT / 32];
     float mx[kG];
 #pragma unroll
     for (int hh = 0; hh < kG; ++hh) {
       mx[hh] = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < kKT / 16; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx[hh] = fmaxf(mx[hh], st[hh][kb][i]);
     }
@@ -278,7 +281,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       // P^T as the B operand: k slot 8*g4 + i <- key 32*s2 + 4*g4 + i, slot 8*g4 + 4 + i <- key
       // 32*s2 + 16 + 4*g4 + i (blocks 2*s2 and 2*s2+1 of this lane's C registers).
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
+      for (int s2 = 0; s2 < kKT / 32; ++s2) {
         float p[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     for (int db = 0; db < 8; ++db) {
       const uint32_t chunk = (uint32_t)((((2 * db) + c_lo) ^ rsw) << 4);
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
+      for (int s2 = 0; s2 < kKT / 32; ++s2) {
         const uint2 lo = ldtr(Vs + v_rd + chunk + (32 * s2) * kRowB);
         const uint2 hi = ldtr(Vs + v_rd + chunk + (32 * s2 + 16) * kRowB);
         const bf16x8_t va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
