@@ -7,6 +7,7 @@ so prefill can read K/V back from the pool.  GPU only.
 """
 from __future__ import annotations
 
+from collections import OrderedDict
 from typing import Optional
 
 import torch
@@ -85,12 +86,14 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     return prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, int(max_seqlen_q), float(scale), bool(causal))
 
 
-_CU_CACHE: dict = {}
+_CU_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_CU_CACHE_MAX = 64
 
 
 def _cu(n: int, length: int, device) -> torch.Tensor:
-    """Cumulative lengths 0, L, 2L, ... nL.  Cached outside graph capture only: a tensor made during a capture
-    lives in that graph's memory pool and must not outlive it or be shared with another graph."""
+    """Cumulative lengths 0, L, 2L, ... nL.  Cached (the 64 most recent shapes) outside graph capture only: a
+    tensor made during a capture lives in that graph's memory pool and must not outlive it or be shared with
+    another graph."""
     if torch.cuda.is_current_stream_capturing():
         return torch.arange(0, (n + 1) * length, length, dtype=torch.int32, device=device)
     key = (n, length, str(device))
@@ -98,6 +101,10 @@ def _cu(n: int, length: int, device) -> torch.Tensor:
     if t is None:
         t = torch.arange(0, (n + 1) * length, length, dtype=torch.int32, device=device)
         _CU_CACHE[key] = t
+        if len(_CU_CACHE) > _CU_CACHE_MAX:
+            _CU_CACHE.popitem(last=False)
+    else:
+        _CU_CACHE.move_to_end(key)
     return t
 
 
