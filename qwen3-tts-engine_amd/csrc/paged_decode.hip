@@ -27,6 +27,9 @@
 // the row attends over cache_seqlens + 1 tokens, and the last one is this step's k/v row.  The wave
 // that consumes a row's last tile swaps that token's registers for the k_new/v_new row, writes the
 // row into the page slot, and attends with the registers; the slot's old contents are never used.
+// In the stream-K kernel a segment's q rows and a row's new k/v rows reach the wave through LDS, copied
+// there together with the tile that needs them (see stage_q), so segment starts and row ends never
+// drain the tile in flight.
 #include "q3a_common.h"
 #include "../../include/q3attn.h"
 
@@ -129,7 +132,8 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, const TileList& 
 // 16 lanes holding it take this step's k/v row instead of the stale slot (its old contents are never
 // used) and store that row into the slot; an invalid page is neither written nor attended (tile_update
 // masks it).  The two row loads are issued here, at consume time, so they never sit in a register across
-// the tile pipeline; the wave waits once per row for them.
+// the tile pipeline; the wave waits once per row for them (the fixed-split kernel, one row end per
+// workgroup; the stream-K kernel stages the rows instead, take_staged_token).
 __device__ __forceinline__ void take_new_token(const DecodeArgs& a, const TileList& L, uint32_t lane_off,
                                                int grp, int g, int j, int row, KVTile& T) {
   const int page = readlane(L.page, j);
@@ -163,6 +167,63 @@ __device__ __forceinline__ void take_new_token(const DecodeArgs& a, const TileLi
   // with nothing outstanding: the loop's own waits then stay at "this tile only" on every tile.
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __builtin_amdgcn_sched_barrier(0);
+}
+
+// ------------------------------------------------------------------------------ segment staging (stream-K)
+// Per wave and tile parity, 1 KiB of LDS receives, by direct-to-LDS copies issued together with a tile's K/V
+// loads, the q rows of the segment the tile opens (both heads, 512 B; the 16 B-per-lane copy also writes
+// zeros over the next 512 B) and, in the append form when the tile ends its row, this step's new k row (at
+// kStageNew) and v row (256 B later).  The consumer reads them after the next tile has been issued, from the
+// other parity's array, so neither a segment start nor a row end waits for the tile in flight.  Every tile
+// issues the q copy (out of bounds when it opens no segment), so each tile puts the same number of operations
+// on vmcnt and the compiler's count-based waits stay exact.
+constexpr int kStageBytes = 1024;
+constexpr int kStageNew = 512;
+constexpr int kMaxWaves = 16;
+constexpr int kWaitGroup = 0x0F70 | 9;  // s_waitcnt vmcnt(9) (expcnt, lgkmcnt untouched)
+
+__device__ __forceinline__ void stage_q(const DecodeArgs& a, int b, int g, int lane, bool valid, uint8_t* st) {
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q + (int64_t)b * a.q_sb + (int64_t)(kG * g) * a.q_sh,
+                                              valid ? (uint32_t)(((kG - 1) * a.q_sh + kD) * 2) : 0u);
+  const uint32_t off = lane < kG * 16 ? (uint32_t)((lane >> 4) * a.q_sh * 2 + (lane & 15) * 16) : kOutOfRange;
+  lds_copy16(rq, st, off);
+}
+
+__device__ __forceinline__ void stage_new_rows(const DecodeArgs& a, int b, int g, int lane, uint8_t* st) {
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2);
+  lds_copy4(rk, st + kStageNew, (uint32_t)lane * 4);
+  lds_copy4(rv, st + kStageNew + kD * 2, (uint32_t)lane * 4);
+}
+
+// Append form, the last tile of a row, read after the next tile was issued: as take_new_token, with the new
+// k/v rows taken from the wave's stage and the slot stores left in flight.
+__device__ __forceinline__ void take_staged_token(const DecodeArgs& a, const TileList& L, uint32_t lane_off,
+                                                  int grp, int j, const uint8_t* st, KVTile& T) {
+  const int page = readlane(L.page, j);
+  const int off = readlane(L.off, j);
+  const int tn = readlane(L.nvalid, j) - 1;
+  const int i_new = tn >> 2;
+  const bool mine = grp == (tn & 3);
+  const bool ok = (unsigned)page < (unsigned)a.num_pages;
+  const int chunk = (int)(threadIdx.x & 15) * 16;
+  const uint4 kn = ld16(st + kStageNew + chunk);
+  const uint4 vn = ld16(st + kStageNew + kD * 2 + chunk);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i == i_new && mine) {
+      T.k[i] = kn;
+      T.v[i] = vn;
+    }
+  }
+  const int64_t pbase = ok ? (int64_t)page * a.kv_sp : 0;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kc + pbase, ok ? a.page_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + pbase, ok ? a.page_bytes : 0u);
+  const uint32_t slot_off = (uint32_t)((off + 4 * i_new) * a.kv_st * 2);
+  if (mine) {
+    buffer_store16_s(kn, rk, lane_off, slot_off);
+    buffer_store16_s(vn, rv, lane_off, slot_off);
+  }
 }
 
 __device__ __forceinline__ uint32_t u4get(const uint4& v, int c) {
@@ -430,6 +491,9 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   __shared__ int s_ctx[kSkMaxRows];
   __shared__ int s_prefix[kSkMaxRows + 1];
   __shared__ int s_wsum[16];
+  // Segment staging, one array per tile parity (see stage_q).
+  __shared__ __align__(16) uint8_t s_stage0[kMaxWaves * kStageBytes];
+  __shared__ __align__(16) uint8_t s_stage1[kMaxWaves * kStageBytes];
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
   const int g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform KV head
@@ -478,11 +542,13 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
   float* part = a.ws + (int64_t)blockIdx.x * kSkSlots * a.hkv * kPartFloats;
 
-  uint4 q[kG], q_next[kG];
+  uint8_t* const st0 = s_stage0 + g * kStageBytes;
+  uint8_t* const st1 = s_stage1 + g * kStageBytes;
+  uint4 q[kG];
   float m[kG], l[kG], acc[kG][8];
   reset_state(m, l, acc);
   int seg_row = 0, seg_flags = 0, seg_slot = 0;
-  q[0] = q[1] = q_next[0] = q_next[1] = make_uint4(0u, 0u, 0u, 0u);
+  q[0] = q[1] = make_uint4(0u, 0u, 0u, 0u);
 
   for (int cb = lo; cb < hi; cb += 64) {
     TileList L;
@@ -511,8 +577,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
                (mt == 0 ? kRowStart : 0) | (mt == ntr - 1 ? kRowEnd : 0);
     }
 
-    // Segment bookkeeping for tile j, run before tile j+1 is issued.  A segment's q was loaded into
-    // q_next together with its first tile (see issue), so opening it costs no extra wait.
+    // Segment bookkeeping for tile j, run before tile j+1 is issued (no memory operand involved).
     auto open_segment = [&](int j) {
       const int fl = readlane(vflags, j);
       if (fl & kFirst) {
@@ -520,14 +585,26 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         seg_flags = fl;
         seg_slot = (cb + j == lo) ? 0 : 1;
         reset_state(m, l, acc);
-        q[0] = q_next[0];
-        q[1] = q_next[1];
       }
     };
-    auto process = [&](KVTile& T, int j) {
+    // Consumes tile j after tile j+1 was issued; the segment's q (and the new k/v rows) come from the stage
+    // array of tile j's parity, which tile j+1's copies do not touch.
+    auto process = [&](KVTile& T, int j, const uint8_t* st) {
       const int fl = readlane(vflags, j);
+      if (fl & (kAppend ? (kFirst | kRowEnd) : kFirst)) {
+        // The compiler does not order LDS reads after these copies by itself: wait until tile j's group
+        // (issued before tile j+1's) has landed.  Tile j+1's group, and the append form's slot stores of
+        // the previous tile, are younger; the count is the smallest group (8 loads and the q copy), so
+        // the wait is exact when the younger operations are one such group and conservative otherwise.
+        __builtin_amdgcn_s_waitcnt(kWaitGroup);
+        __asm__ volatile("" ::: "memory");
+      }
+      if (fl & kFirst) {
+        q[0] = ld16(st + dl * 2);
+        q[1] = ld16(st + kD * 2 + dl * 2);
+      }
       if constexpr (kAppend) {
-        if (fl & kRowEnd) take_new_token(a, L, lane_off, grp, g, j, seg_row, T);
+        if (fl & kRowEnd) take_staged_token(a, L, lane_off, grp, j, st, T);
       }
       tile_update(a, L, q, T, j, grp, m, l, acc);
       if (fl & kLast) {
@@ -541,25 +618,34 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       }
     };
 
-    auto issue = [&](int j, KVTile& T) {
+    auto issue = [&](int j, KVTile& T, uint8_t* st) {
       issue_tile(a, L, lane_off, grp, j, T);
-      if (j < L.n && (readlane(vflags, j) & kFirst)) load_q(a, readlane(vrow, j), g, dl, q_next);
+      const int jj = j < L.n ? j : 0;
+      const int fl = j < L.n ? readlane(vflags, jj) : 0;
+      const int row = readlane(vrow, jj);
+      stage_q(a, row, g, lane, (fl & kFirst) != 0, st);
+      if constexpr (kAppend) {
+        if (fl & kRowEnd) stage_new_rows(a, row, g, lane, st);
+      }
       // Keep the whole tile's loads ahead of the consumer: no instruction of the next tile_update may
       // be scheduled between them (that would wait for the current tile in the middle of the issue).
       __builtin_amdgcn_sched_barrier(0);
     };
 
     KVTile A, Bt;
-    issue(0, A);
+    issue(0, A, st0);
     for (int j = 0; j < L.n; j += 2) {
       open_segment(j);
-      issue(j + 1, Bt);
-      process(A, j);
+      issue(j + 1, Bt, st1);
+      process(A, j, st0);
       if (j + 1 < L.n) open_segment(j + 1);
-      issue(j + 2, A);
-      if (j + 1 < L.n) process(Bt, j + 1);
+      issue(j + 2, A, st0);
+      if (j + 1 < L.n) process(Bt, j + 1, st1);
     }
   }
+  // The last issue() targets tiles past the list; let its (out-of-bounds) copies into LDS land before the
+  // wave ends.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 // One workgroup per row: merges the partial records of rows that straddle workgroup ranges, and

@@ -76,6 +76,18 @@ __device__ __forceinline__ void buffer_store16_s(uint4 v, __amdgpu_buffer_rsrc_t
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)byte_off, (int)s_off, 0);
 }
 
+// Direct-to-LDS copies (buffer_load ... lds): lane i's `bytes` (4 or 16) land at lds + bytes * i, with no
+// register staging; lanes failing the descriptor's bounds write zeros.  `lds` must be wave-uniform.  The
+// copies count on vmcnt like loads, and the compiler's waits before an LDS read cover only the copies into the
+// same __shared__ array, so a copy into one array can stay in flight while another array is read.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t byte_off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, (int)byte_off, 0, 0, 0);
+}
+__device__ __forceinline__ void lds_copy4(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t byte_off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 4, (int)byte_off, 0, 0, 0);
+}
+
 // Streaming variant with the non-temporal hint (`nt`): data read exactly once (the K/V pages of a
 // decode call) bypasses cache retention, which measured ~12% more HBM read bandwidth on MI355X
 // than plain loads for the same access pattern.
