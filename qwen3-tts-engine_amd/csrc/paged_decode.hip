@@ -855,6 +855,10 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   if ((q_stride_b | q_stride_h | kv_stride_page | kv_stride_tok | kv_stride_head | o_stride_b | o_stride_h |
        kn_stride_b | vn_stride_b) % 8 != 0)
     return fail(Q3A_EINVAL, "%s: strides must be multiples of 8 elements (16 bytes)", who);
+  // q's two head rows of a KV group are read through one buffer descriptor with a 32-bit extent.
+  if (q_stride_h <= 0 || ((int64_t)(kG - 1) * q_stride_h + head_dim) * 2 >= ((int64_t)1 << 31))
+    return fail(Q3A_EINVAL, "%s: q head stride %lld unsupported (need > 0, head pair extent < 2 GiB)", who,
+                (long long)q_stride_h);
   if (split_tokens < 0 || split_tokens % kTile != 0)
     return fail(Q3A_EINVAL, "%s: split_tokens %d is not 0 or a positive multiple of %d", who, split_tokens, kTile);
   if (split_tokens > kMaxSplitTokens)

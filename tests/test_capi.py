@@ -55,6 +55,8 @@ def _decode(**kw):
     (dict(max_pages=4096, split=16), "splits exceed"),
     (dict(split=2048), "exceeds 1024"),
     (dict(sh=-128), "page extent"),
+    (dict(q_sh=1 << 30), "q head stride"),
+    (dict(q_sh=-128), "q head stride"),
     (dict(ws_bytes=10), "workspace"),
     (dict(B=-1), "batch"),
 ])
