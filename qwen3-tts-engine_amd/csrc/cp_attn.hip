@@ -11,9 +11,10 @@
 //
 // One wave per (row, KV head).  Scores: lane l takes slot l/4 and a quarter of the head
 // dimension (4 x 16 B loads; the 4 lanes of a slot read 64 contiguous bytes per instruction) and
-// reduces with two quad DPP steps.  P.V: lane l owns output dims 2l, 2l+1 of both query heads and
-// walks the slots; each slot is one 256 B coalesced load and the slot's probability is broadcast
-// with v_readlane.  All loads of the wave are issued before the first use, without branches: the
+// reduces with two quad DPP steps; q is loaded once per wave and handed to those lanes with
+// ds_bpermute.  P.V: lane l owns output dims 2l, 2l+1 of both query heads and walks the slots up to
+// n_live rounded up to a multiple of 4 (one instantiation per multiple); each slot is one 256 B
+// coalesced load and the slot's probability is broadcast with v_readlane.  All loads of the wave are issued before the first use, without branches: the
 // scratch rows go through a buffer descriptor whose extent ends at the last row read, so the loads
 // of dead slots return zeros without touching memory.  Cross-row reductions use the gfx950 lane
 // swaps.
@@ -58,7 +59,16 @@ __device__ __forceinline__ float sum_xor16(float x) { const float2 r = swap16(x)
 __device__ __forceinline__ float max_xor32(float x) { const float2 r = swap32(x); return fmaxf(r.x, r.y); }
 __device__ __forceinline__ float max_xor16(float x) { const float2 r = swap16(x); return fmaxf(r.x, r.y); }
 
-template <bool kAppend>
+// The 16 bytes lane `src` holds (ds_bpermute: the LDS crossbar, no LDS storage).  All lanes must be active.
+__device__ __forceinline__ uint4 bpermute16(const uint4& v, int src) {
+  const int addr = src * 4;
+  return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.x), (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.y),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.z), (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.w));
+}
+
+// kNV: slots whose V rows are loaded and walked by P.V, n_live rounded up to a multiple of 4 (one instantiation
+// each, so every load stays unconditional and the slot loop fully unrolled).
+template <bool kAppend, int kNV>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpArgs a) {
   const int wave = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (wave >= a.pairs) return;
@@ -84,47 +94,49 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, span);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, span);
 
-  // Lane (slot, c) holds dims 32*i + 8*c .. +8 for i = 0..3, of K[slot] and of both query heads.
-  uint4 kr[4], qr[kG][4], kn[4];
-  uint32_t vr[kSlots], vn = 0u;
-#pragma unroll
-  for (int h = 0; h < kG; ++h)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qr[h][i] = ld16(qb + h * kD + 32 * i + 8 * c);
+  // Lane (slot, c) holds dims 32*i + 8*c .. +8 for i = 0..3, of K[slot] and of both query heads.  q (and in
+  // the append form the new k row) is loaded once, one 16 B chunk per lane, and handed to the lanes that need
+  // it with ds_bpermute: loading it per lane would return the same 512 B sixteen times over (8 KiB per wave,
+  // the largest share of the kernel's vector-memory data return).
+  uint4 kr[4], qr[kG][4];
+  uint32_t vr[kNV], vn = 0u;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qb, kG * kD * 2);
+  const uint4 qc = buffer_load16(rq, lane < kG * 16 ? (uint32_t)lane * 16 : kOutOfRange);
 #pragma unroll
   for (int i = 0; i < 4; ++i) kr[i] = buffer_load16(rk, (uint32_t)slot * row_b + (32 * i + 8 * c) * 2);
-  // In the append form the new k row goes to the lanes of slot `last` (the other lanes' offsets are out of
-  // bounds: zeros).
-  const bool mine = kAppend && slot == last;
-  __amdgpu_buffer_rsrc_t rkn = rk, rvn = rv;
-  if constexpr (kAppend) {
-    rkn = make_rsrc(a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD, kD * 2);
-    rvn = make_rsrc(a.v_new + (int64_t)b * a.vn_sb + (int64_t)g * kD, kD * 2);
+  // Append form: lanes 0..15 hold this step's k row, lane l its dims 8l..8l+7.
+  const __amdgpu_buffer_rsrc_t rkn =
+      kAppend ? make_rsrc(a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD, kD * 2) : rk;
+  const __amdgpu_buffer_rsrc_t rvn =
+      kAppend ? make_rsrc(a.v_new + (int64_t)b * a.vn_sb + (int64_t)g * kD, kD * 2) : rv;
+  uint4 knc = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (kAppend) knc = buffer_load16(rkn, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kn[i] = buffer_load16(rkn, mine ? (uint32_t)(32 * i + 8 * c) * 2 : 0x80000000u);
-  }
-#pragma unroll
-  for (int s = 0; s < kSlots; ++s)
+  for (int s = 0; s < kNV; ++s)
     vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, (int)((uint32_t)s * row_b + lane * 4), 0, 0);
   if constexpr (kAppend) vn = __builtin_amdgcn_raw_buffer_load_b32(rvn, lane * 4, 0, 0);
   // Every load is in flight before any is waited for.
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int h = 0; h < kG; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qr[h][i] = bpermute16(qc, 16 * h + 4 * i + c);
   if constexpr (kAppend) {
+    // Slot `last` takes the new k/v rows (its scratch row was not read: out of the descriptor's bounds).
+    const bool mine = slot == last;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      kr[i].x |= kn[i].x;
-      kr[i].y |= kn[i].y;
-      kr[i].z |= kn[i].z;
-      kr[i].w |= kn[i].w;
+      const uint4 kn = bpermute16(knc, 4 * i + c);
+      if (mine) kr[i] = kn;
     }
 #pragma unroll
-    for (int s = 0; s < kSlots; ++s)
+    for (int s = 0; s < kNV; ++s)
       if (s == last) vr[s] = vn;
-    // Slot `last` of the scratch, written with vector buffer stores (lanes of other slots are out of bounds).
+    // Slot `last` of the scratch, written with vector buffer stores (lanes 16..63 of the k store are out of
+    // bounds).
     const __amdgpu_buffer_rsrc_t wk = make_rsrc(kb + (int64_t)last * a.kv_ss, kD * 2);
     const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.kv_ss, kD * 2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) buffer_store16_s(kn[i], wk, mine ? (uint32_t)(32 * i + 8 * c) * 2 : 0x80000000u, 0u);
+    buffer_store16_s(knc, wk, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange, 0u);
     __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, 0);
   }
 
@@ -152,7 +164,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
 #pragma unroll
   for (int h = 0; h < kG; ++h) o[h][0] = o[h][1] = 0.f;
 #pragma unroll
-  for (int s = 0; s < kSlots; ++s) {
+  for (int s = 0; s < kNV; ++s) {
     const float lo = bf16_lo(vr[s]);
     const float hi = bf16_hi(vr[s]);
 #pragma unroll
@@ -215,12 +227,20 @@ static int cp_launch(const void* q, int64_t q_stride_b, void* k, void* v, int64_
   a.n_live = n_live;
   a.scale_log2 = softmax_scale * kLog2e;
   const int blocks = (int)((pairs + kWavesPerBlock - 1) / kWavesPerBlock);
-  if (k_new != nullptr)
-    hipLaunchKernelGGL(cp_attn_kernel<true>, dim3(blocks), dim3(64 * kWavesPerBlock), 0,
-                       static_cast<hipStream_t>(stream), a);
-  else
-    hipLaunchKernelGGL(cp_attn_kernel<false>, dim3(blocks), dim3(64 * kWavesPerBlock), 0,
-                       static_cast<hipStream_t>(stream), a);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(blocks), block(64 * kWavesPerBlock);
+  const int nv = (n_live + 3) / 4;
+  if (k_new != nullptr) {
+    if (nv == 1) hipLaunchKernelGGL((cp_attn_kernel<true, 4>), grid, block, 0, st, a);
+    else if (nv == 2) hipLaunchKernelGGL((cp_attn_kernel<true, 8>), grid, block, 0, st, a);
+    else if (nv == 3) hipLaunchKernelGGL((cp_attn_kernel<true, 12>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((cp_attn_kernel<true, 16>), grid, block, 0, st, a);
+  } else {
+    if (nv == 1) hipLaunchKernelGGL((cp_attn_kernel<false, 4>), grid, block, 0, st, a);
+    else if (nv == 2) hipLaunchKernelGGL((cp_attn_kernel<false, 8>), grid, block, 0, st, a);
+    else if (nv == 3) hipLaunchKernelGGL((cp_attn_kernel<false, 12>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((cp_attn_kernel<false, 16>), grid, block, 0, st, a);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   return Q3A_OK;
