@@ -113,7 +113,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   if constexpr (kAppend) knc = buffer_load16(rkn, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange);
 #pragma unroll
   for (int s = 0; s < kNV; ++s)
-    vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, (int)((uint32_t)s * row_b + lane * 4), 0, 0);
+    vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, (int)((uint32_t)s * row_b), 0);
   if constexpr (kAppend) vn = __builtin_amdgcn_raw_buffer_load_b32(rvn, lane * 4, 0, 0);
   // Every load is in flight before any is waited for.
   __builtin_amdgcn_sched_barrier(0);
@@ -157,7 +157,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
     const float mx = max_xor32(max_xor16(quads_max(x)));
     const float e = fast_exp2(x - mx);
     const float z = sum_xor32(sum_xor16(quads_sum(e)));
-    p[h] = round_bf16(e / z);
+    // z >= 1 (the max slot contributes exp2(0)), so the reciprocal is well conditioned.
+    p[h] = round_bf16(e * __builtin_amdgcn_rcpf(z));
   }
 
   float o[kG][2];
