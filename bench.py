@@ -6,7 +6,7 @@ ctx = 0, GQA 16/8, head_dim 128, bf16, 16-token pages, every layer with its own 
 page table over one 131,072-page pool (8.59 GB of K+V).  Inputs are resident in HBM before the
 timed region.  Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--workload c5|c3|c2|c4|admit]
 """
 from __future__ import annotations
 
@@ -391,13 +391,60 @@ def bench_prefill(args, dev):
     return rec
 
 
+def bench_admit(args, dev):
+    """Fast-admission prefill (engine/arrivals.py:133-152): S = 8 sequences (the largest graphed bucket) of R = 42 new
+    tokens over a 35-token shared prefix (n = 77 keys), bottom-right causal (engine/arrivals.py:148), 28 layers per
+    step, each layer with its own q/k/v."""
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    S, R, n = 8, 42, 77
+    wls = [W.make_admit(dev, S, R, n, seed=args.seed + l) for l in range(LAYERS)]
+    w0 = wls[0]
+
+    def call(wl):
+        return q3attn.flash_attn_func(wl.q, wl.k, wl.v, softmax_scale=wl.scale, causal=True)
+
+    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [call(wl) for wl in wls], args.steps, args.warmup)
+    call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
+    tflops = w0.flops() / (call_us * 1e-6) / 1e12
+    log(f"[bench] admission prefill S={S} R={R} n={n}: {call_us:.2f} us/call, {tflops:.1f} TFLOP/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.torch_cpu import prefill_prefix_rows
+        q, K, V = w0.q.float().cpu(), w0.k.float().cpu(), w0.v.float().cpu()
+        times = []
+        for rep in range(5):
+            t0 = time.perf_counter()
+            prefill_prefix_rows(q, K, V, w0.scale)
+            times.append(time.perf_counter() - t0)
+        us = statistics.median(times) * 1e6
+        cpu = {"value": round(us * LAYERS, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"layer 0 with the reference's fp32 torch form (engine/arrivals.py:125-131), median of 5 = "
+                         f"{us:.0f} us, x{LAYERS} layers"}
+    rec = base_record(f"fast-admission prefill attn µs/step (28 layers) at S={S}, R={R}, n={n}, 1×MI355X",
+                      round(ms_per_step * 1e3, 2), "us/step", args, ms_per_step, False,
+                      {"workload": f"fast-admission prefill: {S} sequences of {R} new tokens over a {n - R}-token "
+                                   f"shared prefix, bottom-right causal, GQA 16/8, head_dim 128, bf16, 28 layers",
+                       "parallelism": "single GPU"})
+    rec.update({"us_per_layer_call": round(call_us, 2), "tflops": round(tflops, 2),
+                "roofline": {"bound": "latency (155 MFLOP and 1.4 MB per call)", "achieved": round(tflops, 2),
+                             "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                             "flops_per_call": w0.flops()},
+                "cpu_baseline": cpu})
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c5", choices=["c5", "c3", "c2", "c4"],
-                    help="c5 (default, the headline metric), c3 decode, c2 code predictor, c4 prefill")
+    ap.add_argument("--workload", default="c5", choices=["c5", "c3", "c2", "c4", "admit"],
+                    help="c5 (default, the headline metric), c3 decode, c2 code predictor, c4 prefill, "
+                         "admit fast-admission prefill")
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-append", action="store_true", help="skip the KV-append comparison of the decode bench")
@@ -429,6 +476,8 @@ def main() -> int:
         rec = bench_decode(args, dev, args.workload)
     elif args.workload == "c2":
         rec = bench_cp(args, dev)
+    elif args.workload == "admit":
+        rec = bench_admit(args, dev)
     else:
         rec = bench_prefill(args, dev)
     print(json.dumps(rec), flush=True)

@@ -139,8 +139,9 @@ int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void* k_new, int
  * Talker prefill attention (packed variable-length, MFMA).
  *
  * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, ..., causal=True) at
- * engine/talker.py:169 (fp32 form engine/talker.py:163-167) and the prefix + new flash_attn_func(q, K, V,
- * causal=True) of engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131).
+ * engine/talker.py:169 (fp32 form engine/talker.py:163-167); with cu_seqlens_k != cu_seqlens_q it also covers
+ * prefix + new sequences packed by length (the dense flash_attn_func of engine/arrivals.py:148 is
+ * q3a_prefill_dense below).
  *
  *   q       [T, Hq, D] bf16, token stride q_stride_t, head stride q_stride_h; sequence s owns tokens
  *           cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1
@@ -160,6 +161,23 @@ int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int
                 int64_t bt_stride_b, int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out,
                 int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads,
                 int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream);
+
+/*
+ * Prefix + new prefill attention on dense [S, R, H, D] tensors (MFMA): the layout flash_attn_func takes at
+ * engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131), with no cumulative-length arrays.
+ *
+ *   q    [S, Lq, Hq, D] bf16 (sequence/token/head strides q_stride_s/t/h), Lq = seqlen_q
+ *   k, v [S, Lk, Hkv, D] bf16 (kv_stride_s/t/h), Lk = seqlen_k
+ *   out  [S, Lq, Hq, D] bf16 (o_stride_s/t/h)
+ * With causal != 0, query i sees keys j <= Lk - Lq + i (bottom-right aligned).  Query rows that see no key are
+ * zeros.  Requirements as in q3a_prefill (D == 128, Hq == 2*Hkv, 16-byte aligned rows, strides multiples of 8
+ * elements, K/V token stride in [D, 2^26]); sequence strides non-negative.
+ */
+int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h, const void* k,
+                      const void* v, int64_t kv_stride_s, int64_t kv_stride_t, int64_t kv_stride_h, void* out,
+                      int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int seqlen_q,
+                      int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                      int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -58,3 +58,17 @@ def prefill_rows(q, k, v, cu_seqlens, scale):
         a = torch.matmul(qh, kh.transpose(-1, -2)) * scale + torch.full((L, L), float("-inf")).triu(1)
         out[s0:s1] = torch.matmul(torch.softmax(a, dim=-1), vh).reshape(Hq, L, D).transpose(0, 1)
     return out
+
+
+def prefill_prefix_rows(q, K, V, scale):
+    """``FastAdmit._attn_ref`` (engine/arrivals.py:125-131) on CPU fp32 tensors: q [S, R, 16, 128] attends over
+    K/V [S, n, 8, 128], query i seeing the n - R prefix keys and the new keys <= i (mask triu(n - R + 1)).
+    Returns [S, R, 16, 128]."""
+    S, R, Hq, D = q.shape
+    n, Hkv = K.shape[1], K.shape[2]
+    m = torch.full((R, n), float("-inf")).triu(n - R + 1)
+    qh = q.permute(0, 2, 1, 3).reshape(S, Hkv, Hq // Hkv, R, D)
+    Kh = K.permute(0, 2, 1, 3)[:, :, None]
+    Vh = V.permute(0, 2, 1, 3)[:, :, None]
+    a = torch.matmul(qh, Kh.transpose(-1, -2)) * scale + m
+    return torch.matmul(torch.softmax(a, dim=-1), Vh).reshape(S, Hq, R, D).permute(0, 2, 1, 3)

@@ -3,7 +3,9 @@
 // Semantics: packed variable-length causal attention.  Sequence s owns query tokens
 // [cu_q[s], cu_q[s+1]) of q [T, Hq, D] and keys 0..Lk-1 with Lk = cu_k[s+1] - cu_k[s], read either
 // from a packed [Tk, Hkv, D] tensor (token j at row cu_k[s] + j) or from the paged KV pool
-// (token j at page block_table[s][j / page_size], offset j % page_size).  With `causal`, query i
+// (token j at page block_table[s][j / page_size], offset j % page_size).  Without cu arrays (the dense
+// form of flash_attn_func) every sequence has Lq = seqlen_q, Lk = seqlen_k and starts at s times the
+// sequence stride of q, K/V and out.  With `causal`, query i
 // sees keys j <= Lk - Lq + i (bottom-right alignment).  This covers flash_attn_varlen_func at
 // engine/talker.py:169 (cu_q == cu_k, fp32 form engine/talker.py:163-167), the prefix + new form
 // of flash_attn_func at engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131), and both
@@ -53,6 +55,9 @@ struct PrefillArgs {
   const int32_t* cu_k;
   uint16_t* out;
   int64_t o_st, o_sh;
+  // Dense form (cu_q == nullptr): sequence strides and the common lengths.
+  int64_t q_ss, kv_ss, o_ss;
+  int dense_lq, dense_lk;
   int causal;
   int hkv;
   float scale_log2;
@@ -126,11 +131,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   };
   if (paged) load_window(0);
 
-  const int q0 = a.cu_q[s];
-  const int Lq = a.cu_q[s + 1] - q0;
+  // Element offsets of the sequence's first query/output row and first packed key row.
+  int Lq, Lk;
+  int64_t qbase, obase, kbase;
+  if (a.cu_q != nullptr) {
+    const int q0 = a.cu_q[s];
+    const int k0 = a.cu_k[s];
+    Lq = a.cu_q[s + 1] - q0;
+    Lk = a.cu_k[s + 1] - k0;
+    qbase = (int64_t)q0 * a.q_st;
+    obase = (int64_t)q0 * a.o_st;
+    kbase = (int64_t)k0 * a.kv_st;
+  } else {
+    Lq = a.dense_lq;
+    Lk = a.dense_lk;
+    qbase = (int64_t)s * a.q_ss;
+    obase = (int64_t)s * a.o_ss;
+    kbase = (int64_t)s * a.kv_ss;
+  }
   if (qt * kQT >= Lq) return;
-  const int k0 = a.cu_k[s];
-  int Lk = a.cu_k[s + 1] - k0;
   if (a.bt != nullptr) Lk = min(Lk, a.max_pages * a.page_size);
   Lk = max(Lk, 0);
 
@@ -145,7 +164,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       uint4 x = make_uint4(0u, 0u, 0u, 0u);
-      if (qvalid) x = ld16(a.q + (int64_t)(q0 + tq) * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
+      if (qvalid) x = ld16(a.q + qbase + (int64_t)tq * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
       qb[hh][kk] = as_bf16x8(x);
     }
   }
@@ -180,7 +199,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       ok = ok && (unsigned)page < (unsigned)a.num_pages;
       off = (int64_t)page * a.kv_sp + (int64_t)(j0 & (a.page_size - 1)) * a.kv_st;
     } else {
-      off = (int64_t)(k0 + j0) * a.kv_st;
+      off = kbase + (int64_t)j0 * a.kv_st;
     }
     return make_rsrc(base + (ok ? off : 0) + (int64_t)g * a.kv_sh, ok ? (uint32_t)(((nv - 1) * a.kv_st + kD) * 2) : 0u);
   };
@@ -342,7 +361,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     lt += __shfl_xor(lt, 32);
     if (qvalid) {
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      uint16_t* o = a.out + (int64_t)(q0 + tq) * a.o_st + (kG * g + hh) * a.o_sh + 4 * g4;
+      uint16_t* o = a.out + obase + (int64_t)tq * a.o_st + (kG * g + hh) * a.o_sh + 4 * g4;
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         uint2 w;
@@ -359,6 +378,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
 using namespace q3a;
 
+// Checks shared by both entry points; returns Q3A_OK or an error code with the message set.
+static int check_common(const void* q, const void* k, const void* v, const void* out, int64_t q_st, int64_t q_sh,
+                        int64_t kv_st, int64_t kv_sh, int64_t o_st, int64_t o_sh, int num_q_heads, int num_kv_heads,
+                        int head_dim, const char* who) {
+  if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
+  if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
+    return fail(Q3A_EINVAL, "%s: num_q_heads %d must be %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
+  if (!q || !k || !v || !out) return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;
+  if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: q/k/v/out must be 16-byte aligned", who);
+  if ((q_st | q_sh | kv_st | kv_sh | o_st | o_sh) % 8 != 0)
+    return fail(Q3A_EINVAL, "%s: strides must be multiples of 8 elements (16 bytes)", who);
+  if (kv_st < head_dim || kv_sh < 0 || kv_st > ((int64_t)1 << 26))
+    return fail(Q3A_EINVAL, "%s: token stride %lld must be in [head_dim, 2^26] and head stride >= 0", who,
+                (long long)kv_st);
+  return Q3A_OK;
+}
+
+static int launch(const PrefillArgs& a, int num_seqs, int max_seqlen_q, void* stream, const char* who) {
+  const int nqt = (max_seqlen_q + kQT - 1) / kQT;
+  if ((int64_t)num_seqs * a.hkv > 0x7fffffff || nqt > 65535)
+    return fail(Q3A_EINVAL, "%s: grid too large (%d seqs x %d KV heads x %d query tiles)", who, num_seqs, a.hkv,
+                nqt);
+  hipLaunchKernelGGL(prefill_kernel, dim3(num_seqs * a.hkv, 1, nqt), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+  return Q3A_OK;
+}
+
 extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
                            const void* k, const void* v, int64_t kv_stride_page, int64_t kv_stride_tok,
                            int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
@@ -368,17 +417,10 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
                            void* stream) {
   if (num_seqs < 0 || max_seqlen_q < 0) return fail(Q3A_EINVAL, "prefill: negative num_seqs/max_seqlen_q");
   if (num_seqs == 0 || max_seqlen_q == 0) return Q3A_OK;
-  if (head_dim != kD) return fail(Q3A_EINVAL, "prefill: head_dim %d unsupported (need %d)", head_dim, kD);
-  if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
-    return fail(Q3A_EINVAL, "prefill: num_q_heads %d must be %d * num_kv_heads %d", num_q_heads, kG, num_kv_heads);
-  if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out) return fail(Q3A_EINVAL, "prefill: null pointer argument");
-  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;
-  if (align % 16 != 0) return fail(Q3A_EINVAL, "prefill: q/k/v/out must be 16-byte aligned");
-  if ((q_stride_t | q_stride_h | kv_stride_tok | kv_stride_head | o_stride_t | o_stride_h) % 8 != 0)
-    return fail(Q3A_EINVAL, "prefill: strides must be multiples of 8 elements (16 bytes)");
-  if (kv_stride_tok < head_dim || kv_stride_head < 0 || kv_stride_tok > ((int64_t)1 << 26))
-    return fail(Q3A_EINVAL, "prefill: token stride %lld must be in [head_dim, 2^26] and head stride >= 0",
-                (long long)kv_stride_tok);
+  if (!cu_seqlens_q || !cu_seqlens_k) return fail(Q3A_EINVAL, "prefill: null pointer argument");
+  int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, kv_stride_tok, kv_stride_head, o_stride_t, o_stride_h,
+                        num_q_heads, num_kv_heads, head_dim, "prefill");
+  if (rc != Q3A_OK) return rc;
   if (block_table != nullptr) {
     if (page_size <= 0 || num_pages <= 0 || max_pages_per_seq <= 0)
       return fail(Q3A_EINVAL, "prefill: paged K/V needs page_size, num_pages and max_pages_per_seq > 0");
@@ -386,12 +428,8 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
     if (page_size < 16 || (page_size & (page_size - 1)) != 0)
       return fail(Q3A_EINVAL, "prefill: page_size %d must be a power of two >= 16", page_size);
   }
-  const int nqt = (max_seqlen_q + kQT - 1) / kQT;
-  if ((int64_t)num_seqs * num_kv_heads > 0x7fffffff || nqt > 65535)
-    return fail(Q3A_EINVAL, "prefill: grid too large (%d seqs x %d KV heads x %d query tiles)", num_seqs,
-                num_kv_heads, nqt);
 
-  PrefillArgs a;
+  PrefillArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_t;
   a.q_sh = q_stride_h;
@@ -415,9 +453,44 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
   a.causal = causal ? 1 : 0;
   a.scale_log2 = softmax_scale * kLog2e;
   a.hkv = num_kv_heads;
-  hipLaunchKernelGGL(prefill_kernel, dim3(num_seqs * num_kv_heads, 1, nqt), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "prefill: launch failed: %s", hipGetErrorString(e));
-  return Q3A_OK;
+  return launch(a, num_seqs, max_seqlen_q, stream, "prefill");
+}
+
+extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
+                                 const void* k, const void* v, int64_t kv_stride_s, int64_t kv_stride_t,
+                                 int64_t kv_stride_h, void* out, int64_t o_stride_s, int64_t o_stride_t,
+                                 int64_t o_stride_h, int num_seqs, int seqlen_q, int seqlen_k, int num_q_heads,
+                                 int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream) {
+  if (num_seqs < 0 || seqlen_q < 0 || seqlen_k < 0)
+    return fail(Q3A_EINVAL, "prefill_dense: negative num_seqs/seqlen_q/seqlen_k");
+  if (num_seqs == 0 || seqlen_q == 0) return Q3A_OK;
+  int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, kv_stride_t, kv_stride_h, o_stride_t, o_stride_h,
+                        num_q_heads, num_kv_heads, head_dim, "prefill_dense");
+  if (rc != Q3A_OK) return rc;
+  if ((q_stride_s | kv_stride_s | o_stride_s) % 8 != 0 || q_stride_s < 0 || kv_stride_s < 0 || o_stride_s < 0)
+    return fail(Q3A_EINVAL, "prefill_dense: sequence strides must be non-negative multiples of 8 elements");
+
+  PrefillArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.q_ss = q_stride_s;
+  a.cu_q = nullptr;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.kv_st = kv_stride_t;
+  a.kv_sh = kv_stride_h;
+  a.kv_ss = kv_stride_s;
+  a.bt = nullptr;
+  a.cu_k = nullptr;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_st = o_stride_t;
+  a.o_sh = o_stride_h;
+  a.o_ss = o_stride_s;
+  a.dense_lq = seqlen_q;
+  a.dense_lk = seqlen_k;
+  a.causal = causal ? 1 : 0;
+  a.scale_log2 = softmax_scale * kLog2e;
+  a.hkv = num_kv_heads;
+  return launch(a, num_seqs, seqlen_q, stream, "prefill_dense");
 }

@@ -14,4 +14,4 @@ from ._lib import LIB_PATH, Q3AttnError, lib  # noqa: F401
 from .cp_attn import cp_attn, cp_attn_append, cp_attn_append_op, cp_attn_op  # noqa: F401
 from .ops import flash_attn_with_kvcache, paged_decode, paged_decode_append  # noqa: F401
 from .pages import PagePool, PoolExhausted  # noqa: F401
-from .prefill import flash_attn_func, flash_attn_varlen_func, prefill  # noqa: F401
+from .prefill import flash_attn_func, flash_attn_varlen_func, prefill, prefill_dense  # noqa: F401

@@ -69,6 +69,13 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int,                # num_seqs, max_seqlen_q, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
     ]),
+    "q3a_prefill_dense": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # q, q strides (seq, tok, head)
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k, v, kv strides (seq, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # out, o strides (seq, tok, head)
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, seqlen_k, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
+    ]),
 }
 
 _lock = threading.Lock()

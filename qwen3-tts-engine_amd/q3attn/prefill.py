@@ -7,7 +7,6 @@ so prefill can read K/V back from the pool.  GPU only.
 """
 from __future__ import annotations
 
-from collections import OrderedDict
 from typing import Optional
 
 import torch
@@ -86,26 +85,34 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     return prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, int(max_seqlen_q), float(scale), bool(causal))
 
 
-_CU_CACHE: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
-_CU_CACHE_MAX = 64
+@torch.library.custom_op("q3attn::prefill_dense", mutates_args=())
+def prefill_dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale: float,
+                  causal: bool) -> torch.Tensor:
+    """q [S, R, Hq, D]; k, v [S, n, Hkv, D] (any strides with a contiguous head dim).  Returns [S, R, Hq, D] bf16."""
+    _req(q.is_cuda, "q3attn.flash_attn_func: tensors must be on a GPU (there is no CPU path)")
+    _req(k.device == q.device and v.device == q.device, "q3attn.flash_attn_func: q, k, v must share a device")
+    _req(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
+         "q3attn.flash_attn_func: q, k, v must be bfloat16")
+    _req(q.dim() == 4 and k.dim() == 4 and k.shape == v.shape and k.stride() == v.stride()
+         and q.shape[0] == k.shape[0] and q.shape[3] == k.shape[3],
+         "q3attn.flash_attn_func: q [S,R,H,D], k/v [S,n,Hkv,D] with equal k/v strides")
+    _req(q.stride(3) == 1 and k.stride(3) == 1, "q3attn.flash_attn_func: head_dim must be contiguous")
+    S, R, Hq, D = q.shape
+    n, Hkv = k.shape[1], k.shape[2]
+    out = torch.empty((S, R, Hq, D), dtype=q.dtype, device=q.device)
+    if S == 0 or R == 0:
+        return out
+    rc = lib().q3a_prefill_dense(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+        k.stride(2), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), S, R, n, Hq, Hkv, D,
+        float(softmax_scale), 1 if causal else 0, torch.cuda.current_stream(q.device).cuda_stream)
+    check(rc, "q3a_prefill_dense")
+    return out
 
 
-def _cu(n: int, length: int, device) -> torch.Tensor:
-    """Cumulative lengths 0, L, 2L, ... nL.  Cached (the 64 most recent shapes) outside graph capture only: a
-    tensor made during a capture lives in that graph's memory pool and must not outlive it or be shared with
-    another graph."""
-    if torch.cuda.is_current_stream_capturing():
-        return torch.arange(0, (n + 1) * length, length, dtype=torch.int32, device=device)
-    key = (n, length, str(device))
-    t = _CU_CACHE.get(key)
-    if t is None:
-        t = torch.arange(0, (n + 1) * length, length, dtype=torch.int32, device=device)
-        _CU_CACHE[key] = t
-        if len(_CU_CACHE) > _CU_CACHE_MAX:
-            _CU_CACHE.popitem(last=False)
-    else:
-        _CU_CACHE.move_to_end(key)
-    return t
+@prefill_dense.register_fake
+def _prefill_dense_fake(q, k, v, softmax_scale, causal):
+    return q.new_empty(q.shape)
 
 
 def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
@@ -114,16 +121,5 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False, wi
     q [S, R, Hq, D], k/v [S, n, Hkv, D]; with ``causal`` query i sees the n - R prefix keys and the new keys
     <= i (bottom-right).  Returns [S, R, Hq, D]."""
     _unsupported(dropout_p, window_size, softcap, alibi_slopes, return_attn_probs)
-    _req(q.dim() == 4 and k.dim() == 4 and k.shape == v.shape, "q3attn.flash_attn_func: q [S,R,H,D], k/v [S,n,Hkv,D]")
-    S, R, Hq, D = q.shape
-    n = k.shape[1]
-    if q.stride(0) != R * q.stride(1):
-        q = q.contiguous()
-    if k.stride(0) != n * k.stride(1):
-        k = k.contiguous()
-    if v.stride(0) != n * v.stride(1):
-        v = v.contiguous()
-    scale = softmax_scale if softmax_scale is not None else D ** -0.5
-    o = prefill(q.reshape(S * R, Hq, D), k.reshape(S * n, k.shape[2], D), v.reshape(S * n, v.shape[2], D),
-                _cu(S, R, q.device), _cu(S, n, q.device), None, R, float(scale), bool(causal))
-    return o.view(S, R, Hq, D)
+    scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
+    return prefill_dense(q, k, v, float(scale), bool(causal))

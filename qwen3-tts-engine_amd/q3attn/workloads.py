@@ -12,6 +12,8 @@ Decode workloads (16 query heads over 8 KV heads, head_dim 128, pages of 16 toke
     ctx = 0 at the tail, random table over a 131,072-page pool.
 The code-predictor workload ``c2`` is 512 rows with dense 16-slot K/V buffers (5 layers x 16 steps).
 Prefill workload ``c4``: 32 sequences of U[150, 400] tokens packed, causal, K/V through the page pool.
+Admission workload (``make_admit``): the fast-admission prefill of engine/arrivals.py:133-152, S sequences of R new
+tokens over a shared prefix, q [S, R, 16, 128] against K/V [S, n, 8, 128] (n = prefix + R), bottom-right causal.
 """
 from __future__ import annotations
 
@@ -245,3 +247,33 @@ def make_prefill(device, lens, seed: int = 0, paged: bool = True, page: int = PA
         wl.k_cache, wl.v_cache = kc, vc
         wl.block_table = torch.from_numpy(bt.astype(np.int32)).to(device)
     return wl
+
+
+@dataclasses.dataclass
+class AdmitWorkload:
+    q: torch.Tensor              # [S, R, Hq, D] bf16: the new tokens, positions n - R .. n - 1
+    k: torch.Tensor              # [S, n, Hkv, D] bf16: prefix + new tokens, positions 0 .. n - 1
+    v: torch.Tensor
+    scale: float = HEAD_DIM ** -0.5
+
+    def flops(self) -> int:
+        """QK^T and PV over the keys each new token sees (n - R prefix keys plus the new ones up to itself)."""
+        S, R = self.q.shape[0], self.q.shape[1]
+        n = self.k.shape[1]
+        seen = R * (n - R) + R * (R + 1) // 2
+        return 4 * HEAD_DIM * HQ * S * seen
+
+
+def make_admit(device, S: int, R: int, n: int, seed: int = 0) -> AdmitWorkload:
+    """Fast-admission prefill inputs (engine/arrivals.py:112-118, 148): each sequence's K carries RoPE at positions
+    0..n-1 and q at the new tokens' positions n-R..n-1."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    cos, sin = rope_tables(n, device)
+    q = _rope(_unit_rms(torch.randn((S, R, HQ, HEAD_DIM), generator=gen, device=device)),
+              cos[n - R:][None, :, None], sin[n - R:][None, :, None])
+    k = _rope(_unit_rms(torch.randn((S, n, HKV, HEAD_DIM), generator=gen, device=device)),
+              cos[None, :, None], sin[None, :, None])
+    v = torch.randn((S, n, HKV, HEAD_DIM), generator=gen, device=device)
+    return AdmitWorkload(q=q.to(torch.bfloat16), k=k.to(torch.bfloat16), v=v.to(torch.bfloat16))

@@ -124,6 +124,10 @@ def test_python_entry_points_refuse_cpu_tensors():
         q3attn.cp_attn(torch.zeros(2, 16, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16),
                        torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16), 3, 0.1)
     with pytest.raises(RuntimeError, match="GPU"):
+        q3attn.flash_attn_func(torch.zeros(2, 5, 16, 128, dtype=torch.bfloat16),
+                               torch.zeros(2, 9, 8, 128, dtype=torch.bfloat16),
+                               torch.zeros(2, 9, 8, 128, dtype=torch.bfloat16), causal=True)
+    with pytest.raises(RuntimeError, match="GPU"):
         q3attn.cp_attn_append(torch.zeros(2, 16, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 128, dtype=torch.bfloat16),
                               torch.zeros(2, 8, 128, dtype=torch.bfloat16), torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16),
                               torch.zeros(2, 8, 16, 128, dtype=torch.bfloat16), 2, 0.1)
@@ -177,7 +181,34 @@ def test_fake_impl_traces_shapes():
         c = torch.ops.q3attn.cp_attn(q, torch.empty(3, 8, 16, 128, dtype=torch.bfloat16),
                                      torch.empty(3, 8, 16, 128, dtype=torch.bfloat16), 4, 0.1)
         assert c.shape == (3, 2048)
+        p = torch.ops.q3attn.prefill_dense(torch.empty(2, 5, 16, 128, dtype=torch.bfloat16),
+                                           torch.empty(2, 9, 8, 128, dtype=torch.bfloat16),
+                                           torch.empty(2, 9, 8, 128, dtype=torch.bfloat16), 0.1, True)
+        assert p.shape == (2, 5, 16, 128)
         kv = torch.empty(3, 8, 128, dtype=torch.bfloat16)
         c = torch.ops.q3attn.cp_attn_append(q, kv, kv, torch.empty(3, 8, 16, 128, dtype=torch.bfloat16),
                                             torch.empty(3, 8, 16, 128, dtype=torch.bfloat16), 4, 0.1)
         assert c.shape == (3, 2048)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(D=64), "head_dim"), (dict(Hq=8), "num_q_heads"), (dict(q=None), "null pointer"), (dict(k=18), "aligned"),
+    (dict(q_st=2050), "strides"), (dict(kv_st=64), "token stride"), (dict(q_ss=-2048), "sequence strides"),
+    (dict(o_ss=12), "sequence strides"), (dict(Lk=-1), "negative"), (dict(S=-1), "negative"),
+])
+def test_prefill_dense_rejects_bad_arguments(kw, frag):
+    a = dict(q=16, q_ss=42 * 2048, q_st=2048, q_sh=128, k=16, v=16, kv_ss=77 * 1024, kv_st=1024, kv_sh=128, out=16,
+             o_ss=42 * 2048, o_st=2048, o_sh=128, S=8, Lq=42, Lk=77, Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
+    a.update(kw)
+    rc = _lib.lib().q3a_prefill_dense(a["q"], a["q_ss"], a["q_st"], a["q_sh"], a["k"], a["v"], a["kv_ss"], a["kv_st"],
+                                      a["kv_sh"], a["out"], a["o_ss"], a["o_st"], a["o_sh"], a["S"], a["Lq"], a["Lk"],
+                                      a["Hq"], a["Hkv"], a["D"], a["scale"], a["causal"], None)
+    assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_prefill_dense_empty_is_a_noop():
+    L = _lib.lib()
+    assert L.q3a_prefill_dense(16, 0, 2048, 128, 16, 16, 0, 1024, 128, 16, 0, 2048, 128, 0, 42, 77, 16, 8, 128, 0.1, 1,
+                               None) == 0
+    assert L.q3a_prefill_dense(16, 0, 2048, 128, 16, 16, 0, 1024, 128, 16, 0, 2048, 128, 8, 0, 77, 16, 8, 128, 0.1, 1,
+                               None) == 0

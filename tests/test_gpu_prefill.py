@@ -124,3 +124,42 @@ def test_graph_capture_prefill(cuda_device):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(static, eager)
+
+
+def test_flash_attn_func_strided_views(cuda_device):
+    """q, K, V as views into wider tensors (the engine slices them out of projection outputs): the dense entry
+    point reads them through their strides, no copies."""
+    g = torch.Generator(device=cuda_device).manual_seed(11)
+    S, R, n = 3, 42, 77
+    qbig = torch.randn(S, R, 24, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    kvbig = torch.randn(S, n + 5, 2, 12, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    q, K, V = qbig[:, :, 4:20], kvbig[:, 5:, 0, 2:10], kvbig[:, 5:, 1, 2:10]
+    assert not q.is_contiguous() and not K.is_contiguous()
+    out = q3attn.flash_attn_func(q, K, V, softmax_scale=128 ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    check(out, ora.prefill_prefix(to_np(q), to_np(K), to_np(V), 128 ** -0.5), "strided prefix views")
+    out_c = q3attn.flash_attn_func(q.contiguous(), K.contiguous(), V.contiguous(), softmax_scale=128 ** -0.5,
+                                   causal=True)
+    assert torch.equal(out, out_c)
+
+
+def test_graph_capture_flash_attn_func(cuda_device):
+    """The admission path captures flash_attn_func in graphs (engine/arrivals.py:133-166): replays equal the eager
+    result, with other work between replays."""
+    wl = W.make_admit(cuda_device, 4, 42, 77, seed=12)
+    f = lambda: q3attn.flash_attn_func(wl.q, wl.k, wl.v, softmax_scale=wl.scale, causal=True)
+    eager = f().clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        f()
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s):
+        static = f()
+    for _ in range(3):
+        torch.randn(1 << 18, device=cuda_device)
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static, eager)
+    check(eager, ora.prefill_prefix(to_np(wl.q), to_np(wl.k), to_np(wl.v), wl.scale), "admission shape")

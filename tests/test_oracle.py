@@ -300,3 +300,8 @@ def test_cpu_baseline_ports_agree_with_oracle():
     vp = _bf16(r.standard_normal((23, 8, 32)))
     got = tc.prefill_rows(torch.from_numpy(qp), torch.from_numpy(kp), torch.from_numpy(vp), cu, 0.2).numpy()
     np.testing.assert_allclose(got, ora.prefill_varlen(qp, kp, vp, cu, 0.2), atol=2e-6)
+    qa = _bf16(r.standard_normal((2, 5, 16, 32)))
+    Ka = _bf16(r.standard_normal((2, 9, 8, 32)))
+    Va = _bf16(r.standard_normal((2, 9, 8, 32)))
+    got = tc.prefill_prefix_rows(torch.from_numpy(qa), torch.from_numpy(Ka), torch.from_numpy(Va), 0.2).numpy()
+    np.testing.assert_allclose(got, ora.prefill_prefix(qa, Ka, Va, 0.2), atol=2e-6)
