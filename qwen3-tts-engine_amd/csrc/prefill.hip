@@ -178,6 +178,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int jlim = a.causal ? min(Lk - 1, qpos) : Lk - 1;  // last key this lane's token sees
   // Last key that every token of this wave sees (wave-uniform).
   const int wlim = a.causal ? min(Lk - 1, Lk - Lq + qt * kQT + wave * 16) : Lk - 1;
+  // Last key that some token of this wave sees (wave-uniform); -1 when the wave holds no query token.  Tiles past
+  // it would add exact zeros, so the wave skips their arithmetic (it still copies and meets every barrier).
+  const int wfirst = qt * kQT + wave * 16;
+  const int wmax = wfirst >= Lq ? -1 : (a.causal ? min(Lk - 1, Lk - Lq + min(Lq - 1, wfirst + 15)) : Lk - 1);
 
   // Tile copies.  A 32-key tile is 2 groups of 16 keys and a group never straddles a page (page sizes are
   // powers of two >= 16), so each group has one uniform base address; waves 0 and 1 copy K groups 0 and 1,
@@ -241,6 +245,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   float m[kG] = {kMaxSeed, kMaxSeed}, l[kG] = {0.f, 0.f};
 
   auto compute = [&](int t, const uint8_t* Ks, const uint8_t* Vs) __attribute__((always_inline)) {
+    if (t * kKT > wmax) return;
     // S^T for the tile's 2 blocks of 16 keys, both heads; each K operand is read once.
     f32x4_t st[kG][kKT / 16];
 #pragma unroll
