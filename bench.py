@@ -6,7 +6,7 @@ ctx = 0, GQA 16/8, head_dim 128, bf16, 16-token pages, every layer with its own 
 page table over one 131,072-page pool (8.59 GB of K+V).  Inputs are resident in HBM before the
 timed region.  Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--workload c5|c3|c2|c4|admit]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra] [--workload c5|c3|c2|c4|admit]
 """
 from __future__ import annotations
 
@@ -437,6 +437,33 @@ def bench_admit(args, dev):
     return rec
 
 
+def other_workloads(args, dev):
+    """Short GPU-only runs of the other configurations beside the headline (20 graph replays each, no CPU
+    baselines; `--workload NAME` gives the full line of each): C3 decode, C2 code predictor, C4 prefill and the
+    fast-admission prefill.  A failure is recorded in place of the numbers and does not affect the headline."""
+    import copy
+
+    import torch
+
+    lite = copy.copy(args)
+    lite.steps, lite.warmup, lite.no_cpu_baseline, lite.no_append = 20, 3, True, True
+    out = {}
+    for name, fn in (("c3_decode", lambda: bench_decode(lite, dev, "c3")), ("c2_code_predictor", lambda: bench_cp(lite, dev)),
+                     ("c4_prefill", lambda: bench_prefill(lite, dev)), ("admission_prefill", lambda: bench_admit(lite, dev))):
+        try:
+            r = fn()
+            keep = {k: r[k] for k in ("us_per_layer_call", "us_per_call", "hbm_gbps", "pct_hbm_peak", "tflops",
+                                      "three_launch_us_per_step") if k in r}
+            keep["us_per_step"] = r["value"]
+            keep["roofline_frac"] = r["roofline"]["frac"]
+            keep["roofline_unit"] = r["roofline"]["unit"]
+            out[name] = keep
+        except Exception as e:  # noqa: BLE001 - reported, never fatal for the headline
+            out[name] = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -449,6 +476,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-append", action="store_true", help="skip the KV-append comparison of the decode bench")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="C5 only: skip the short GPU-only runs of the other workloads (other_workloads field)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -474,6 +503,8 @@ def main() -> int:
         return 0
     if args.workload in ("c5", "c3"):
         rec = bench_decode(args, dev, args.workload)
+        if args.workload == "c5" and not args.no_extra:
+            rec["other_workloads"] = other_workloads(args, dev)
     elif args.workload == "c2":
         rec = bench_cp(args, dev)
     elif args.workload == "admit":
