@@ -197,15 +197,12 @@ __device__ __forceinline__ void stage_new_rows(const DecodeArgs& a, int b, int g
 }
 
 // Append form, the last tile of a row, read after the next tile was issued: as take_new_token, with the new
-// k/v rows taken from the wave's stage and the slot stores left in flight.
-__device__ __forceinline__ void take_staged_token(const DecodeArgs& a, const TileList& L, uint32_t lane_off,
-                                                  int grp, int j, const uint8_t* st, KVTile& T) {
-  const int page = readlane(L.page, j);
-  const int off = readlane(L.off, j);
+// k/v rows taken from the wave's stage.  The slot itself is written by the combine kernel.
+__device__ __forceinline__ void take_staged_token(const DecodeArgs& a, const TileList& L, int grp, int j,
+                                                  const uint8_t* st, KVTile& T) {
   const int tn = readlane(L.nvalid, j) - 1;
   const int i_new = tn >> 2;
   const bool mine = grp == (tn & 3);
-  const bool ok = (unsigned)page < (unsigned)a.num_pages;
   const int chunk = (int)(threadIdx.x & 15) * 16;
   const uint4 kn = ld16(st + kStageNew + chunk);
   const uint4 vn = ld16(st + kStageNew + kD * 2 + chunk);
@@ -216,14 +213,7 @@ __device__ __forceinline__ void take_staged_token(const DecodeArgs& a, const Til
       T.v[i] = vn;
     }
   }
-  const int64_t pbase = ok ? (int64_t)page * a.kv_sp : 0;
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kc + pbase, ok ? a.page_bytes : 0u);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + pbase, ok ? a.page_bytes : 0u);
-  const uint32_t slot_off = (uint32_t)((off + 4 * i_new) * a.kv_st * 2);
-  if (mine) {
-    buffer_store16_s(kn, rk, lane_off, slot_off);
-    buffer_store16_s(vn, rv, lane_off, slot_off);
-  }
+  (void)a;
 }
 
 __device__ __forceinline__ uint32_t u4get(const uint4& v, int c) {
@@ -616,7 +606,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         q[1] = ld16(st + kD * 2 + dl * 2);
       }
       if constexpr (kAppend) {
-        if (fl & kRowEnd) take_staged_token(a, L, lane_off, grp, j, st, T);
+        if (fl & kRowEnd) take_staged_token(a, L, grp, j, st, T);
       }
       tile_update(a, L, q, T, j, grp, m, l, acc);
       if (fl & kLast) {
@@ -668,10 +658,32 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
 
 // One workgroup per row: merges the partial records of rows that straddle workgroup ranges, and
 // writes zeros for rows with no context.
+//
+// Append form: it also writes each row's new k/v row into its page slot.  The decode kernel attends with the staged
+// copies and never reads the slot, and no other row reads it in the same call, so the store can wait for this
+// kernel, which runs without a read stream to disturb: the same 2.1 MB of 256 B stores cost ~5 us inside the decode
+// kernel's read stream (576 rows, 296k tokens).
+template <bool kAppend>
 __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
   const int lane = threadIdx.x & 63;
+  if constexpr (kAppend) {
+    // Position c = cache_seqlens[b] receives the new token, unless the row is skipped (row_ctx: c < 0 or c at
+    // capacity); an invalid page id receives nothing.  Lane l copies 4 bytes of head g's k and v rows.
+    const int c = a.seqlens[b];
+    if (c >= 0 && c < a.max_pages * a.page_size) {
+      const int pidx = c / a.page_size;
+      const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
+      if ((unsigned)page < (unsigned)a.num_pages) {
+        const int64_t dst = (int64_t)page * a.kv_sp + (int64_t)(c - pidx * a.page_size) * a.kv_st + (int64_t)g * a.kv_sh;
+        const uint32_t kw = reinterpret_cast<const uint32_t*>(a.k_new + (int64_t)b * a.kn_sb + g * kD)[lane];
+        const uint32_t vw = reinterpret_cast<const uint32_t*>(a.v_new + (int64_t)b * a.vn_sb + g * kD)[lane];
+        reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.kc) + dst)[lane] = kw;
+        reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.vc) + dst)[lane] = vw;
+      }
+    }
+  }
   const int p0 = a.prefix[b];
   const int p1 = a.prefix[b + 1];
   const int NT = a.prefix[a.batch];
@@ -941,7 +953,10 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
       hipLaunchKernelGGL(paged_decode_sk_kernel<false>, dim3(a.grid), block, 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: stream-K launch failed: %s", who, hipGetErrorString(e));
-    hipLaunchKernelGGL(paged_decode_sk_combine_kernel, dim3(batch), block, 0, st, a);
+    if (append)
+      hipLaunchKernelGGL(paged_decode_sk_combine_kernel<true>, dim3(batch), block, 0, st, a);
+    else
+      hipLaunchKernelGGL(paged_decode_sk_combine_kernel<false>, dim3(batch), block, 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: combine launch failed: %s", who, hipGetErrorString(e));
     return Q3A_OK;
