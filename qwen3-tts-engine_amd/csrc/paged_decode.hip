@@ -662,45 +662,53 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
 // Append form: it also writes each row's new k/v row into its page slot.  The decode kernel attends with the staged
 // copies and never reads the slot, and no other row reads it in the same call, so the store can wait for this
 // kernel, which runs without a read stream to disturb: the same 2.1 MB of 256 B stores cost ~5 us inside the decode
-// kernel's read stream (576 rows, 296k tokens).
+// kernel's read stream (576 rows, 296k tokens).  Its loads are issued beside the merge's (the slot's page id next
+// to the record loads) and the stores come last, so the slot write adds no round trip to the merge's chain.
 template <bool kAppend>
 __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
   const int lane = threadIdx.x & 63;
+  const int p0 = a.prefix[b];
+  const int p1 = a.prefix[b + 1];
+  const int NT = a.prefix[a.batch];
+  // Position c = cache_seqlens[b] receives the new token, unless the row is skipped (row_ctx: c < 0 or c at
+  // capacity); an invalid page id receives nothing.  Lane l copies 4 bytes of head g's k and v rows.
+  int c = -1, page = -1;
+  uint32_t kw = 0u, vw = 0u;
   if constexpr (kAppend) {
-    // Position c = cache_seqlens[b] receives the new token, unless the row is skipped (row_ctx: c < 0 or c at
-    // capacity); an invalid page id receives nothing.  Lane l copies 4 bytes of head g's k and v rows.
-    const int c = a.seqlens[b];
-    if (c >= 0 && c < a.max_pages * a.page_size) {
-      const int pidx = c / a.page_size;
-      const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
+    c = a.seqlens[b];
+    kw = reinterpret_cast<const uint32_t*>(a.k_new + (int64_t)b * a.kn_sb + g * kD)[lane];
+    vw = reinterpret_cast<const uint32_t*>(a.v_new + (int64_t)b * a.vn_sb + g * kD)[lane];
+    if (c >= 0 && c < a.max_pages * a.page_size) page = a.bt[(int64_t)b * a.bt_sb + c / a.page_size];
+  }
+  auto store_slot = [&]() {
+    if constexpr (kAppend) {
       if ((unsigned)page < (unsigned)a.num_pages) {
+        const int pidx = c / a.page_size;
         const int64_t dst = (int64_t)page * a.kv_sp + (int64_t)(c - pidx * a.page_size) * a.kv_st + (int64_t)g * a.kv_sh;
-        const uint32_t kw = reinterpret_cast<const uint32_t*>(a.k_new + (int64_t)b * a.kn_sb + g * kD)[lane];
-        const uint32_t vw = reinterpret_cast<const uint32_t*>(a.v_new + (int64_t)b * a.vn_sb + g * kD)[lane];
         reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.kc) + dst)[lane] = kw;
         reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.vc) + dst)[lane] = vw;
       }
     }
-  }
-  const int p0 = a.prefix[b];
-  const int p1 = a.prefix[b + 1];
-  const int NT = a.prefix[a.batch];
+  };
   if (p1 == p0) {
     write_zero_row(a, b, g, lane);
+    store_slot();
     return;
   }
   const int64_t G = sk_effective_grid(a.grid, NT);
   const int kf = (int)(((int64_t)(p0 + 1) * G - 1) / NT);
   const int kl = (int)(((int64_t)p1 * G - 1) / NT);
-  if (kf == kl) return;
-  const int first_slot = sk_lo(kf, NT, G) < p0 ? 1 : 0;
-  merge_records(a, b, g, lane, kl - kf + 1, [&](int i) -> const float* {
-    const int k = kf + i;
-    const int slot = i == 0 ? first_slot : 0;
-    return a.ws + (((int64_t)k * kSkSlots + slot) * a.hkv + g) * kPartFloats;
-  });
+  if (kf != kl) {
+    const int first_slot = sk_lo(kf, NT, G) < p0 ? 1 : 0;
+    merge_records(a, b, g, lane, kl - kf + 1, [&](int i) -> const float* {
+      const int k = kf + i;
+      const int slot = i == 0 ? first_slot : 0;
+      return a.ws + (((int64_t)k * kSkSlots + slot) * a.hkv + g) * kPartFloats;
+    });
+  }
+  store_slot();
 }
 
 // ------------------------------------------------------------------------------ fixed-split path
