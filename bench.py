@@ -6,7 +6,7 @@ ctx = 0, GQA 16/8, head_dim 128, bf16, 16-token pages, every layer with its own 
 page table over one 131,072-page pool (8.59 GB of K+V).  Inputs are resident in HBM before the
 timed region.  Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra] [--workload c5|c3|c2|c4|admit]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra] [--workload decode576|decode256|cp512|prefill32|admit]
 """
 from __future__ import annotations
 
@@ -91,7 +91,7 @@ def cpu_baseline(wl, reps_min: int = 3, budget_s: float = 12.0):
 def measured_traffic():
     """HBM bytes per decode-kernel launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
     WRITE_SIZE scaled by a plain-copy calibration), or None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "paged_decode_c5.md")
+    path = os.path.join(ROOT, "profiles", "paged_decode_576rows.md")
     try:
         for ln in open(path):
             if ln.startswith("traffic_bytes_per_launch"):
@@ -187,7 +187,7 @@ def bench_decode(args, dev, name):
         cpu = cpu_baseline(wl)
         log(f"[bench] cpu baseline {cpu['us_per_layer_call']:.0f} us/call in {time.time() - t0:.1f} s")
 
-    if name == "c5":
+    if name == "decode576":
         desc = ("talker paged decode attention, 576 rows (518 live, ctx log-uniform [64,1800]; 58 padded ctx=0), "
                 "GQA 16/8, head_dim 128, bf16 K/V, fp32 softmax/accumulate, 16-token pages, 131072-page pool, "
                 "28 layer calls per step with per-layer random tables")
@@ -207,7 +207,7 @@ def bench_decode(args, dev, name):
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic() if name == "c5" else None,
+            "traffic": measured_traffic() if name == "decode576" else None,
             "kernel": "paged decode call (stream-K decode kernel + combine kernel), per call inside the graph",
             "bytes_per_call": nbytes,
         },
@@ -342,14 +342,14 @@ def bench_cp(args, dev):
 
 
 def bench_prefill(args, dev):
-    """Prompt prefill C4: 32 sequences, lengths U[150,400], K/V read from the paged pool, 28 layers per step,
+    """Prompt prefill, 32 sequences, lengths U[150,400], K/V read from the paged pool, 28 layers per step,
     each layer with its own q/k/v."""
     import torch
 
     import q3attn
     from q3attn import workloads as W
 
-    lens = W.prefill_lengths("c4", args.seed)
+    lens = W.prefill_lengths("prefill32", args.seed)
     wls = [W.make_prefill(dev, lens, seed=args.seed + l, paged=True, num_pages=4096) for l in range(LAYERS)]
     w0 = wls[0]
 
@@ -439,7 +439,7 @@ def bench_admit(args, dev):
 
 def other_workloads(args, dev):
     """Short GPU-only runs of the other configurations beside the headline (20 graph replays each, no CPU
-    baselines; `--workload NAME` gives the full line of each): C3 decode, C2 code predictor, C4 prefill and the
+    baselines; `--workload NAME` gives the full line of each): 256-row decode, 512-row code predictor, 32-sequence prefill and the
     fast-admission prefill.  A failure is recorded in place of the numbers and does not affect the headline."""
     import copy
 
@@ -448,8 +448,8 @@ def other_workloads(args, dev):
     lite = copy.copy(args)
     lite.steps, lite.warmup, lite.no_cpu_baseline, lite.no_append = 20, 3, True, True
     out = {}
-    for name, fn in (("c3_decode", lambda: bench_decode(lite, dev, "c3")), ("c2_code_predictor", lambda: bench_cp(lite, dev)),
-                     ("c4_prefill", lambda: bench_prefill(lite, dev)), ("admission_prefill", lambda: bench_admit(lite, dev))):
+    for name, fn in (("decode256", lambda: bench_decode(lite, dev, "decode256")), ("cp512", lambda: bench_cp(lite, dev)),
+                     ("prefill32", lambda: bench_prefill(lite, dev)), ("admission_prefill", lambda: bench_admit(lite, dev))):
         try:
             r = fn()
             keep = {k: r[k] for k in ("us_per_layer_call", "us_per_call", "hbm_gbps", "pct_hbm_peak", "tflops",
@@ -469,7 +469,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c5", choices=["c5", "c3", "c2", "c4", "admit"],
+    ap.add_argument("--workload", default="decode576", choices=["decode576", "decode256", "cp512", "prefill32", "admit"],
                     help="c5 (default, the headline metric), c3 decode, c2 code predictor, c4 prefill, "
                          "admit fast-admission prefill")
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
@@ -477,7 +477,7 @@ def main() -> int:
     ap.add_argument("--no-append", action="store_true", help="skip the KV-append comparison of the decode bench")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-extra", action="store_true",
-                    help="C5 only: skip the short GPU-only runs of the other workloads (other_workloads field)")
+                    help="576-row decode only: skip the short GPU-only runs of the other workloads (other_workloads field)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -501,11 +501,11 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
         return 0
-    if args.workload in ("c5", "c3"):
+    if args.workload in ("decode576", "decode256"):
         rec = bench_decode(args, dev, args.workload)
-        if args.workload == "c5" and not args.no_extra:
+        if args.workload == "decode576" and not args.no_extra:
             rec["other_workloads"] = other_workloads(args, dev)
-    elif args.workload == "c2":
+    elif args.workload == "cp512":
         rec = bench_cp(args, dev)
     elif args.workload == "admit":
         rec = bench_admit(args, dev)

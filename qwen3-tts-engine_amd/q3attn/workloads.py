@@ -83,19 +83,19 @@ def decode_bytes(ctx, page: int, hq: int = HQ, hkv: int = HKV, d: int = HEAD_DIM
 
 def draw_contexts(name: str, seed: int = 0) -> np.ndarray:
     rng = np.random.default_rng(seed)
-    if name == "c1":
+    if name == "decode1x64":
         return np.array([64], dtype=np.int64)
-    if name == "c3":
+    if name == "decode256":
         return rng.integers(200, 1201, size=256).astype(np.int64)
-    if name == "c5":
+    if name == "decode576":
         n_rows, n_pad = 576, 58
         live = np.rint(np.exp(rng.uniform(math.log(64), math.log(1800), size=n_rows - n_pad))).astype(np.int64)
         return np.concatenate([live, np.zeros(n_pad, dtype=np.int64)])
     raise ValueError(f"unknown decode workload {name!r}")
 
 
-POOL_PAGES = {"c1": 4, "c3": 65536, "c5": 131072}
-MAX_CTX = {"c1": 64, "c3": 1200, "c5": 1800}
+POOL_PAGES = {"decode1x64": 4, "decode256": 65536, "decode576": 131072}
+MAX_CTX = {"decode1x64": 64, "decode256": 1200, "decode576": 1800}
 
 
 def make_decode(name: str, device, layers: int = 1, seed: int = 0, ctx: np.ndarray | None = None,
@@ -107,7 +107,7 @@ def make_decode(name: str, device, layers: int = 1, seed: int = 0, ctx: np.ndarr
     ctx = draw_contexts(name, seed) if ctx is None else np.asarray(ctx, dtype=np.int64)
     num_pages = POOL_PAGES.get(name) if num_pages is None else num_pages
     max_ctx = MAX_CTX.get(name, int(ctx.max(initial=1))) if max_ctx is None else max_ctx
-    identity = (name == "c1") if identity is None else identity
+    identity = (name == "decode1x64") if identity is None else identity
     B = int(ctx.shape[0])
     P = max(1, -(-max_ctx // page))
     if B * P > num_pages:
@@ -209,7 +209,7 @@ class PrefillWorkload:
 
 def prefill_lengths(name: str, seed: int = 0) -> np.ndarray:
     rng = np.random.default_rng(seed)
-    if name == "c4":
+    if name == "prefill32":
         return rng.integers(150, 401, size=32).astype(np.int64)
     raise ValueError(f"unknown prefill workload {name!r}")
 

@@ -72,7 +72,7 @@ def test_paged_decode_empty_batch_is_a_noop():
 
 def test_workspace_and_default_split():
     L = _lib.lib()
-    # C5 shape: 576 rows, 113 pages of 16 tokens
+    # 576-row shape: 576 rows, 113 pages of 16 tokens
     split = L.q3a_paged_decode_default_split(576, 8, 113, 16)
     assert split % 16 == 0 and split >= 16
     n_splits = -(-113 * 16 // split)

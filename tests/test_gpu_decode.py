@@ -38,10 +38,10 @@ def assert_parity(out, ref, what=""):
 RAGGED = [0, 1, 2, 15, 16, 17, 31, 33, 63, 64, 65, 100, 127, 128, 129, 200, 255, 256, 257, 511, 700, 1023, 1800, 5]
 
 
-def test_c1_single_row(cuda_device):
-    wl = W.make_decode("c1", cuda_device)
+def test_decode_1x64_single_row(cuda_device):
+    wl = W.make_decode("decode1x64", cuda_device)
     out = run(wl)
-    assert_parity(out, decode_oracle(wl), "c1")
+    assert_parity(out, decode_oracle(wl), "decode1x64")
 
 
 @pytest.mark.parametrize("split", [0, 32, 64, 128, 1024])
@@ -127,16 +127,16 @@ def test_strided_cache_and_query(cuda_device):
     assert torch.equal(out, run(wl))
 
 
-def test_c3_full(cuda_device):
-    wl = W.make_decode("c3", cuda_device)
+def test_decode256_full(cuda_device):
+    wl = W.make_decode("decode256", cuda_device)
     out = run(wl)
-    assert_parity(out, decode_oracle(wl), "c3")
+    assert_parity(out, decode_oracle(wl), "decode256")
     del wl
     torch.cuda.empty_cache()
 
 
-def test_c5_full_size(cuda_device):
-    wl = W.make_decode("c5", cuda_device, layers=2)
+def test_decode576_full_size(cuda_device):
+    wl = W.make_decode("decode576", cuda_device, layers=2)
     ctx = wl.ctx
     out0 = run(wl, 0)
     # oracle on a subset: the longest, shortest and padded rows plus a seeded sample
@@ -186,7 +186,7 @@ def test_batch_beyond_stream_k_limit_uses_fixed_splits(cuda_device):
 
 
 def test_stream_k_matches_fixed_split(cuda_device):
-    wl = W.make_decode("c3", cuda_device)
+    wl = W.make_decode("decode256", cuda_device)
     a = run(wl)
     b = run(wl, split=128)
     ok, st = ora.compare(to_np(a), to_np(b), max_abs=8e-3, mean_abs=2e-4)

@@ -103,9 +103,9 @@ def test_append_many_short_rows_stream_k(cuda_device):
     assert torch.equal(wl.k_cache, ref_k) and torch.equal(wl.v_cache, ref_v)
 
 
-def test_append_c5_full_size(cuda_device):
-    """C5 (576 rows, 58 padded, 131,072-page pool): bitwise equal to index_copy_ + decode; oracle on a subset."""
-    wl = W.make_decode("c5", cuda_device, layers=1, seed=24)
+def test_append_decode576_full_size(cuda_device):
+    """576 rows (58 padded, 131,072-page pool): bitwise equal to index_copy_ + decode; oracle on a subset."""
+    wl = W.make_decode("decode576", cuda_device, layers=1, seed=24)
     k, v, old, ref_k, ref_v = _split_step(wl)
     ref = _reference(wl, ref_k, ref_v)
     del ref_k, ref_v

@@ -1,5 +1,5 @@
 """GPU parity of the MFMA prefill (q3a_prefill through the C ABI) against the oracle: packed varlen causal
-(engine/talker.py:169), read back from the paged pool (C4), the prefix + new bottom-right form
+(engine/talker.py:169), read back from the paged pool (32 sequences of U[150,400] tokens), the prefix + new bottom-right form
 (engine/arrivals.py:148), non-causal, and query rows that see no key."""
 import numpy as np
 import pytest
@@ -33,8 +33,8 @@ def test_packed_varlen_causal(cuda_device):
     check(out, oracle_varlen(wl), "packed varlen")
 
 
-def test_paged_c4_full(cuda_device):
-    lens = W.prefill_lengths("c4")
+def test_paged_prefill32_full(cuda_device):
+    lens = W.prefill_lengths("prefill32")
     wl = W.make_prefill(cuda_device, lens, seed=0, paged=True, num_pages=4096)
     out = q3attn.flash_attn_varlen_func(wl.q, wl.k_cache, wl.v_cache, wl.cu_seqlens, wl.cu_seqlens, wl.max_len,
                                         wl.max_len, softmax_scale=wl.scale, causal=True, block_table=wl.block_table)
