@@ -192,10 +192,14 @@ def bench_decode(args, dev, name):
                 "GQA 16/8, head_dim 128, bf16 K/V, fp32 softmax/accumulate, 16-token pages, 131072-page pool, "
                 "28 layer calls per step with per-layer random tables")
         metric = METRIC
-    else:
+    elif name == "decode256":
         desc = (f"talker paged decode attention, {wl.batch} rows, ctx U[200,1200], GQA 16/8, head_dim 128, bf16, "
                 "16-token pages, 65536-page pool, 28 layer calls per step with per-layer random tables")
         metric = f"paged decode attn µs/step and HBM GB/s (% peak) at {wl.batch} seats, 1×MI355X"
+    else:
+        desc = ("talker paged decode attention, 1 row of 64 tokens, GQA 16/8, head_dim 128, bf16, 16-token pages, "
+                "identity table, 28 layer calls per step")
+        metric = "paged decode attn µs/step at 1 seat x 64 tokens, 1×MI355X"
     rec = base_record(metric, round(ms_per_step * 1e3, 2), "us/step", args, ms_per_step, False, {
         "workload": desc, "rows": wl.batch, "sum_ctx": int(wl.ctx.sum()), "layers_per_step": LAYERS,
         "split_tokens": args.split or "stream-K", "parallelism": "single GPU"})
@@ -469,7 +473,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="decode576", choices=["decode576", "decode256", "cp512", "prefill32", "admit"],
+    ap.add_argument("--workload", default="decode576",
+                    choices=["decode576", "decode256", "decode1x64", "cp512", "prefill32", "admit"],
                     help="c5 (default, the headline metric), c3 decode, c2 code predictor, c4 prefill, "
                          "admit fast-admission prefill")
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
@@ -501,7 +506,7 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
         return 0
-    if args.workload in ("decode576", "decode256"):
+    if args.workload in ("decode576", "decode256", "decode1x64"):
         rec = bench_decode(args, dev, args.workload)
         if args.workload == "decode576" and not args.no_extra:
             rec["other_workloads"] = other_workloads(args, dev)

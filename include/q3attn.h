@@ -25,7 +25,8 @@ extern "C" {
 #define Q3A_ELAUNCH (-5)  /* the HIP runtime refused the launch */
 #define Q3A_ESPACE (-28)  /* workspace smaller than q3a_paged_decode_workspace_bytes() */
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature change); q3a_abi_version() returns the library's. */
+#define Q3A_ABI_VERSION 2
 int q3a_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -39,7 +40,8 @@ const char* q3a_last_error(void);
  *
  *   q            [B, Hq, D] bf16   row stride q_stride_b, head stride q_stride_h, dim stride 1
  *   k_cache      [num_pages, page_size, Hkv, D] bf16, strides kv_stride_page / kv_stride_tok /
- *   v_cache      kv_stride_head, dim stride 1 (both caches share the strides)
+ *   v_cache      kv_stride_head, dim stride 1 (both caches share the strides: the engine allocates the
+ *                per-layer pools alike, engine/talker.py:30-31)
  *   cache_seqlens[B] int32   context length of each row (tokens 0..ctx-1 are attended)
  *   block_table  [B, max_pages_per_seq] int32, row stride bt_stride_b: token t of row b lives at
  *                page block_table[b][t / page_size], offset t % page_size
@@ -108,14 +110,15 @@ int q3a_paged_decode_default_split(int batch, int num_kv_heads, int max_pages_pe
  * are float32, the probabilities are rounded to bf16 before P.V, P.V accumulates in float32.
  *
  *   q   [B, Hq, D] bf16 with row stride q_stride_b (head stride D)
- *   k,v [B, Hkv, S, D] bf16 with strides kv_stride_b / kv_stride_h / kv_stride_s (dim stride 1)
+ *   k   [B, Hkv, S, D] bf16 with strides k_stride_b / k_stride_h / k_stride_s (dim stride 1)
+ *   v   [B, Hkv, S, D] bf16 with strides v_stride_b / v_stride_h / v_stride_s (dim stride 1)
  *   out [B, Hq*D] bf16 with row stride o_stride_b
  * Requirements: D == 128, Hq == 2*Hkv, 1 <= n_live <= 16, 16-byte aligned pointers and strides,
- * D <= kv_stride_s <= 2^26 elements.
+ * D <= k_stride_s, v_stride_s <= 2^26 elements.
  */
-int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
-                int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,
-                int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, int64_t k_stride_b, int64_t k_stride_h,
+                int64_t k_stride_s, const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+                void* out, int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                 int n_live, float softmax_scale, void* stream);
 
 /*
@@ -130,10 +133,10 @@ int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
  *   q, k, v, out, strides and requirements as in q3a_cp_attn; k and v are written (slot n_live - 1 only).
  */
 int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void* k_new, int64_t kn_stride_b,
-                       const void* v_new, int64_t vn_stride_b, void* k, void* v, int64_t kv_stride_b,
-                       int64_t kv_stride_h, int64_t kv_stride_s, void* out, int64_t o_stride_b, int batch,
-                       int num_q_heads, int num_kv_heads, int head_dim, int n_live, float softmax_scale,
-                       void* stream);
+                       const void* v_new, int64_t vn_stride_b, void* k, int64_t k_stride_b, int64_t k_stride_h,
+                       int64_t k_stride_s, void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+                       void* out, int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                       int n_live, float softmax_scale, void* stream);
 
 /*
  * Talker prefill attention (packed variable-length, MFMA).
@@ -141,43 +144,48 @@ int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void* k_new, int
  * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, ..., causal=True) at
  * engine/talker.py:169 (fp32 form engine/talker.py:163-167); with cu_seqlens_k != cu_seqlens_q it also covers
  * prefix + new sequences packed by length (the dense flash_attn_func of engine/arrivals.py:148 is
- * q3a_prefill_dense below).
+ * q3a_prefill_dense below).  K and V carry their own strides: at engine/talker.py:158-160 k is a fresh
+ * [T, 8, 128] tensor (token stride 1024) while v is a view into the qkv projection (token stride 4096).
  *
  *   q       [T, Hq, D] bf16, token stride q_stride_t, head stride q_stride_h; sequence s owns tokens
  *           cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1
- *   k, v    block_table == NULL: packed [Tk, Hkv, D] (token stride kv_stride_tok, head stride kv_stride_head),
- *           sequence s owns rows cu_seqlens_k[s] .. cu_seqlens_k[s+1]-1;
- *           block_table != NULL: the paged pool [num_pages, page_size, Hkv, D] (kv_stride_page/tok/head), key j
+ *   k, v    block_table == NULL: packed [Tk, Hkv, D] (token strides k/v_stride_tok, head strides
+ *           k/v_stride_head; the page strides are ignored), sequence s owns rows cu_seqlens_k[s] ..
+ *           cu_seqlens_k[s+1]-1;
+ *           block_table != NULL: the paged pools [num_pages, page_size, Hkv, D] (k/v_stride_page/tok/head), key j
  *           of sequence s at page block_table[s][j / page_size], offset j % page_size, with
  *           Lk = cu_seqlens_k[s+1] - cu_seqlens_k[s] keys
  *   out     [T, Hq, D] bf16 (token stride o_stride_t, head stride o_stride_h)
  * With causal != 0, query i of a sequence sees keys j <= Lk - Lq + i (bottom-right aligned; for Lq == Lk the
  * standard causal mask).  Query rows that see no key are zeros.  Requirements: D == 128, Hq == 2*Hkv,
- * 16-byte aligned rows; max_seqlen_q >= every Lq.
+ * 16-byte aligned rows, strides multiples of 8 elements, K/V token strides in [D, 2^26]; max_seqlen_q >= every Lq.
  */
 int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
-                const void* k, const void* v, int64_t kv_stride_page, int64_t kv_stride_tok,
-                int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
-                int64_t bt_stride_b, int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out,
-                int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads,
-                int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream);
+                const void* k, int64_t k_stride_page, int64_t k_stride_tok, int64_t k_stride_head,
+                const void* v, int64_t v_stride_page, int64_t v_stride_tok, int64_t v_stride_head,
+                int num_pages, int page_size, const int32_t* block_table, int64_t bt_stride_b,
+                int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out, int64_t o_stride_t,
+                int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
+                int head_dim, float softmax_scale, int causal, void* stream);
 
 /*
  * Prefix + new prefill attention on dense [S, R, H, D] tensors (MFMA): the layout flash_attn_func takes at
  * engine/arrivals.py:148 (fp32 form engine/arrivals.py:125-131), with no cumulative-length arrays.
  *
  *   q    [S, Lq, Hq, D] bf16 (sequence/token/head strides q_stride_s/t/h), Lq = seqlen_q
- *   k, v [S, Lk, Hkv, D] bf16 (kv_stride_s/t/h), Lk = seqlen_k
+ *   k    [S, Lk, Hkv, D] bf16 (k_stride_s/t/h), Lk = seqlen_k
+ *   v    [S, Lk, Hkv, D] bf16 (v_stride_s/t/h)
  *   out  [S, Lq, Hq, D] bf16 (o_stride_s/t/h)
  * With causal != 0, query i sees keys j <= Lk - Lq + i (bottom-right aligned).  Query rows that see no key are
  * zeros.  Requirements as in q3a_prefill (D == 128, Hq == 2*Hkv, 16-byte aligned rows, strides multiples of 8
- * elements, K/V token stride in [D, 2^26]); sequence strides non-negative.
+ * elements, K/V token strides in [D, 2^26]); sequence strides non-negative.
  */
-int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h, const void* k,
-                      const void* v, int64_t kv_stride_s, int64_t kv_stride_t, int64_t kv_stride_h, void* out,
-                      int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int seqlen_q,
-                      int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
-                      int causal, void* stream);
+int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
+                      const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
+                      const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
+                      void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs,
+                      int seqlen_q, int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
+                      float softmax_scale, int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,6 @@ int fail(int code, const char* fmt, ...) {
 }
 }  // namespace q3a
 
-extern "C" int q3a_abi_version(void) { return 1; }
+extern "C" int q3a_abi_version(void) { return Q3A_ABI_VERSION; }
 
 extern "C" const char* q3a_last_error(void) { return g_last_error; }

@@ -34,7 +34,8 @@ struct CpArgs {
   int64_t q_sb;
   uint16_t* k;  // written only at slot n_live - 1, and only when k_new != nullptr
   uint16_t* v;
-  int64_t kv_sb, kv_sh, kv_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
   const uint16_t* k_new;  // optional [B, Hkv, D] rows for slot n_live - 1 (row strides kn_sb / vn_sb,
   const uint16_t* v_new;  // head stride D)
   int64_t kn_sb, vn_sb;
@@ -79,8 +80,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   const int c = lane & 3;
   const bool live = slot < a.n_live;
 
-  uint16_t* kb = a.k + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
-  uint16_t* vb = a.v + (int64_t)b * a.kv_sb + (int64_t)g * a.kv_sh;
+  uint16_t* kb = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
+  uint16_t* vb = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh;
   const uint16_t* qb = a.q + (int64_t)b * a.q_sb + (int64_t)(kG * g) * kD;
   // The scratch rows read are 0..n_read-1: all live slots, or in the append form all but the last, which
   // comes from this step's k/v rows (and is stored into the scratch here; it is never read back from the
@@ -89,10 +90,10 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   // never read and no branch or early wait sits between the loads.
   const int last = a.n_live - 1;
   const int n_read = kAppend ? last : a.n_live;
-  const uint32_t row_b = (uint32_t)a.kv_ss * 2;
-  const uint32_t span = n_read > 0 ? (uint32_t)(n_read - 1) * row_b + kD * 2 : 0u;
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, span);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, span);
+  const uint32_t krow_b = (uint32_t)a.k_ss * 2;
+  const uint32_t vrow_b = (uint32_t)a.v_ss * 2;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, n_read > 0 ? (uint32_t)(n_read - 1) * krow_b + kD * 2 : 0u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, n_read > 0 ? (uint32_t)(n_read - 1) * vrow_b + kD * 2 : 0u);
 
   // Lane (slot, c) holds dims 32*i + 8*c .. +8 for i = 0..3, of K[slot] and of both query heads.  q (and in
   // the append form the new k row) is loaded once, one 16 B chunk per lane, and handed to the lanes that need
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(qb, kG * kD * 2);
   const uint4 qc = buffer_load16(rq, lane < kG * 16 ? (uint32_t)lane * 16 : kOutOfRange);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) kr[i] = buffer_load16(rk, (uint32_t)slot * row_b + (32 * i + 8 * c) * 2);
+  for (int i = 0; i < 4; ++i) kr[i] = buffer_load16(rk, (uint32_t)slot * krow_b + (32 * i + 8 * c) * 2);
   // Append form: lanes 0..15 hold this step's k row, lane l its dims 8l..8l+7.
   const __amdgpu_buffer_rsrc_t rkn =
       kAppend ? make_rsrc(a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD, kD * 2) : rk;
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   if constexpr (kAppend) knc = buffer_load16(rkn, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange);
 #pragma unroll
   for (int s = 0; s < kNV; ++s)
-    vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, (int)((uint32_t)s * row_b), 0);
+    vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, (int)((uint32_t)s * vrow_b), 0);
   if constexpr (kAppend) vn = __builtin_amdgcn_raw_buffer_load_b32(rvn, lane * 4, 0, 0);
   // Every load is in flight before any is waited for.
   __builtin_amdgcn_sched_barrier(0);
@@ -134,8 +135,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
       if (s == last) vr[s] = vn;
     // Slot `last` of the scratch, written with vector buffer stores (lanes 16..63 of the k store are out of
     // bounds).
-    const __amdgpu_buffer_rsrc_t wk = make_rsrc(kb + (int64_t)last * a.kv_ss, kD * 2);
-    const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.kv_ss, kD * 2);
+    const __amdgpu_buffer_rsrc_t wk = make_rsrc(kb + (int64_t)last * a.k_ss, kD * 2);
+    const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.v_ss, kD * 2);
     buffer_store16_s(knc, wk, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange, 0u);
     __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, 0);
   }
@@ -187,11 +188,11 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
 
 using namespace q3a;
 
-static int cp_launch(const void* q, int64_t q_stride_b, void* k, void* v, int64_t kv_stride_b,
-                     int64_t kv_stride_h, int64_t kv_stride_s, const void* k_new, const void* v_new,
-                     int64_t kn_stride_b, int64_t vn_stride_b, void* out, int64_t o_stride_b, int batch,
-                     int num_q_heads, int num_kv_heads, int head_dim, int n_live, float softmax_scale,
-                     void* stream, const char* who) {
+static int cp_launch(const void* q, int64_t q_stride_b, void* k, int64_t k_stride_b, int64_t k_stride_h,
+                     int64_t k_stride_s, void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+                     const void* k_new, const void* v_new, int64_t kn_stride_b, int64_t vn_stride_b, void* out,
+                     int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim, int n_live,
+                     float softmax_scale, void* stream, const char* who) {
   if (batch < 0) return fail(Q3A_EINVAL, "%s: batch %d < 0", who, batch);
   if (batch == 0) return Q3A_OK;
   if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
@@ -202,21 +203,27 @@ static int cp_launch(const void* q, int64_t q_stride_b, void* k, void* v, int64_
   const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)k_new |
                           (uintptr_t)v_new;
   if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: q/K/V/out/k_new/v_new must be 16-byte aligned", who);
-  if ((q_stride_b | kv_stride_b | kv_stride_h | kv_stride_s | o_stride_b | kn_stride_b | vn_stride_b) % 8 != 0)
+  if ((q_stride_b | k_stride_b | k_stride_h | k_stride_s | v_stride_b | v_stride_h | v_stride_s | o_stride_b |
+       kn_stride_b | vn_stride_b) % 8 != 0)
     return fail(Q3A_EINVAL, "%s: strides must be multiples of 8 elements (16 bytes)", who);
   const int64_t pairs = (int64_t)batch * num_kv_heads;
   if (pairs > ((int64_t)1 << 30)) return fail(Q3A_EINVAL, "%s: batch too large", who);
-  if (kv_stride_s < head_dim || kv_stride_s > ((int64_t)1 << 26))
-    return fail(Q3A_EINVAL, "%s: slot stride %lld must be in [head_dim, 2^26] elements", who, (long long)kv_stride_s);
+  const int64_t lim = (int64_t)1 << 26;
+  if (k_stride_s < head_dim || k_stride_s > lim || v_stride_s < head_dim || v_stride_s > lim)
+    return fail(Q3A_EINVAL, "%s: slot strides %lld/%lld must be in [head_dim, 2^26] elements", who,
+                (long long)k_stride_s, (long long)v_stride_s);
 
   CpArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_stride_b;
   a.k = static_cast<uint16_t*>(k);
   a.v = static_cast<uint16_t*>(v);
-  a.kv_sb = kv_stride_b;
-  a.kv_sh = kv_stride_h;
-  a.kv_ss = kv_stride_s;
+  a.k_sb = k_stride_b;
+  a.k_sh = k_stride_h;
+  a.k_ss = k_stride_s;
+  a.v_sb = v_stride_b;
+  a.v_sh = v_stride_h;
+  a.v_ss = v_stride_s;
   a.k_new = static_cast<const uint16_t*>(k_new);
   a.v_new = static_cast<const uint16_t*>(v_new);
   a.kn_sb = kn_stride_b;
@@ -247,22 +254,23 @@ static int cp_launch(const void* q, int64_t q_stride_b, void* k, void* v, int64_
   return Q3A_OK;
 }
 
-extern "C" int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, const void* v,
-                           int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_s, void* out,
-                           int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads,
-                           int head_dim, int n_live, float softmax_scale, void* stream) {
-  return cp_launch(q, q_stride_b, const_cast<void*>(k), const_cast<void*>(v), kv_stride_b, kv_stride_h,
-                   kv_stride_s, nullptr, nullptr, 0, 0, out, o_stride_b, batch, num_q_heads, num_kv_heads,
-                   head_dim, n_live, softmax_scale, stream, "cp_attn");
+extern "C" int q3a_cp_attn(const void* q, int64_t q_stride_b, const void* k, int64_t k_stride_b, int64_t k_stride_h,
+                           int64_t k_stride_s, const void* v, int64_t v_stride_b, int64_t v_stride_h,
+                           int64_t v_stride_s, void* out, int64_t o_stride_b, int batch, int num_q_heads,
+                           int num_kv_heads, int head_dim, int n_live, float softmax_scale, void* stream) {
+  return cp_launch(q, q_stride_b, const_cast<void*>(k), k_stride_b, k_stride_h, k_stride_s, const_cast<void*>(v),
+                   v_stride_b, v_stride_h, v_stride_s, nullptr, nullptr, 0, 0, out, o_stride_b, batch, num_q_heads,
+                   num_kv_heads, head_dim, n_live, softmax_scale, stream, "cp_attn");
 }
 
 extern "C" int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void* k_new, int64_t kn_stride_b,
-                                  const void* v_new, int64_t vn_stride_b, void* k, void* v, int64_t kv_stride_b,
-                                  int64_t kv_stride_h, int64_t kv_stride_s, void* out, int64_t o_stride_b,
-                                  int batch, int num_q_heads, int num_kv_heads, int head_dim, int n_live,
-                                  float softmax_scale, void* stream) {
+                                  const void* v_new, int64_t vn_stride_b, void* k, int64_t k_stride_b,
+                                  int64_t k_stride_h, int64_t k_stride_s, void* v, int64_t v_stride_b,
+                                  int64_t v_stride_h, int64_t v_stride_s, void* out, int64_t o_stride_b, int batch,
+                                  int num_q_heads, int num_kv_heads, int head_dim, int n_live, float softmax_scale,
+                                  void* stream) {
   if (!k_new || !v_new) return fail(Q3A_EINVAL, "cp_attn_append: null k_new/v_new");
-  return cp_launch(q, q_stride_b, k, v, kv_stride_b, kv_stride_h, kv_stride_s, k_new, v_new, kn_stride_b,
-                   vn_stride_b, out, o_stride_b, batch, num_q_heads, num_kv_heads, head_dim, n_live,
-                   softmax_scale, stream, "cp_attn_append");
+  return cp_launch(q, q_stride_b, k, k_stride_b, k_stride_h, k_stride_s, v, v_stride_b, v_stride_h, v_stride_s,
+                   k_new, v_new, kn_stride_b, vn_stride_b, out, o_stride_b, batch, num_q_heads, num_kv_heads,
+                   head_dim, n_live, softmax_scale, stream, "cp_attn_append");
 }

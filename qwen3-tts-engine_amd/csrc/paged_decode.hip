@@ -30,6 +30,9 @@
 // In the stream-K kernel a segment's q rows and a row's new k/v rows reach the wave through LDS, copied
 // there together with the tile that needs them (see stage_q), so segment starts and row ends never
 // drain the tile in flight.
+#include <algorithm>
+#include <atomic>
+
 #include "q3a_common.h"
 #include "../../include/q3attn.h"
 
@@ -807,13 +810,15 @@ int default_split(int batch, int hkv, int max_pages, int page_size) {
 }
 
 // Workgroups of the stream-K kernel the current device holds at once (cached per device).
-// The workspace is sized for the larger of the two forms, so one buffer serves both.
+// The workspace is sized for the larger of the two forms, so one buffer serves both.  Entries are atomics: two
+// host threads may fill the same entry at once (both store the same value).
 int sk_grid_of(int hkv, bool append) {
-  static int cache[64][17][2];
+  static std::atomic<int> cache[64][17][2];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kSkMaxGrid;
-  int& c = cache[dev][hkv][append ? 1 : 0];
-  if (c > 0) return c;
+  std::atomic<int>& c = cache[dev][hkv][append ? 1 : 0];
+  const int cached = c.load(std::memory_order_relaxed);
+  if (cached > 0) return cached;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return kSkMaxGrid;
   const hipError_t e =
@@ -822,13 +827,19 @@ int sk_grid_of(int hkv, bool append) {
   if (e != hipSuccess) return kSkMaxGrid;
   int g = cus * (per_cu > 0 ? per_cu : 1);
   g = g < 1 ? 1 : (g > kSkMaxGrid ? kSkMaxGrid : g);
-  c = g;
+  c.store(g, std::memory_order_relaxed);
   return g;
 }
 
 int sk_grid(int hkv) {
   const int g0 = sk_grid_of(hkv, false), g1 = sk_grid_of(hkv, true);
   return g0 > g1 ? g0 : g1;
+}
+
+// Host copy of sk_effective_grid for a tile-count bound (non-decreasing in the count).
+int sk_effective_grid_host(int grid, int64_t nt) {
+  const int64_t g = std::max<int64_t>(std::min<int64_t>(nt, 8), (nt + 3) / 4);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(grid, g));
 }
 
 bool use_sk(int batch, int split_tokens) { return split_tokens == 0 && batch <= kSkMaxRows; }
@@ -952,7 +963,12 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   const dim3 block(64 * num_kv_heads);
   hipError_t e;
   if (sk) {
+    // Launch no more workgroups than the call can use: the tile count is at most rows x table capacity, and the
+    // workgroups past sk_effective_grid of the actual count exit after the prologue (every workgroup computes the
+    // same effective grid from a.grid, so bounding a.grid here changes no range when the bound holds).
+    const int64_t nt_bound = (int64_t)batch * ceil_div(max_ctx, kTile);
     a.grid = sk_grid_of(num_kv_heads, append);
+    a.grid = sk_effective_grid_host(a.grid, nt_bound);
     a.prefix = static_cast<int*>(workspace);
     a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256((size_t)(batch + 1) * sizeof(int)));
     if (append)
@@ -1020,3 +1036,4 @@ extern "C" int q3a_paged_decode_append(const void* q, int64_t q_stride_b, int64_
                        workspace_bytes_, batch, num_q_heads, num_kv_heads, head_dim, softmax_scale, split_tokens,
                        stream, "paged_decode_append");
 }
+

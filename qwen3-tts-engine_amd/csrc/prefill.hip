@@ -47,7 +47,8 @@ struct PrefillArgs {
   const int32_t* cu_q;
   const uint16_t* k;
   const uint16_t* v;
-  int64_t kv_sp, kv_st, kv_sh;
+  int64_t k_sp, k_st, k_sh;  // K and V carry their own strides (k fresh, v a view of the qkv projection)
+  int64_t v_sp, v_st, v_sh;
   int num_pages, page_size, page_shift;  // paged: page_size is a power of two >= 16
   const int32_t* bt;  // nullptr: packed K/V
   int64_t bt_sb;
@@ -56,7 +57,7 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t o_st, o_sh;
   // Dense form (cu_q == nullptr): sequence strides and the common lengths.
-  int64_t q_ss, kv_ss, o_ss;
+  int64_t q_ss, k_ss, v_ss, o_ss;
   int dense_lq, dense_lk;
   int causal;
   int hkv;
@@ -123,6 +124,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // loads wait for one memory round trip, not two.
   const bool paged = a.bt != nullptr;
   const int64_t bt_row = (int64_t)s * a.bt_sb;
+  // Waves 0 and 1 copy K tiles, waves 2 and 3 V tiles (below); each uses its operand's own strides, which are
+  // wave-uniform and stay in scalar registers.
+  const bool copies_k = wave < 2;
+  const int64_t c_sp = copies_k ? a.k_sp : a.v_sp;
+  const int64_t c_st = copies_k ? a.k_st : a.v_st;
+  const int64_t c_sh = copies_k ? a.k_sh : a.v_sh;
   int pwin = -1, pwin_base = 0;
   auto load_window = [&](int base) __attribute__((always_inline)) {
     pwin_base = base;
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
   // Element offsets of the sequence's first query/output row and first packed key row.
   int Lq, Lk;
-  int64_t qbase, obase, kbase;
+  int64_t qbase, obase, kbase;  // kbase: the first key row of the operand this wave copies
   if (a.cu_q != nullptr) {
     const int q0 = a.cu_q[s];
     const int k0 = a.cu_k[s];
@@ -141,13 +148,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     Lk = a.cu_k[s + 1] - k0;
     qbase = (int64_t)q0 * a.q_st;
     obase = (int64_t)q0 * a.o_st;
-    kbase = (int64_t)k0 * a.kv_st;
+    kbase = (int64_t)k0 * c_st;
   } else {
     Lq = a.dense_lq;
     Lk = a.dense_lk;
     qbase = (int64_t)s * a.q_ss;
     obase = (int64_t)s * a.o_ss;
-    kbase = (int64_t)s * a.kv_ss;
+    kbase = (int64_t)s * (copies_k ? a.k_ss : a.v_ss);
   }
   if (qt * kQT >= Lq) return;
   if (a.bt != nullptr) Lk = min(Lk, a.max_pages * a.page_size);
@@ -193,7 +200,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // window (lane i = table entry pwin_base + i), read with v_readlane; it is refilled once per 64 pages.
   static_assert(kKT == 32 && kQT == 64, "the copy assignment below is for 4 waves and 2 groups per tile");
   const int cgrp = wave & 1;                     // the 16-key group of a tile this wave copies
-  const uint16_t* cbase = wave < 2 ? a.k : a.v;  // waves 0, 1 copy K; waves 2, 3 copy V
+  const uint16_t* cbase = copies_k ? a.k : a.v;  // waves 0, 1 copy K; waves 2, 3 copy V
   auto group_rsrc = [&](const uint16_t* base, int t, int page) __attribute__((always_inline)) {
     const int j0 = t * kKT + 16 * cgrp;
     const int nv = min(16, Lk - j0);
@@ -201,17 +208,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     int64_t off = 0;
     if (paged) {
       ok = ok && (unsigned)page < (unsigned)a.num_pages;
-      off = (int64_t)page * a.kv_sp + (int64_t)(j0 & (a.page_size - 1)) * a.kv_st;
+      off = (int64_t)page * c_sp + (int64_t)(j0 & (a.page_size - 1)) * c_st;
     } else {
-      off = kbase + (int64_t)j0 * a.kv_st;
+      off = kbase + (int64_t)j0 * c_st;
     }
-    return make_rsrc(base + (ok ? off : 0) + (int64_t)g * a.kv_sh, ok ? (uint32_t)(((nv - 1) * a.kv_st + kD) * 2) : 0u);
+    return make_rsrc(base + (ok ? off : 0) + (int64_t)g * c_sh, ok ? (uint32_t)(((nv - 1) * c_st + kD) * 2) : 0u);
   };
   uint32_t dma_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int rr = 4 * i + (lane >> 4);
-    dma_off[i] = (uint32_t)((rr * a.kv_st + 8 * ((lane & 15) ^ rr)) * 2);
+    dma_off[i] = (uint32_t)((rr * c_st + 8 * ((lane & 15) ^ rr)) * 2);
   }
   auto issue = [&](int t, uint8_t* Kst, uint8_t* Vst) __attribute__((always_inline)) {
     int page = 0;
@@ -221,7 +228,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       page = readlane(pwin, pi - pwin_base);
     }
     const __amdgpu_buffer_rsrc_t rc = group_rsrc(cbase, t, page);
-    uint8_t* dst = wave < 2 ? Kst : Vst;
+    uint8_t* dst = copies_k ? Kst : Vst;
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(rc, dst + (16 * cgrp + 4 * i) * kRowB, dma_off[i]);
   };
@@ -385,19 +392,20 @@ using namespace q3a;
 
 // Checks shared by both entry points; returns Q3A_OK or an error code with the message set.
 static int check_common(const void* q, const void* k, const void* v, const void* out, int64_t q_st, int64_t q_sh,
-                        int64_t kv_st, int64_t kv_sh, int64_t o_st, int64_t o_sh, int num_q_heads, int num_kv_heads,
-                        int head_dim, const char* who) {
+                        int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh, int64_t o_st, int64_t o_sh,
+                        int num_q_heads, int num_kv_heads, int head_dim, const char* who) {
   if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
   if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
     return fail(Q3A_EINVAL, "%s: num_q_heads %d must be %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
   if (!q || !k || !v || !out) return fail(Q3A_EINVAL, "%s: null pointer argument", who);
   const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;
   if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: q/k/v/out must be 16-byte aligned", who);
-  if ((q_st | q_sh | kv_st | kv_sh | o_st | o_sh) % 8 != 0)
+  if ((q_st | q_sh | k_st | k_sh | v_st | v_sh | o_st | o_sh) % 8 != 0)
     return fail(Q3A_EINVAL, "%s: strides must be multiples of 8 elements (16 bytes)", who);
-  if (kv_st < head_dim || kv_sh < 0 || kv_st > ((int64_t)1 << 26))
-    return fail(Q3A_EINVAL, "%s: token stride %lld must be in [head_dim, 2^26] and head stride >= 0", who,
-                (long long)kv_st);
+  const int64_t lim = (int64_t)1 << 26;
+  if (k_st < head_dim || k_sh < 0 || k_st > lim || v_st < head_dim || v_sh < 0 || v_st > lim)
+    return fail(Q3A_EINVAL, "%s: token strides %lld/%lld must be in [head_dim, 2^26] and head strides >= 0", who,
+                (long long)k_st, (long long)v_st);
   return Q3A_OK;
 }
 
@@ -414,22 +422,23 @@ static int launch(const PrefillArgs& a, int num_seqs, int max_seqlen_q, void* st
 }
 
 extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
-                           const void* k, const void* v, int64_t kv_stride_page, int64_t kv_stride_tok,
-                           int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
-                           int64_t bt_stride_b, int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out,
-                           int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int max_seqlen_q,
-                           int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal,
-                           void* stream) {
+                           const void* k, int64_t k_stride_page, int64_t k_stride_tok, int64_t k_stride_head,
+                           const void* v, int64_t v_stride_page, int64_t v_stride_tok, int64_t v_stride_head,
+                           int num_pages, int page_size, const int32_t* block_table, int64_t bt_stride_b,
+                           int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out, int64_t o_stride_t,
+                           int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
+                           int head_dim, float softmax_scale, int causal, void* stream) {
   if (num_seqs < 0 || max_seqlen_q < 0) return fail(Q3A_EINVAL, "prefill: negative num_seqs/max_seqlen_q");
   if (num_seqs == 0 || max_seqlen_q == 0) return Q3A_OK;
   if (!cu_seqlens_q || !cu_seqlens_k) return fail(Q3A_EINVAL, "prefill: null pointer argument");
-  int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, kv_stride_tok, kv_stride_head, o_stride_t, o_stride_h,
-                        num_q_heads, num_kv_heads, head_dim, "prefill");
+  int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, k_stride_tok, k_stride_head, v_stride_tok,
+                        v_stride_head, o_stride_t, o_stride_h, num_q_heads, num_kv_heads, head_dim, "prefill");
   if (rc != Q3A_OK) return rc;
   if (block_table != nullptr) {
     if (page_size <= 0 || num_pages <= 0 || max_pages_per_seq <= 0)
       return fail(Q3A_EINVAL, "prefill: paged K/V needs page_size, num_pages and max_pages_per_seq > 0");
-    if (kv_stride_page % 8 != 0) return fail(Q3A_EINVAL, "prefill: page stride must be a multiple of 8 elements");
+    if ((k_stride_page | v_stride_page) % 8 != 0)
+      return fail(Q3A_EINVAL, "prefill: page strides must be multiples of 8 elements");
     if (page_size < 16 || (page_size & (page_size - 1)) != 0)
       return fail(Q3A_EINVAL, "prefill: page_size %d must be a power of two >= 16", page_size);
   }
@@ -441,9 +450,12 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
   a.cu_q = cu_seqlens_q;
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
-  a.kv_sp = kv_stride_page;
-  a.kv_st = kv_stride_tok;
-  a.kv_sh = kv_stride_head;
+  a.k_sp = k_stride_page;
+  a.k_st = k_stride_tok;
+  a.k_sh = k_stride_head;
+  a.v_sp = v_stride_page;
+  a.v_st = v_stride_tok;
+  a.v_sh = v_stride_head;
   a.num_pages = num_pages;
   a.page_size = page_size;
   a.page_shift = 0;
@@ -462,17 +474,19 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
 }
 
 extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
-                                 const void* k, const void* v, int64_t kv_stride_s, int64_t kv_stride_t,
-                                 int64_t kv_stride_h, void* out, int64_t o_stride_s, int64_t o_stride_t,
-                                 int64_t o_stride_h, int num_seqs, int seqlen_q, int seqlen_k, int num_q_heads,
-                                 int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream) {
+                                 const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
+                                 const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
+                                 void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs,
+                                 int seqlen_q, int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
+                                 float softmax_scale, int causal, void* stream) {
   if (num_seqs < 0 || seqlen_q < 0 || seqlen_k < 0)
     return fail(Q3A_EINVAL, "prefill_dense: negative num_seqs/seqlen_q/seqlen_k");
   if (num_seqs == 0 || seqlen_q == 0) return Q3A_OK;
-  int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, kv_stride_t, kv_stride_h, o_stride_t, o_stride_h,
-                        num_q_heads, num_kv_heads, head_dim, "prefill_dense");
+  int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, k_stride_t, k_stride_h, v_stride_t, v_stride_h,
+                        o_stride_t, o_stride_h, num_q_heads, num_kv_heads, head_dim, "prefill_dense");
   if (rc != Q3A_OK) return rc;
-  if ((q_stride_s | kv_stride_s | o_stride_s) % 8 != 0 || q_stride_s < 0 || kv_stride_s < 0 || o_stride_s < 0)
+  if ((q_stride_s | k_stride_s | v_stride_s | o_stride_s) % 8 != 0 || q_stride_s < 0 || k_stride_s < 0 ||
+      v_stride_s < 0 || o_stride_s < 0)
     return fail(Q3A_EINVAL, "prefill_dense: sequence strides must be non-negative multiples of 8 elements");
 
   PrefillArgs a{};
@@ -483,9 +497,12 @@ extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_st
   a.cu_q = nullptr;
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
-  a.kv_st = kv_stride_t;
-  a.kv_sh = kv_stride_h;
-  a.kv_ss = kv_stride_s;
+  a.k_st = k_stride_t;
+  a.k_sh = k_stride_h;
+  a.k_ss = k_stride_s;
+  a.v_st = v_stride_t;
+  a.v_sh = v_stride_h;
+  a.v_ss = v_stride_s;
   a.bt = nullptr;
   a.cu_k = nullptr;
   a.out = static_cast<uint16_t*>(out);

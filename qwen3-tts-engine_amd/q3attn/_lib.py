@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (must precede the library load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -49,21 +49,25 @@ SIGNATURES = {
     "q3a_paged_decode_workspace_bytes": (_c_size, [_c_int] * 7),
     "q3a_paged_decode_default_split": (_c_int, [_c_int] * 4),
     "q3a_cp_attn": (_c_int, [
-        _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,   # q, q_sb, k, v, kv strides (b, h, s)
+        _c_vp, _c_i64,                                         # q, q_stride_b
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # k, k strides (b, h, s)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (b, h, s)
         _c_vp, _c_i64,                                         # out, o_stride_b
         _c_int, _c_int, _c_int, _c_int, _c_int,                # batch, Hq, Hkv, D, n_live
         _c_float, _c_vp,                                       # softmax_scale, stream
     ]),
     "q3a_cp_attn_append": (_c_int, [
         _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,           # q, q_sb, k_new, kn_sb, v_new, vn_sb
-        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k, v, kv strides (b, h, s)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # k, k strides (b, h, s)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (b, h, s)
         _c_vp, _c_i64,                                         # out, o_stride_b
         _c_int, _c_int, _c_int, _c_int, _c_int,                # batch, Hq, Hkv, D, n_live
         _c_float, _c_vp,                                       # softmax_scale, stream
     ]),
     "q3a_prefill": (_c_int, [
         _c_vp, _c_i64, _c_i64, _c_vp,                          # q, q_stride_t, q_stride_h, cu_seqlens_q
-        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k, v, kv strides (page, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # k, k strides (page, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (page, tok, head)
         _c_int, _c_int, _c_vp, _c_i64, _c_int,                 # num_pages, page_size, block_table, bt stride, max pages
         _c_vp, _c_vp, _c_i64, _c_i64,                          # cu_seqlens_k, out, o_stride_t, o_stride_h
         _c_int, _c_int, _c_int, _c_int, _c_int,                # num_seqs, max_seqlen_q, Hq, Hkv, D
@@ -71,7 +75,8 @@ SIGNATURES = {
     ]),
     "q3a_prefill_dense": (_c_int, [
         _c_vp, _c_i64, _c_i64, _c_i64,                         # q, q strides (seq, tok, head)
-        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k, v, kv strides (seq, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # k, k strides (seq, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (seq, tok, head)
         _c_vp, _c_i64, _c_i64, _c_i64,                         # out, o strides (seq, tok, head)
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, seqlen_k, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream

@@ -29,7 +29,8 @@ def cp_attn_op(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, n_live: int, s
     if B == 0:
         return out
     rc = lib().q3a_cp_attn(
-        q2.data_ptr(), q2.stride(0), K.data_ptr(), V.data_ptr(), K.stride(0), K.stride(1), K.stride(2),
+        q2.data_ptr(), q2.stride(0), K.data_ptr(), K.stride(0), K.stride(1), K.stride(2),
+        V.data_ptr(), V.stride(0), V.stride(1), V.stride(2),
         out.data_ptr(), out.stride(0), B, Hq, Hkv, D, int(n_live), float(scale),
         torch.cuda.current_stream(q.device).cuda_stream)
     check(rc, "q3a_cp_attn")
@@ -41,10 +42,9 @@ def _check_common(q, K, V, n_live, who):
     _req(K.device == q.device and V.device == q.device, f"q3attn.{who}: q, K, V must share a device")
     _req(q.dtype == torch.bfloat16 and K.dtype == torch.bfloat16 and V.dtype == torch.bfloat16,
          f"q3attn.{who}: q, K, V must be bfloat16")
-    _req(K.dim() == 4 and K.shape == V.shape and K.stride() == V.stride(),
-         f"q3attn.{who}: K and V must be [B, kv_heads, slots, head_dim] with equal strides")
+    _req(K.dim() == 4 and K.shape == V.shape, f"q3attn.{who}: K and V must be [B, kv_heads, slots, head_dim]")
     B, Hkv, S, D = K.shape
-    _req(K.stride(3) == 1, f"q3attn.{who}: K/V head_dim must be contiguous")
+    _req(K.stride(3) == 1 and V.stride(3) == 1, f"q3attn.{who}: K/V head_dim must be contiguous")
     _req(1 <= n_live <= S, f"q3attn.{who}: n_live {n_live} outside [1, {S}]")
     q2 = q.reshape(q.shape[0], -1)
     _req(q2.shape[0] == B and q2.shape[1] % D == 0, f"q3attn.{who}: q and K batch/head_dim mismatch")
@@ -73,7 +73,7 @@ def cp_attn_append_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, K: torc
         return out
     rc = lib().q3a_cp_attn_append(
         q2.data_ptr(), q2.stride(0), k3.data_ptr(), k3.stride(0), v3.data_ptr(), v3.stride(0),
-        K.data_ptr(), V.data_ptr(), K.stride(0), K.stride(1), K.stride(2),
+        K.data_ptr(), K.stride(0), K.stride(1), K.stride(2), V.data_ptr(), V.stride(0), V.stride(1), V.stride(2),
         out.data_ptr(), out.stride(0), B, Hq, Hkv, D, int(p) + 1, float(scale),
         torch.cuda.current_stream(q.device).cuda_stream)
     check(rc, "q3a_cp_attn_append")

@@ -31,8 +31,10 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: tor
     _req(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
          "q3attn.prefill: q, k, v must be bfloat16")
     _req(q.dim() == 3 and q.stride(-1) == 1, "q3attn.prefill: q must be [tokens, heads, head_dim], dim contiguous")
-    _req(k.shape == v.shape and k.stride() == v.stride(), "q3attn.prefill: k and v must match in shape and strides")
-    _req(k.stride(-1) == 1, "q3attn.prefill: k/v head_dim must be contiguous")
+    # k and v may differ in strides: the talker passes a fresh k and v as a view of the qkv projection
+    # (engine/talker.py:158-160).
+    _req(k.shape == v.shape, "q3attn.prefill: k and v must have the same shape")
+    _req(k.stride(-1) == 1 and v.stride(-1) == 1, "q3attn.prefill: k/v head_dim must be contiguous")
     _req(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32,
          "q3attn.prefill: cu_seqlens must be int32")
     _req(cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous() and cu_seqlens_q.shape == cu_seqlens_k.shape,
@@ -45,18 +47,19 @@ def prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: tor
     if block_table is None:
         _req(k.dim() == 3 and k.shape[2] == D, "q3attn.prefill: packed k/v must be [tokens, kv_heads, head_dim]")
         Hkv = k.shape[1]
-        sp, st, sh, num_pages, page, bt_ptr, bt_sb, max_pages = 0, k.stride(0), k.stride(1), 0, 0, None, 0, 0
+        ks, vs = (0, k.stride(0), k.stride(1)), (0, v.stride(0), v.stride(1))
+        num_pages, page, bt_ptr, bt_sb, max_pages = 0, 0, None, 0, 0
     else:
         _req(k.dim() == 4 and k.shape[3] == D, "q3attn.prefill: paged k/v must be [num_pages, page, kv_heads, head_dim]")
         _req(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == n
              and block_table.stride(1) == 1 and block_table.device == q.device,
              "q3attn.prefill: block_table must be int32 [n, max_pages] with contiguous rows")
         num_pages, page, Hkv = k.shape[0], k.shape[1], k.shape[2]
-        sp, st, sh = k.stride(0), k.stride(1), k.stride(2)
+        ks, vs = (k.stride(0), k.stride(1), k.stride(2)), (v.stride(0), v.stride(1), v.stride(2))
         bt_ptr, bt_sb, max_pages = block_table.data_ptr(), block_table.stride(0), block_table.shape[1]
     rc = lib().q3a_prefill(
         q.data_ptr(), q.stride(0), q.stride(1), cu_seqlens_q.data_ptr(),
-        k.data_ptr(), v.data_ptr(), sp, st, sh, num_pages, page, bt_ptr, bt_sb, max_pages,
+        k.data_ptr(), *ks, v.data_ptr(), *vs, num_pages, page, bt_ptr, bt_sb, max_pages,
         cu_seqlens_k.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
         n, int(max_seqlen_q), Hq, Hkv, D, float(softmax_scale), 1 if causal else 0,
         torch.cuda.current_stream(q.device).cuda_stream)
@@ -93,18 +96,19 @@ def prefill_dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_sca
     _req(k.device == q.device and v.device == q.device, "q3attn.flash_attn_func: q, k, v must share a device")
     _req(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
          "q3attn.flash_attn_func: q, k, v must be bfloat16")
-    _req(q.dim() == 4 and k.dim() == 4 and k.shape == v.shape and k.stride() == v.stride()
+    _req(q.dim() == 4 and k.dim() == 4 and k.shape == v.shape
          and q.shape[0] == k.shape[0] and q.shape[3] == k.shape[3],
-         "q3attn.flash_attn_func: q [S,R,H,D], k/v [S,n,Hkv,D] with equal k/v strides")
-    _req(q.stride(3) == 1 and k.stride(3) == 1, "q3attn.flash_attn_func: head_dim must be contiguous")
+         "q3attn.flash_attn_func: q [S,R,H,D], k/v [S,n,Hkv,D]")
+    _req(q.stride(3) == 1 and k.stride(3) == 1 and v.stride(3) == 1, "q3attn.flash_attn_func: head_dim must be contiguous")
     S, R, Hq, D = q.shape
     n, Hkv = k.shape[1], k.shape[2]
     out = torch.empty((S, R, Hq, D), dtype=q.dtype, device=q.device)
     if S == 0 or R == 0:
         return out
     rc = lib().q3a_prefill_dense(
-        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
-        k.stride(2), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), S, R, n, Hq, Hkv, D,
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(), out.stride(0), out.stride(1),
+        out.stride(2), S, R, n, Hq, Hkv, D,
         float(softmax_scale), 1 if causal else 0, torch.cuda.current_stream(q.device).cuda_stream)
     check(rc, "q3a_prefill_dense")
     return out

@@ -38,7 +38,11 @@ def sample_topk(logits, temperature, k, gen):
 
 
 class SyntheticTalker:
-    def __init__(self, device, layers=28, seed=0, max_pos=1024, dtype=torch.bfloat16):
+    def __init__(self, device, layers=28, seed=0, max_pos=1024, dtype=torch.bfloat16, o_gain=4.0):
+        """``o_gain`` scales the o-projection's init std.  At 1.0 (the standard 1/sqrt(fan_in)) a random stack's
+        residual stream is dominated by the embeddings and MLPs, and attention moves the logits little; at 4.0 the
+        attention output carries a large share of each layer's update, so a rounding difference in attention
+        reaches the codebook-0 logits at full strength (the harder test of the criterion)."""
         self.device, self.dtype = torch.device(device), dtype
         g = torch.Generator(device=self.device)
         g.manual_seed(seed)
@@ -57,7 +61,7 @@ class SyntheticTalker:
             self.layers.append(dict(
                 ln1=norm_w(), ln2=norm_w(), qn=head_norm_w(), kn=head_norm_w(),
                 qkv=w((NH + 2 * NKV) * HD, H, std=H ** -0.5),
-                o=w(H, NH * HD, std=(NH * HD) ** -0.5 * 4.0),
+                o=w(H, NH * HD, std=(NH * HD) ** -0.5 * o_gain),
                 gu=w(2 * FFN, H, std=H ** -0.5),
                 down=w(H, FFN, std=FFN ** -0.5 * 0.5)))
         self.norm = norm_w()
@@ -101,8 +105,9 @@ class SyntheticTalker:
         return F.linear(h, self.codec_head).float()
 
 
-def oracle_attention(q, kc, vc, ctx, bt, scale):
-    """The oracle's paged decode on host copies of the pages the rows reference, back as bf16."""
+def oracle_attention(q, kc, vc, ctx, bt, scale, acc=np.float32):
+    """The oracle's paged decode on host copies of the pages the rows reference, back as bf16 (accumulating in
+    ``acc``)."""
     from oracle import attention as ora
     page = kc.shape[1]
     ctx_h = ctx.cpu().numpy().astype(np.int64)
@@ -114,8 +119,14 @@ def oracle_attention(q, kc, vc, ctx, bt, scale):
     k = kc.index_select(0, idx).float().cpu().numpy()
     v = vc.index_select(0, idx).float().cpu().numpy()
     tab = remap[np.where(bt_h < len(remap), bt_h, 0)]
-    out = ora.paged_decode(q.float().cpu().numpy(), k, v, ctx_h, tab, scale)
-    return torch.from_numpy(out).to(q.device).to(q.dtype)
+    out = ora.paged_decode(q.float().cpu().numpy(), k, v, ctx_h, tab, scale, acc=acc)
+    return torch.from_numpy(out.astype(np.float32)).to(q.device).to(q.dtype)
+
+
+def oracle64_attention(q, kc, vc, ctx, bt, scale):
+    """The same oracle accumulating in float64: a second correct implementation whose bf16 outputs differ from the
+    float32 oracle's only by rounding, so its code-0 disagreement with it is the floor any bf16 kernel meets."""
+    return oracle_attention(q, kc, vc, ctx, bt, scale, acc=np.float64)
 
 
 def torch_bf16_attention(q, kc, vc, ctx, bt, scale):

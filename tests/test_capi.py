@@ -87,29 +87,31 @@ def test_workspace_and_default_split():
 
 @pytest.mark.parametrize("kw,frag", [
     (dict(n_live=0), "n_live"), (dict(n_live=17), "n_live"), (dict(D=64), "head_dim"),
-    (dict(Hq=12), "num_q_heads"), (dict(q=None), "null"), (dict(kv_ss=100), "strides"),
-    (dict(kv_ss=64), "slot stride"), (dict(kv_ss=(1 << 26) + 8), "slot stride"),
+    (dict(Hq=12), "num_q_heads"), (dict(q=None), "null"), (dict(k_ss=100), "strides"), (dict(v_sh=4), "strides"),
+    (dict(k_ss=64), "slot strides"), (dict(v_ss=64), "slot strides"), (dict(v_ss=(1 << 26) + 8), "slot strides"),
 ])
 def test_cp_attn_rejects_bad_arguments(kw, frag):
-    a = dict(q=16, q_sb=2048, k=16, v=16, kv_sb=16384, kv_sh=2048, kv_ss=128, out=16, o_sb=2048,
-             B=4, Hq=16, Hkv=8, D=128, n_live=3, scale=0.088)
+    a = dict(q=16, q_sb=2048, k=16, k_sb=16384, k_sh=2048, k_ss=128, v=16, v_sb=32768, v_sh=4096, v_ss=256, out=16,
+             o_sb=2048, B=4, Hq=16, Hkv=8, D=128, n_live=3, scale=0.088)
     a.update(kw)
-    rc = _lib.lib().q3a_cp_attn(a["q"], a["q_sb"], a["k"], a["v"], a["kv_sb"], a["kv_sh"], a["kv_ss"], a["out"],
-                                a["o_sb"], a["B"], a["Hq"], a["Hkv"], a["D"], a["n_live"], a["scale"], None)
+    rc = _lib.lib().q3a_cp_attn(a["q"], a["q_sb"], a["k"], a["k_sb"], a["k_sh"], a["k_ss"], a["v"], a["v_sb"],
+                                a["v_sh"], a["v_ss"], a["out"], a["o_sb"], a["B"], a["Hq"], a["Hkv"], a["D"],
+                                a["n_live"], a["scale"], None)
     assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
 
 
 @pytest.mark.parametrize("kw,frag", [
     (dict(kn=None), "k_new"), (dict(vn=None), "k_new"), (dict(kn=18), "aligned"), (dict(vn_sb=1030), "strides"),
-    (dict(n_live=0), "n_live"), (dict(Hq=8), "num_q_heads"),
+    (dict(n_live=0), "n_live"), (dict(Hq=8), "num_q_heads"), (dict(v=24), "aligned"),
 ])
 def test_cp_attn_append_rejects_bad_arguments(kw, frag):
-    a = dict(q=16, q_sb=2048, kn=16, kn_sb=1024, vn=16, vn_sb=4096, k=16, v=16, kv_sb=16384, kv_sh=2048,
-             kv_ss=128, out=16, o_sb=2048, B=4, Hq=16, Hkv=8, D=128, n_live=3, scale=0.088)
+    a = dict(q=16, q_sb=2048, kn=16, kn_sb=1024, vn=16, vn_sb=4096, k=16, k_sb=16384, k_sh=2048, k_ss=128, v=16,
+             v_sb=16384, v_sh=2048, v_ss=128, out=16, o_sb=2048, B=4, Hq=16, Hkv=8, D=128, n_live=3, scale=0.088)
     a.update(kw)
-    rc = _lib.lib().q3a_cp_attn_append(a["q"], a["q_sb"], a["kn"], a["kn_sb"], a["vn"], a["vn_sb"], a["k"], a["v"],
-                                       a["kv_sb"], a["kv_sh"], a["kv_ss"], a["out"], a["o_sb"], a["B"], a["Hq"],
-                                       a["Hkv"], a["D"], a["n_live"], a["scale"], None)
+    rc = _lib.lib().q3a_cp_attn_append(a["q"], a["q_sb"], a["kn"], a["kn_sb"], a["vn"], a["vn_sb"], a["k"],
+                                       a["k_sb"], a["k_sh"], a["k_ss"], a["v"], a["v_sb"], a["v_sh"], a["v_ss"],
+                                       a["out"], a["o_sb"], a["B"], a["Hq"], a["Hkv"], a["D"], a["n_live"],
+                                       a["scale"], None)
     assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
 
 
@@ -193,22 +195,70 @@ def test_fake_impl_traces_shapes():
 
 @pytest.mark.parametrize("kw,frag", [
     (dict(D=64), "head_dim"), (dict(Hq=8), "num_q_heads"), (dict(q=None), "null pointer"), (dict(k=18), "aligned"),
-    (dict(q_st=2050), "strides"), (dict(kv_st=64), "token stride"), (dict(q_ss=-2048), "sequence strides"),
-    (dict(o_ss=12), "sequence strides"), (dict(Lk=-1), "negative"), (dict(S=-1), "negative"),
+    (dict(v=40), "aligned"), (dict(q_st=2050), "strides"), (dict(k_st=64), "token strides"),
+    (dict(v_st=64), "token strides"), (dict(v_sh=3), "strides"), (dict(q_ss=-2048), "sequence strides"),
+    (dict(v_ss=-8), "sequence strides"), (dict(o_ss=12), "sequence strides"), (dict(Lk=-1), "negative"),
+    (dict(S=-1), "negative"),
 ])
 def test_prefill_dense_rejects_bad_arguments(kw, frag):
-    a = dict(q=16, q_ss=42 * 2048, q_st=2048, q_sh=128, k=16, v=16, kv_ss=77 * 1024, kv_st=1024, kv_sh=128, out=16,
-             o_ss=42 * 2048, o_st=2048, o_sh=128, S=8, Lq=42, Lk=77, Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
+    a = dict(q=16, q_ss=42 * 2048, q_st=2048, q_sh=128, k=16, k_ss=77 * 1024, k_st=1024, k_sh=128, v=16,
+             v_ss=77 * 4096, v_st=4096, v_sh=128, out=16, o_ss=42 * 2048, o_st=2048, o_sh=128, S=8, Lq=42, Lk=77,
+             Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
     a.update(kw)
-    rc = _lib.lib().q3a_prefill_dense(a["q"], a["q_ss"], a["q_st"], a["q_sh"], a["k"], a["v"], a["kv_ss"], a["kv_st"],
-                                      a["kv_sh"], a["out"], a["o_ss"], a["o_st"], a["o_sh"], a["S"], a["Lq"], a["Lk"],
-                                      a["Hq"], a["Hkv"], a["D"], a["scale"], a["causal"], None)
+    rc = _lib.lib().q3a_prefill_dense(a["q"], a["q_ss"], a["q_st"], a["q_sh"], a["k"], a["k_ss"], a["k_st"],
+                                      a["k_sh"], a["v"], a["v_ss"], a["v_st"], a["v_sh"], a["out"], a["o_ss"],
+                                      a["o_st"], a["o_sh"], a["S"], a["Lq"], a["Lk"], a["Hq"], a["Hkv"], a["D"],
+                                      a["scale"], a["causal"], None)
     assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
 
 
 def test_prefill_dense_empty_is_a_noop():
     L = _lib.lib()
-    assert L.q3a_prefill_dense(16, 0, 2048, 128, 16, 16, 0, 1024, 128, 16, 0, 2048, 128, 0, 42, 77, 16, 8, 128, 0.1, 1,
-                               None) == 0
-    assert L.q3a_prefill_dense(16, 0, 2048, 128, 16, 16, 0, 1024, 128, 16, 0, 2048, 128, 8, 0, 77, 16, 8, 128, 0.1, 1,
-                               None) == 0
+    assert L.q3a_prefill_dense(16, 0, 2048, 128, 16, 0, 1024, 128, 16, 0, 4096, 128, 16, 0, 2048, 128, 0, 42, 77, 16,
+                               8, 128, 0.1, 1, None) == 0
+    assert L.q3a_prefill_dense(16, 0, 2048, 128, 16, 0, 1024, 128, 16, 0, 4096, 128, 16, 0, 2048, 128, 8, 0, 77, 16,
+                               8, 128, 0.1, 1, None) == 0
+
+
+def _prefill(**kw):
+    """The talker's own prefill layout (engine/talker.py:157-169): q [T,16,128] and k [T,8,128] fresh tensors, v a
+    view of the [T, 4096] qkv projection (token stride 4096)."""
+    a = dict(q=16, q_st=2048, q_sh=128, cu_q=16, k=16, k_sp=0, k_st=1024, k_sh=128, v=16, v_sp=0, v_st=4096,
+             v_sh=128, num_pages=0, page=0, bt=None, bt_sb=0, max_pages=0, cu_k=16, out=16, o_st=2048, o_sh=128,
+             n=4, max_q=400, Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
+    a.update(kw)
+    return _lib.lib().q3a_prefill(a["q"], a["q_st"], a["q_sh"], a["cu_q"], a["k"], a["k_sp"], a["k_st"], a["k_sh"],
+                                  a["v"], a["v_sp"], a["v_st"], a["v_sh"], a["num_pages"], a["page"], a["bt"],
+                                  a["bt_sb"], a["max_pages"], a["cu_k"], a["out"], a["o_st"], a["o_sh"], a["n"],
+                                  a["max_q"], a["Hq"], a["Hkv"], a["D"], a["scale"], a["causal"], None)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(D=64), "head_dim"), (dict(cu_q=None), "null pointer"), (dict(v=None), "null pointer"),
+    (dict(v=8), "aligned"), (dict(v_st=4100), "strides"), (dict(k_st=64), "token strides"),
+    (dict(v_st=(1 << 26) + 8), "token strides"), (dict(n=-1), "negative"),
+    (dict(bt=16, page=16, num_pages=0, max_pages=4), "paged K/V"),
+    (dict(bt=16, page=48, num_pages=8, max_pages=4, k_sp=16384, v_sp=16384), "power of two"),
+    (dict(bt=16, page=16, num_pages=8, max_pages=4, k_sp=16384, v_sp=16380), "page strides"),
+])
+def test_prefill_rejects_bad_arguments(kw, frag):
+    assert _prefill(**kw) < 0
+    assert frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_prefill_empty_is_a_noop():
+    assert _prefill(n=0) == 0 and _prefill(max_q=0) == 0
+
+
+def test_prefill_accepts_the_reference_kv_layout_on_the_host_side():
+    """The equal-stride requirement is gone from the Python op: only shape and the contiguous head dim are checked
+    before any device work, so the error a CPU tensor raises is the device one."""
+    T = 10
+    qkv = torch.zeros(T, 4096, dtype=torch.bfloat16)
+    q = torch.zeros(T, 16, 128, dtype=torch.bfloat16)
+    k = torch.zeros(T, 8, 128, dtype=torch.bfloat16)
+    v = qkv[:, 3072:].view(T, 8, 128)
+    assert k.stride() != v.stride()
+    cu = torch.tensor([0, 4, T], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        q3attn.flash_attn_varlen_func(q, k, v, cu, cu, 6, 6, softmax_scale=0.1, causal=True)

@@ -1,7 +1,7 @@
 """GPU parity of the talker paged decode (q3a_paged_decode through the C ABI) against the oracle.
 
 Bar (bf16 output): max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32-softmax oracle on the same
-bf16 inputs.  Full-size workloads are checked on an oracle subset plus size-independent properties
+bf16 inputs.  Full-size workloads are checked on every row against the oracle, plus size-independent properties
 (bitwise determinism, page-table permutation invariance, split-size invariance)."""
 import numpy as np
 import pytest
@@ -136,16 +136,12 @@ def test_decode256_full(cuda_device):
 
 
 def test_decode576_full_size(cuda_device):
+    """Every row of both layers against the oracle (518 live rows, ~297k context tokens each), plus properties."""
     wl = W.make_decode("decode576", cuda_device, layers=2)
-    ctx = wl.ctx
     out0 = run(wl, 0)
-    # oracle on a subset: the longest, shortest and padded rows plus a seeded sample
-    rng = np.random.default_rng(0)
-    rows = sorted(set([int(ctx.argmax()), int(np.argmin(np.where(ctx > 0, ctx, 10 ** 9))), 575, 520])
-                  | set(rng.choice(576, 60, replace=False).tolist()))
-    assert_parity(out0[rows], decode_oracle(wl, 0, rows), "c5 layer0 subset")
+    assert_parity(out0, decode_oracle(wl, 0), "decode576 layer0 all rows")
     out1 = run(wl, 1)
-    assert_parity(out1[rows], decode_oracle(wl, 1, rows), "c5 layer1 subset")
+    assert_parity(out1, decode_oracle(wl, 1), "decode576 layer1 all rows")
     assert not out0[518:].float().abs().sum().item()
     # bitwise determinism
     assert torch.equal(out0, run(wl, 0))
