@@ -94,6 +94,24 @@ int q3a_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_
                             int batch, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
                             int split_tokens, void* stream);
 
+/*
+ * q3a_paged_decode without a workspace argument: it allocates nothing and takes no caller buffer beyond q, the
+ * caches, the length/table arrays and out.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses that forbid allocation).
+ *
+ * The workspace is a static 8 MiB device array inside the library, one per GPU, held until the process ends.  Shapes
+ * whose workspace (q3a_paged_decode_workspace_bytes) exceeds it are rejected with Q3A_ESPACE; every stream-K call
+ * (split_tokens == 0, batch <= 4096) fits on MI355X.  All calls on one GPU share that array: calls that overlap on one
+ * GPU (two streams at once) race, calls ordered on one stream do not.  Arguments, semantics and results are those of
+ * q3a_paged_decode, bit for bit.
+ */
+int q3a_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                             const void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                             int64_t kv_stride_head, int num_pages, int page_size, const int32_t* cache_seqlens,
+                             const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq, void* out,
+                             int64_t o_stride_b, int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads,
+                             int head_dim, float softmax_scale, int split_tokens, void* stream);
+
 /* Bytes of workspace q3a_paged_decode needs for this shape and split (0 if none is needed). */
 size_t q3a_paged_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                         int max_pages_per_seq, int page_size, int split_tokens);

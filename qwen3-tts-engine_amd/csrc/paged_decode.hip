@@ -1037,3 +1037,69 @@ extern "C" int q3a_paged_decode_append(const void* q, int64_t q_stride_b, int64_
                        stream, "paged_decode_append");
 }
 
+// ------------------------------------------------------------------------------ allocation-free entry point
+// For callers that cannot allocate device memory (code under graph capture, tight serving loops, harnesses that
+// forbid it): q3a_paged_decode with the workspace taken from this file-scope array instead of the caller.  Each GPU
+// the library runs on holds its own copy (kNoAllocScratchBytes) until the process ends.  Its device address comes from
+// hipGetSymbolAddress, fetched once per device with that device current; host code never uses the array's name
+// as an address.  No byte of it needs to start at zero: the combine kernel reads only what the same call's decode
+// kernel wrote (tile prefix sums, partial records).  Every call on one GPU shares the array, so calls that overlap on
+// one GPU (two streams at once) race; calls on one stream are ordered and safe.
+namespace q3a {
+namespace {
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// The scratch array's device address on the current device (nullptr and a message on failure).
+void* scratch_address(const char* who) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(Q3A_ELAUNCH, "%s: no current HIP device (or device index >= %d)", who, kMaxDevices);
+    return nullptr;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  void* q = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || q == nullptr) {
+    fail(Q3A_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev, hipGetErrorString(e));
+    return nullptr;
+  }
+  // Two threads may both look the address up; they store the same value.
+  g_scratch_ptr[dev].store(q, std::memory_order_release);
+  return q;
+}
+}  // namespace
+}  // namespace q3a
+
+extern "C" int q3a_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                                        const void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                                        int64_t kv_stride_head, int num_pages, int page_size,
+                                        const int32_t* cache_seqlens, const int32_t* block_table, int64_t bt_stride_b,
+                                        int max_pages_per_seq, void* out, int64_t o_stride_b, int64_t o_stride_h,
+                                        int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                        float softmax_scale, int split_tokens, void* stream) {
+  const char* who = "paged_decode_noalloc";
+  if (batch < 0) return fail(Q3A_EINVAL, "%s: batch %d < 0", who, batch);
+  if (batch == 0) return Q3A_OK;
+  if (num_kv_heads < 1 || num_kv_heads > 16)
+    return fail(Q3A_EINVAL, "%s: num_kv_heads %d outside [1, 16]", who, num_kv_heads);
+  if (page_size <= 0 || max_pages_per_seq <= 0 || split_tokens < 0)
+    return fail(Q3A_EINVAL, "%s: page_size %d / max_pages_per_seq %d must be > 0, split_tokens >= 0", who, page_size,
+                max_pages_per_seq);
+  if ((int64_t)max_pages_per_seq * page_size > (int64_t)1 << 30)
+    return fail(Q3A_EINVAL, "%s: context capacity too large", who);
+  void* ws = scratch_address(who);
+  if (ws == nullptr) return Q3A_ELAUNCH;
+  const size_t need = workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, split_tokens);
+  if (need > kNoAllocScratchBytes)
+    return fail(Q3A_ESPACE, "%s: this shape needs %zu bytes of workspace, more than the %zu-byte static scratch "
+                "(batch %d, split_tokens %d)", who, need, kNoAllocScratchBytes, batch, split_tokens);
+  return launch_decode(q, q_stride_b, q_stride_h, nullptr, 0, nullptr, 0, k_cache, v_cache, kv_stride_page,
+                       kv_stride_tok, kv_stride_head, num_pages, page_size, cache_seqlens, block_table, bt_stride_b,
+                       max_pages_per_seq, out, o_stride_b, o_stride_h, ws, kNoAllocScratchBytes, batch, num_q_heads,
+                       num_kv_heads, head_dim, softmax_scale, split_tokens, stream, who);
+}

@@ -46,6 +46,15 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int,             # batch, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                    # softmax_scale, split_tokens, stream
     ]),
+    "q3a_paged_decode_noalloc": (_c_int, [
+        _c_vp, _c_i64, _c_i64,                      # q, q_stride_b, q_stride_h
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,       # k_cache, v_cache, kv strides (page, tok, head)
+        _c_int, _c_int,                             # num_pages, page_size
+        _c_vp, _c_vp, _c_i64, _c_int,               # cache_seqlens, block_table, bt_stride_b, max_pages
+        _c_vp, _c_i64, _c_i64,                      # out, o_stride_b, o_stride_h
+        _c_int, _c_int, _c_int, _c_int,             # batch, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                    # softmax_scale, split_tokens, stream
+    ]),
     "q3a_paged_decode_workspace_bytes": (_c_size, [_c_int] * 7),
     "q3a_paged_decode_default_split": (_c_int, [_c_int] * 4),
     "q3a_cp_attn": (_c_int, [
