@@ -80,19 +80,6 @@ __device__ __forceinline__ uint2 ldtr(const uint8_t* lds) {
   return __builtin_bit_cast(uint2, r);
 }
 
-// max(x, x of lane l ^ 32) and max(x, x of lane l ^ 16) with the gfx950 lane-swap instructions (plain VALU
-// operations, unlike a shuffle through the LDS crossbar): v_permlane32_swap exchanges lanes 32..63 of its first
-// operand with lanes 0..31 of its second, v_permlane16_swap the odd 16-lane rows of the first with the even rows
-// of the second, so with x in both operands the two results hold x and its partner lane's x.
-__device__ __forceinline__ float max_xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float max_xor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 // Waits for this wave's outstanding vector-memory operations (the direct-to-LDS copies); vmcnt(0), the other
 // counters untouched.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -368,9 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // The 4 lanes of a token hold partial sums over disjoint keys.
 #pragma unroll
   for (int hh = 0; hh < kG; ++hh) {
-    float lt = l[hh];
-    lt += __shfl_xor(lt, 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = sum_xor32(sum_xor16(l[hh]));
     if (qvalid) {
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
       uint16_t* o = a.out + obase + (int64_t)tq * a.o_st + (kG * g + hh) * a.o_sh + 4 * g4;
@@ -381,6 +366,169 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         w.y = pack_bf16x2(acc[hh][db][2] * inv, acc[hh][db][3] * inv);
         *reinterpret_cast<uint2*>(o + db * 16) = w;
       }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ short key ranges
+// The fast-admission shape (engine/arrivals.py:148: R = 42 new tokens over n = 77 keys) has so little work per
+// (sequence, head) that the tiled kernel above is one chain of copy -> barrier -> MFMA -> softmax -> MFMA per key tile
+// for a single wave per SIMD.  Here one workgroup, for one query head of a GQA pair, holds the sequence's whole K/V
+// range of that KV head in LDS (at most kResMaxTiles tiles of 32 keys, copied at once; the two heads' workgroups
+// copy it separately, which halves the LDS operand traffic per CU), and each wave takes 16 query tokens: the tile
+// then runs with no copy, wait or barrier, as one pass over all keys (scores of every tile, one row max, P, P.V: no
+// running max to carry from tile to tile), and a wave's arithmetic is half the two-head one.  Dense
+// form only (seqlen_k <= 128); the query tokens of a sequence are split over workgroups of at most kResMaxGroups
+// 16-token groups.
+constexpr int kResMaxTiles = 4;
+constexpr int kResQ = 16;
+constexpr int kResMaxGroups = 16;  // waves per workgroup
+
+__global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(const PrefillArgs a, int ntiles) {
+  __shared__ __align__(16) uint8_t sK[kResMaxTiles * kTileB];
+  __shared__ __align__(16) uint8_t sV[kResMaxTiles * kTileB];
+
+  const int s = blockIdx.x / a.hkv;
+  const int g = blockIdx.x - s * a.hkv;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int lane = tid & 63;
+  const int col = lane & 15;
+  const int g4 = lane >> 4;
+  const int hh = blockIdx.z & 1;                               // query head 2g + hh
+  const int tg = (blockIdx.z >> 1) * kResMaxGroups + wave;     // 16-token query group
+
+  const int Lq = a.dense_lq;
+  const int Lk = a.dense_lk;
+  const int64_t qbase = (int64_t)s * a.q_ss, obase = (int64_t)s * a.o_ss;
+
+  // Copies: the 16-key groups of K and V (2 per tile and operand) are dealt round-robin to the waves; four
+  // direct-to-LDS loads each, same layout and swizzle as the tiled kernel.
+  const int ngroups = 4 * ntiles;
+  for (int c = wave; c < ngroups; c += nwaves) {
+    const int op = c & 1;                       // 0: K, 1: V
+    const int grp = c >> 1;                     // 16-key group 0 .. 2 ntiles - 1
+    const uint16_t* base = op == 0 ? a.k : a.v;
+    const int64_t st = op == 0 ? a.k_st : a.v_st;
+    const int64_t sh = op == 0 ? a.k_sh : a.v_sh;
+    const int64_t ss = op == 0 ? a.k_ss : a.v_ss;
+    const int jg = 16 * grp;
+    const int nv = min(16, Lk - jg);
+    const bool ok = nv > 0;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (ok ? (int64_t)s * ss + (int64_t)jg * st : 0) + (int64_t)g * sh,
+                                               ok ? (uint32_t)(((nv - 1) * st + kD) * 2) : 0u);
+    uint8_t* dst = (op == 0 ? sK : sV) + grp * 16 * kRowB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 4 * i + (lane >> 4);
+      dma16(r, dst + 4 * i * kRowB, (uint32_t)((rr * st + 8 * ((lane & 15) ^ rr)) * 2));
+    }
+  }
+  const int tq = tg * kResQ + col;
+  const bool qvalid = tq < Lq;
+  bf16x8_t qb[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if (qvalid) x = ld16(a.q + qbase + (int64_t)tq * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
+    qb[kk] = as_bf16x8(x);
+  }
+  wait_vmem();
+  __syncthreads();
+  if (tg * kResQ >= Lq) return;                 // a wave with no query token (after the barrier: it copied)
+
+  const int jlim = a.causal ? min(Lk - 1, Lk - Lq + tq) : Lk - 1;
+  const int wfirst = tg * kResQ;
+  // last key some token of this wave sees, and the last one every token of it sees
+  const int wmax = a.causal ? min(Lk - 1, Lk - Lq + min(Lq - 1, wfirst + kResQ - 1)) : Lk - 1;
+  const int wlim = a.causal ? min(Lk - 1, Lk - Lq + wfirst) : Lk - 1;
+  const int rsw = 4 * g4 + ((lane & 15) >> 2);
+  const int c_lo = ((lane & 15) & 3) >> 1;
+  const uint32_t v_rd = (uint32_t)(rsw * kRowB + (lane & 1) * 8);
+
+  // One pass over at most 128 keys, no running max: every tile's scores first (independent MFMA chains), one row
+  // max, then P and O^T = V^T P^T.  nt = tiles this wave's tokens see (wave-uniform).
+  const int nt = min(ntiles, wmax / kKT + 1);
+  f32x4_t st[kResMaxTiles][kKT / 16];
+#pragma unroll
+  for (int t = 0; t < kResMaxTiles; ++t) {
+#pragma unroll
+    for (int kb = 0; kb < kKT / 16; ++kb) {
+      st[t][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (t < nt) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const bf16x8_t kv =
+              as_bf16x8(ld16(sK + t * kTileB + kb * 16 * kRowB + col * kRowB + (((4 * kk + g4) ^ col) << 4)));
+          st[t][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qb[kk], st[t][kb], 0, 0, 0);
+        }
+      }
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < kResMaxTiles; ++t) {
+    if (t < nt) {
+      if (t * kKT + kKT - 1 > wlim) {
+        // key t*32 + 16 kb + 4 g4 + i is visible to this lane's token iff it is <= jlim
+        const int lim = jlim - t * kKT - 4 * g4;
+#pragma unroll
+        for (int kb = 0; kb < kKT / 16; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[t][kb][i] = (kb * 16 + i <= lim) ? st[t][kb][i] : -INFINITY;
+      }
+#pragma unroll
+      for (int kb = 0; kb < kKT / 16; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[t][kb][i]);
+    }
+  }
+  // a token that sees no key keeps the finite seed, so its p are exp2(-inf) = 0 and its output is zero
+  const float m = fmaxf(kMaxSeed, max_xor16(max_xor32(mx)) * a.scale_log2);
+  f32x4_t acc[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+#pragma unroll
+  for (int t = 0; t < kResMaxTiles; ++t) {
+    if (t < nt) {
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = fast_exp2(fmaf(st[t][0][i], a.scale_log2, -m));
+        p[4 + i] = fast_exp2(fmaf(st[t][1][i], a.scale_log2, -m));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l += p[i];
+      uint4 w;
+      w.x = pack_bf16x2(p[0], p[1]);
+      w.y = pack_bf16x2(p[2], p[3]);
+      w.z = pack_bf16x2(p[4], p[5]);
+      w.w = pack_bf16x2(p[6], p[7]);
+      const bf16x8_t pb = as_bf16x8(w);
+      const uint8_t* Vs = sV + t * kTileB;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        const uint32_t chunk = (uint32_t)((((2 * db) + c_lo) ^ rsw) << 4);
+        const uint2 lo = ldtr(Vs + v_rd + chunk);
+        const uint2 hi = ldtr(Vs + v_rd + chunk + 16 * kRowB);
+        acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb,
+                                                          acc[db], 0, 0, 0);
+      }
+    }
+  }
+  // The 4 lanes of a token hold partial sums over disjoint keys.
+  l = sum_xor32(sum_xor16(l));
+  if (qvalid) {
+    const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
+    uint16_t* o = a.out + obase + (int64_t)tq * a.o_st + (kG * g + hh) * a.o_sh + 4 * g4;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      uint2 w;
+      w.x = pack_bf16x2(acc[db][0] * inv, acc[db][1] * inv);
+      w.y = pack_bf16x2(acc[db][2] * inv, acc[db][3] * inv);
+      *reinterpret_cast<uint2*>(o + db * 16) = w;
     }
   }
 }
@@ -514,5 +662,20 @@ extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_st
   a.causal = causal ? 1 : 0;
   a.scale_log2 = softmax_scale * kLog2e;
   a.hkv = num_kv_heads;
+  if (seqlen_k <= kResMaxTiles * kKT) {
+    // Short key range: the whole K/V range of a (sequence, KV head) in LDS, one wave per 16 tokens and query head.
+    const int ntiles = seqlen_k > 0 ? (seqlen_k + kKT - 1) / kKT : 0;
+    const int ngroups = (seqlen_q + kResQ - 1) / kResQ;
+    const int nblk = (ngroups + kResMaxGroups - 1) / kResMaxGroups;
+    const int waves = ngroups < kResMaxGroups ? ngroups : kResMaxGroups;
+    if ((int64_t)num_seqs * num_kv_heads > 0x7fffffff || 2 * nblk > 65535)
+      return fail(Q3A_EINVAL, "prefill_dense: grid too large (%d seqs x %d KV heads x %d query blocks)", num_seqs,
+                  num_kv_heads, nblk);
+    hipLaunchKernelGGL(prefill_resident_kernel, dim3(num_seqs * num_kv_heads, 1, 2 * nblk), dim3(64 * waves), 0,
+                       static_cast<hipStream_t>(stream), a, ntiles);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "prefill_dense: launch failed: %s", hipGetErrorString(e));
+    return Q3A_OK;
+  }
   return launch(a, num_seqs, seqlen_q, stream, "prefill_dense");
 }

@@ -136,6 +136,21 @@ __device__ __forceinline__ float quads_max(float x) {
   return x;
 }
 
+// x + (x of lane l ^ 32) and x + (x of lane l ^ 16), and the same for max, with the gfx950 lane swaps (VALU
+// operations, not the LDS crossbar): with x in both operands, one result holds x and the other the partner's x.
+__device__ __forceinline__ float2 swap32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 swap16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) { const float2 r = swap32(x); return r.x + r.y; }
+__device__ __forceinline__ float sum_xor16(float x) { const float2 r = swap16(x); return r.x + r.y; }
+__device__ __forceinline__ float max_xor32(float x) { const float2 r = swap32(x); return fmaxf(r.x, r.y); }
+__device__ __forceinline__ float max_xor16(float x) { const float2 r = swap16(x); return fmaxf(r.x, r.y); }
+
 }  // namespace q3a
 
 // ---------------------------------------------------------------------------------- host side

@@ -163,3 +163,29 @@ def test_graph_capture_flash_attn_func(cuda_device):
         torch.cuda.synchronize()
         assert torch.equal(static, eager)
     check(eager, ora.prefill_prefix(to_np(wl.q), to_np(wl.k), to_np(wl.v), wl.scale), "admission shape")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("R,n", [(1, 1), (1, 77), (16, 16), (17, 32), (17, 33), (42, 64), (42, 77), (5, 100),
+                                 (42, 128), (42, 129), (33, 20)])
+def test_flash_attn_func_short_key_ranges(cuda_device, R, n, causal):
+    """Key ranges of at most 128 go to the short-key kernel (the whole K/V range in LDS, one wave per 16 query tokens
+    and query head); 129 keys and more to the tiled kernel.  Both must agree with the oracle on either side of the boundary, causal (bottom-right)
+    or not; with R > n the first R - n queries see no key under the causal mask and are zeros."""
+    g = torch.Generator(device=cuda_device).manual_seed(R * 1000 + n)
+    S = 3
+    q = torch.randn(S, R, 16, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    K = torch.randn(S, n, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    V = torch.randn(S, n, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    out = q3attn.flash_attn_func(q, K, V, softmax_scale=128 ** -0.5, causal=causal)
+    torch.cuda.synchronize()
+    qn, Kn, Vn = to_np(q), to_np(K), to_np(V)
+    if causal:
+        skip = max(0, R - n)
+        if skip:
+            assert not out[:, :skip].float().abs().sum().item()
+        ref = ora.prefill_prefix(qn[:, skip:], Kn, Vn, 128 ** -0.5)
+        check(out[:, skip:], ref, f"short keys R={R} n={n} causal")
+    else:
+        ref = np.stack([_dense(qn[i], Kn[i], Vn[i], 128 ** -0.5) for i in range(S)])
+        check(out, ref, f"short keys R={R} n={n} non-causal")
