@@ -30,20 +30,43 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_model() -> str:
+def host_cpus() -> dict:
+    """The host's CPU facts: os.cpu_count(), the affinity mask, the cgroup CPU quota, and lscpu's model and
+    socket/core/thread counts."""
+    info = {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        info["cgroup_cpus"] = None if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        info["cgroup_cpus"] = None
+    keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core"}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for ln in out.splitlines():
-            if ln.startswith("Model name:"):
-                return ln.split(":", 1)[1].strip()
+            k, _, v = ln.partition(":")
+            if k.strip() in keys:
+                v = v.strip()
+                info[keys[k.strip()]] = int(v) if v.isdigit() else v
     except Exception:
         pass
-    return "unknown"
+    if isinstance(info.get("sockets"), int) and isinstance(info.get("cores_per_socket"), int):
+        info["lscpu_cores"] = info["sockets"] * info["cores_per_socket"]
+    return info
+
+
+def cpu_threads() -> int:
+    """All of the host's cores for the CPU baselines: torch.set_num_threads(os.cpu_count())."""
+    import torch
+
+    n = os.cpu_count() or 1
+    torch.set_num_threads(n)
+    return torch.get_num_threads()
 
 
 def cpu_baseline(wl, reps_min: int = 3, budget_s: float = 12.0):
     """The reference's per-row fp32 torch attention (engine/talker.py:82-88 with the page gather),
-    on the host cores, over layer 0 of the same workload (all 576 rows).  Reported per frame (x28)."""
+    on the host cores, over layer 0 of the same workload (all rows).  Reported per frame (x28)."""
     import numpy as np
     import torch
 
@@ -65,11 +88,12 @@ def cpu_baseline(wl, reps_min: int = 3, budget_s: float = 12.0):
     q = L.q.float().cpu()
     sl = torch.from_numpy(wl.ctx)
     tb = torch.from_numpy(table)
-    threads = torch.get_num_threads()
-    paged_decode_rows(q, k, v, sl, tb, wl.scale)                # warm-up
+    threads = cpu_threads()
+    paged_decode_rows(q, k, v, sl, tb, wl.scale)                # warm-up (two, as the reference's timing does)
+    paged_decode_rows(q, k, v, sl, tb, wl.scale)
     times = []
     t_start = time.perf_counter()
-    while len(times) < reps_min or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+    while len(times) < max(reps_min, 5) or (time.perf_counter() - t_start < budget_s and len(times) < 200):
         t0 = time.perf_counter()
         paged_decode_rows(q, k, v, sl, tb, wl.scale)
         times.append(time.perf_counter() - t0)
@@ -82,7 +106,8 @@ def cpu_baseline(wl, reps_min: int = 3, budget_s: float = 12.0):
         "sample": (f"layer 0 of the same {wl.batch}-row workload (all rows, {int(wl.ctx.sum())} context tokens), "
                    f"median of {len(times)} calls of the reference's per-row fp32 torch loop "
                    f"(engine/talker.py:82-88 + page gather) = {per_call_us:.0f} us/call, x{LAYERS} layers per step; "
-                   f"{threads} threads on {cpu_model()}"),
+                   f"torch.set_num_threads(os.cpu_count() = {os.cpu_count()})"),
+        "host": host_cpus(),
         "us_per_layer_call": round(per_call_us, 1),
         "gbps": round(wl.algorithmic_bytes() / (per_call_us * 1e-6) / 1e9, 2),
     }
@@ -101,10 +126,11 @@ def measured_traffic():
     return None
 
 
-def time_graph(dev, frame_fn, steps: int, warmup: int):
+def time_graph(dev, frame_fn, steps: int, warmup: int, min_warm_s: float = 0.0):
     """Capture frame_fn once into a HIP graph (as the engine does, engine/talker.py:115-137), check a replay
-    against the eager result, then time `steps` replays with a HIP event pair around each.
-    Returns (wall ms per step, list of per-replay event ms)."""
+    against the eager result, then time `steps` replays with a HIP event pair around each.  The untimed warmup is
+    `warmup` replays, continued until min_warm_s seconds have passed (the short extra runs set it, so the GPU's
+    clocks are back up after the host-only CPU baselines).  Returns (wall ms per step, list of per-replay event ms)."""
     import torch
 
     stream = torch.cuda.Stream(dev)
@@ -121,8 +147,13 @@ def time_graph(dev, frame_fn, steps: int, warmup: int):
     if not all(torch.equal(a, b) for a, b in zip(static_out, eager)):
         raise RuntimeError("graph replay differs from the eager frame")
     cur = torch.cuda.current_stream(dev)
-    for _ in range(warmup):
+    t_warm = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t_warm < min_warm_s:
         graph.replay()
+        n += 1
+        if min_warm_s and n % 8 == 0:
+            torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
     t_start = time.perf_counter()
@@ -143,7 +174,7 @@ def base_record(metric, value, unit, args, ms_per_step, higher_is_better, config
     }
 
 
-def bench_decode(args, dev, name):
+def bench_decode(args, dev, name, cpu_budget_s: float = 12.0):
     import torch
 
     import q3attn
@@ -160,7 +191,8 @@ def bench_decode(args, dev, name):
         return q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table,
                                    wl.scale, args.split)
 
-    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [layer_call(L) for L in wl.layers], args.steps, args.warmup)
+    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [layer_call(L) for L in wl.layers], args.steps, args.warmup,
+                                          getattr(args, "min_warm_s", 0.0))
     avg_call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
     achieved = nbytes / (avg_call_us * 1e-6) / 1e9
     log(f"[bench] {args.steps} graph replays of {LAYERS} calls: wall {ms_per_step:.3f} ms/step; events "
@@ -184,7 +216,7 @@ def bench_decode(args, dev, name):
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
-        cpu = cpu_baseline(wl)
+        cpu = cpu_baseline(wl, budget_s=cpu_budget_s)
         log(f"[bench] cpu baseline {cpu['us_per_layer_call']:.0f} us/call in {time.time() - t0:.1f} s")
 
     if name == "decode576":
@@ -305,16 +337,40 @@ def bench_cp(args, dev):
             out.append(q3attn.cp_attn(layers[l][0][p], K, V, p + 1, scale))
         return out
 
-    ms_split, frame_split, _ = time_graph(dev, three_launch, args.steps, args.warmup)
-    ms_per_step, frame_ms, _ = time_graph(dev, fused, args.steps, args.warmup)
+    warm_s = getattr(args, "min_warm_s", 0.0)
+    ms_split, frame_split, _ = time_graph(dev, three_launch, args.steps, args.warmup, warm_s)
+    ms_per_step, frame_ms, graph = time_graph(dev, fused, args.steps, args.warmup, warm_s)
     frame_us = statistics.mean(frame_ms) * 1e3
     split_us = statistics.mean(frame_split) * 1e3
+    # The same frame with the 256 MB Infinity Cache and the L2s flushed before each replay (a 512 MiB read-modify-write
+    # between frames, outside the timed events): in the engine the code predictor's weights stream between steps, so
+    # the scratch is not necessarily cache-resident when a step starts.
+    evict = torch.zeros(256 << 20, dtype=torch.float16, device=dev)
+    cur = torch.cuda.current_stream(dev)
+    cold = []
+    for _ in range(max(5, args.steps // 2)):
+        evict.add_(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        graph.replay()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        cold.append(e0.elapsed_time(e1) * 1e3)
+    del evict
+    cold_us = statistics.median(cold)
+    # Launch floor: a graph of as many one-workgroup kernels (a one-element add) as the frame has calls, in one stream.
+    tiny = torch.zeros(1, device=dev)
+    _, floor_ms, _ = time_graph(dev, lambda: [tiny + 1 for _ in order], args.steps, args.warmup)
+    floor_us = statistics.mean(floor_ms) * 1e3 / len(order)
+    call_us = frame_us / len(order)
     achieved = nbytes / (frame_us * 1e-6) / 1e9
-    log(f"[bench] cp: {len(order)} calls per frame, fused {frame_us:.1f} us/frame = {frame_us / len(order):.2f} us/call "
-        f"({achieved:.0f} GB/s algorithmic); index_copy_ x2 + attention {split_us:.1f} us/frame")
+    log(f"[bench] cp: {len(order)} calls per frame, fused {frame_us:.1f} us/frame = {call_us:.2f} us/call "
+        f"(cache-flushed frame {cold_us:.1f} us); index_copy_ x2 + attention {split_us:.1f} us/frame; launch floor "
+        f"{floor_us:.2f} us/call; {achieved:.0f} GB/s algorithmic")
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.torch_cpu import cp_attn_rows
+        threads = cpu_threads()
         qs, K, V = layers[0]
         qc, Kc, Vc = [t.cpu() for t in qs], K.cpu(), V.cpu()
         rc = [(rows[0, p][0].cpu(), rows[0, p][1].cpu()) for p in range(16)]
@@ -327,7 +383,7 @@ def bench_cp(args, dev):
                 cp_attn_rows(qc[p], Kc, Vc, p + 1, scale)
             times.append(time.perf_counter() - t0)
         us = statistics.median(times) * 1e6 * L
-        cpu = {"value": round(us, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+        cpu = {"value": round(us, 1), "unit": "us/step", "cores": threads, "kind": "port",
                "sample": f"one layer's 16 steps (slot write + attention) at B={B} with the reference's torch bf16 "
                          f"ops on CPU (engine/code_predictor.py:46-47,58), median of 3, x{L} layers"}
     rec = base_record("code-predictor slot write + attention µs/step (16 steps x 5 layers) at 512 rows, 1×MI355X",
@@ -335,12 +391,15 @@ def bench_cp(args, dev):
                       {"workload": "code-predictor 16-slot causal attention with the step's K/V slot write, 512 rows, "
                                    "GQA 16/8, head_dim 128, bf16, n_live 1..16, 5 layers per step",
                        "rows": B, "calls_per_step": len(order), "parallelism": "single GPU"})
-    rec.update({"us_per_call": round(frame_us / len(order), 3),
+    rec.update({"us_per_call": round(call_us, 3),
                 "three_launch_us_per_step": round(split_us, 2),
-                "roofline": {"bound": "latency (K/V resident in the 256 MB Infinity Cache)",
-                             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                             "bytes_per_step": nbytes},
+                "cold_us_per_step": round(cold_us, 2), "cold_us_per_call": round(cold_us / len(order), 3),
+                "launch_floor_us_per_call": round(floor_us, 3),
+                "algorithmic_gbps": round(achieved, 1), "bytes_per_step": nbytes,
+                # 2.1-37.7 MB per call and ~2 flop/B: the call is bound by launch and memory latency, so the roofline
+                # is the latency floor of one dependent kernel in the same graph harness (frac = floor / achieved)
+                "roofline": {"bound": "latency", "achieved": round(call_us, 3), "peak": round(floor_us, 3),
+                             "unit": "us/call", "frac": round(floor_us / call_us, 4), "traffic": None},
                 "cpu_baseline": cpu})
     return rec
 
@@ -362,7 +421,8 @@ def bench_prefill(args, dev):
                                              wl.max_len, softmax_scale=wl.scale, causal=True,
                                              block_table=wl.block_table)
 
-    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [call(wl) for wl in wls], args.steps, args.warmup)
+    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [call(wl) for wl in wls], args.steps, args.warmup,
+                                          getattr(args, "min_warm_s", 0.0))
     call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
     tflops = w0.flops() / (call_us * 1e-6) / 1e12
     gbps = w0.algorithmic_bytes() / (call_us * 1e-6) / 1e9
@@ -370,6 +430,7 @@ def bench_prefill(args, dev):
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.torch_cpu import prefill_rows
+        threads = cpu_threads()
         q, k, v = w0.q.float().cpu(), w0.k.float().cpu(), w0.v.float().cpu()
         cu = w0.cu_seqlens.cpu()
         times = []
@@ -378,7 +439,7 @@ def bench_prefill(args, dev):
             prefill_rows(q, k, v, cu, w0.scale)
             times.append(time.perf_counter() - t0)
         us = statistics.median(times) * 1e6
-        cpu = {"value": round(us * LAYERS, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+        cpu = {"value": round(us * LAYERS, 1), "unit": "us/step", "cores": threads, "kind": "port",
                "sample": f"layer 0 ({len(lens)} sequences) with the reference's fp32 per-sequence torch prefill "
                          f"(engine/talker.py:165-167), median of 3 = {us:.0f} us, x{LAYERS} layers"}
     rec = base_record("talker prefill attn µs/step (28 layers) at 32 sequences, 1×MI355X",
@@ -411,13 +472,15 @@ def bench_admit(args, dev):
     def call(wl):
         return q3attn.flash_attn_func(wl.q, wl.k, wl.v, softmax_scale=wl.scale, causal=True)
 
-    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [call(wl) for wl in wls], args.steps, args.warmup)
+    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [call(wl) for wl in wls], args.steps, args.warmup,
+                                          getattr(args, "min_warm_s", 0.0))
     call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
     tflops = w0.flops() / (call_us * 1e-6) / 1e12
     log(f"[bench] admission prefill S={S} R={R} n={n}: {call_us:.2f} us/call, {tflops:.1f} TFLOP/s")
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.torch_cpu import prefill_prefix_rows
+        threads = cpu_threads()
         q, K, V = w0.q.float().cpu(), w0.k.float().cpu(), w0.v.float().cpu()
         times = []
         for rep in range(5):
@@ -425,7 +488,7 @@ def bench_admit(args, dev):
             prefill_prefix_rows(q, K, V, w0.scale)
             times.append(time.perf_counter() - t0)
         us = statistics.median(times) * 1e6
-        cpu = {"value": round(us * LAYERS, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+        cpu = {"value": round(us * LAYERS, 1), "unit": "us/step", "cores": threads, "kind": "port",
                "sample": f"layer 0 with the reference's fp32 torch form (engine/arrivals.py:125-131), median of 5 = "
                          f"{us:.0f} us, x{LAYERS} layers"}
     rec = base_record(f"fast-admission prefill attn µs/step (28 layers) at S={S}, R={R}, n={n}, 1×MI355X",
@@ -442,25 +505,34 @@ def bench_admit(args, dev):
 
 
 def other_workloads(args, dev):
-    """Short GPU-only runs of the other configurations beside the headline (20 graph replays each, no CPU
-    baselines; `--workload NAME` gives the full line of each): 256-row decode, 512-row code predictor, 32-sequence prefill and the
-    fast-admission prefill.  A failure is recorded in place of the numbers and does not affect the headline."""
+    """Short runs of the other configurations beside the headline (20 graph replays each; `--workload NAME` gives the
+    full line of each): the 256-row and 1-row x 64-token decodes (with their CPU baselines unless --no-cpu-baseline),
+    the 512-row code predictor, the 32-sequence prefill and the fast-admission prefill.  A failure is recorded in place
+    of the numbers and does not affect the headline."""
     import copy
 
     import torch
 
     lite = copy.copy(args)
     lite.steps, lite.warmup, lite.no_cpu_baseline, lite.no_append = 20, 3, True, True
+    lite.min_warm_s = 0.3
+    dec = copy.copy(lite)
+    dec.no_cpu_baseline = args.no_cpu_baseline
     out = {}
-    for name, fn in (("decode256", lambda: bench_decode(lite, dev, "decode256")), ("cp512", lambda: bench_cp(lite, dev)),
+    for name, fn in (("decode256", lambda: bench_decode(dec, dev, "decode256", cpu_budget_s=6.0)),
+                     ("decode1x64", lambda: bench_decode(dec, dev, "decode1x64", cpu_budget_s=2.0)),
+                     ("cp512", lambda: bench_cp(lite, dev)),
                      ("prefill32", lambda: bench_prefill(lite, dev)), ("admission_prefill", lambda: bench_admit(lite, dev))):
         try:
             r = fn()
             keep = {k: r[k] for k in ("us_per_layer_call", "us_per_call", "hbm_gbps", "pct_hbm_peak", "tflops",
-                                      "three_launch_us_per_step") if k in r}
+                                      "three_launch_us_per_step", "cold_us_per_call", "launch_floor_us_per_call")
+                    if k in r}
             keep["us_per_step"] = r["value"]
             keep["roofline_frac"] = r["roofline"]["frac"]
             keep["roofline_unit"] = r["roofline"]["unit"]
+            if r.get("cpu_baseline"):
+                keep["cpu_baseline"] = {k: r["cpu_baseline"][k] for k in ("us_per_layer_call", "gbps", "cores")}
             out[name] = keep
         except Exception as e:  # noqa: BLE001 - reported, never fatal for the headline
             out[name] = {"error": f"{type(e).__name__}: {e}"}
@@ -510,6 +582,12 @@ def main() -> int:
         rec = bench_decode(args, dev, args.workload)
         if args.workload == "decode576" and not args.no_extra:
             rec["other_workloads"] = other_workloads(args, dev)
+            if rec.get("cpu_baseline"):
+                per = {"decode576": {k: rec["cpu_baseline"][k] for k in ("us_per_layer_call", "gbps", "cores")}}
+                for k in ("decode256", "decode1x64"):
+                    if "cpu_baseline" in rec["other_workloads"].get(k, {}):
+                        per[k] = rec["other_workloads"][k]["cpu_baseline"]
+                rec["cpu_baseline"]["per_config"] = per
     elif args.workload == "cp512":
         rec = bench_cp(args, dev)
     elif args.workload == "admit":

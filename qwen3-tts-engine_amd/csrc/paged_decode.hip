@@ -51,6 +51,7 @@ constexpr int kMaxSplitTokens = 64 * kTile;        // one VGPR lane per tile of 
 constexpr int kSkMaxRows = 4096;                   // rows the stream-K prologue scans in LDS
 constexpr int kSkSlots = 2;                        // partial records per stream-K workgroup
 constexpr int kSkMaxGrid = 4096;
+constexpr int kOneSplitTokens = 128;               // table capacity up to which rows are never split
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -919,6 +920,10 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
                 (long long)page_extent);
   const int64_t max_ctx = (int64_t)max_pages_per_seq * page_size;
   if (max_ctx > (int64_t)1 << 30) return fail(Q3A_EINVAL, "%s: context capacity too large", who);
+  // Tables of at most kOneSplitTokens per row: one workgroup per row streams the whole row and writes its output,
+  // one kernel and no partial records.  Stream-K would cut such rows into one-tile pieces and merge them in a second
+  // kernel, whose launch is most of such a call.
+  if (split_tokens == 0 && max_ctx <= kOneSplitTokens) split_tokens = (int)((max_ctx + kTile - 1) / kTile * kTile);
   const bool sk = use_sk(batch, split_tokens);
   if (!sk && split_tokens == 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
   const int max_splits = sk ? 0 : ceil_div(max_ctx, split_tokens);

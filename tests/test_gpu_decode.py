@@ -165,13 +165,31 @@ def test_stream_k_tiny_workloads(cuda_device, ctx):
 
 
 def test_stream_k_many_short_rows(cuda_device):
-    """Thousands of short rows: many segments per workgroup, rows split at every range boundary."""
+    """Thousands of short rows: many segments per workgroup, rows split at every range boundary (the table is
+    wider than the 128-token capacity below which rows are never split)."""
     rng = np.random.default_rng(17)
     ctx = rng.integers(0, 41, size=4000)
-    wl = W.make_decode("short_rows", cuda_device, ctx=ctx, num_pages=16384, max_ctx=48, seed=17)
+    wl = W.make_decode("short_rows", cuda_device, ctx=ctx, num_pages=40960, max_ctx=144, seed=17)
     out = run(wl)
     assert_parity(out, decode_oracle(wl), "4000 short rows")
     assert not out[ctx == 0].float().abs().sum().item()
+
+
+@pytest.mark.parametrize("max_ctx", [16, 64, 128])
+def test_narrow_tables_run_one_workgroup_per_row(cuda_device, max_ctx):
+    """Block tables of at most 128 tokens per row (the 1-row x 64-token configuration's identity table is 4 pages):
+    one workgroup per row, no second kernel; equal to the stream-K path on a wider table over the same pages."""
+    rng = np.random.default_rng(max_ctx)
+    ctx = rng.integers(0, max_ctx + 1, size=37)
+    ctx[0] = max_ctx
+    wl = W.make_decode("narrow", cuda_device, ctx=ctx, num_pages=4096, max_ctx=max_ctx, seed=max_ctx)
+    out = run(wl)
+    assert_parity(out, decode_oracle(wl), f"narrow table {max_ctx}")
+    L = wl.layers[0]
+    wide = torch.full((wl.batch, 16), -1, dtype=torch.int32, device=cuda_device)
+    wide[:, : L.block_table.shape[1]] = L.block_table
+    ok, st = ora.compare(to_np(run(wl, bt=wide)), to_np(out), max_abs=8e-3, mean_abs=2e-4)
+    assert ok, st
 
 
 def test_batch_beyond_stream_k_limit_uses_fixed_splits(cuda_device):

@@ -93,7 +93,7 @@ def test_append_many_short_rows_stream_k(cuda_device):
     """2,000 rows of 1..40 tokens: many rows end inside each stream-K range."""
     rng = np.random.default_rng(23)
     ctx = rng.integers(1, 41, size=2000)
-    wl = W.make_decode("short", cuda_device, ctx=ctx, num_pages=8192, max_ctx=48, seed=23)
+    wl = W.make_decode("short", cuda_device, ctx=ctx, num_pages=20480, max_ctx=144, seed=23)
     k, v, old, ref_k, ref_v = _split_step(wl)
     ref = _reference(wl, ref_k, ref_v)
     L = wl.layers[0]

@@ -189,3 +189,48 @@ def test_flash_attn_func_short_key_ranges(cuda_device, R, n, causal):
     else:
         ref = np.stack([_dense(qn[i], Kn[i], Vn[i], 128 ** -0.5) for i in range(S)])
         check(out, ref, f"short keys R={R} n={n} non-causal")
+
+
+@pytest.mark.parametrize("hkv", [8, 4, 16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_many_sequences(cuda_device, hkv, causal):
+    """120 packed sequences of 0..299 tokens (zero-length and one-token ones included) with 4, 8 or 16 KV heads:
+    more workgroups than the GPU holds at once.  Within the bar of the oracle, and graph replays equal the eager
+    call."""
+    rng = np.random.default_rng(hkv * 10 + int(causal))
+    lens = rng.integers(0, 300, size=120)
+    lens[:4] = [0, 1, 299, 0]
+    T = int(lens.sum())
+    g = torch.Generator(device=cuda_device).manual_seed(hkv)
+    q = torch.randn(T, 2 * hkv, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    k = torch.randn(T, hkv, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    v = torch.randn(T, hkv, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=cuda_device)
+    max_q = int(lens.max())
+    scale = 128 ** -0.5
+    f = lambda: q3attn.flash_attn_varlen_func(q, k, v, cu, cu, max_q, max_q, softmax_scale=scale, causal=causal)
+    out = f()
+    torch.cuda.synchronize()
+    qn, kn, vn, cun = to_np(q), to_np(k), to_np(v), cu.cpu().numpy()
+    if causal:
+        ref = ora.prefill_varlen(qn, kn, vn, cun, scale)
+    else:
+        ref = np.zeros_like(qn)
+        for i in range(len(lens)):
+            sl = slice(cun[i], cun[i + 1])
+            if lens[i]:
+                ref[sl] = _dense(qn[sl], kn[sl], vn[sl], scale)
+    check(out, ref, f"varlen 120 seqs hkv={hkv} causal={causal}")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        f()
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s):
+        static = f()
+    for _ in range(3):
+        torch.randn(1 << 18, device=cuda_device)
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static, out)
