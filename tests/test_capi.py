@@ -57,7 +57,7 @@ def _decode(**kw):
     (dict(sh=-128), "page extent"),
     (dict(q_sh=1 << 30), "q head stride"),
     (dict(q_sh=-128), "q head stride"),
-    (dict(ws_bytes=10), "workspace"),
+    (dict(ws_bytes=10, max_pages=16), "workspace"),     # a 256-token table: stream-K, which needs a workspace
     (dict(B=-1), "batch"),
 ])
 def test_paged_decode_rejects_bad_arguments(kw, frag):
