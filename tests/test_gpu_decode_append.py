@@ -103,6 +103,26 @@ def test_append_many_short_rows_stream_k(cuda_device):
     assert torch.equal(wl.k_cache, ref_k) and torch.equal(wl.v_cache, ref_v)
 
 
+@pytest.mark.parametrize("max_ctx", [16, 64, 128])
+def test_append_narrow_tables_one_workgroup_per_row(cuda_device, max_ctx):
+    """Tables of at most 128 tokens take one workgroup per row, which stores the new rows itself (no second kernel):
+    bitwise equal to index_copy_ + decode, pool included, and within the bar of the oracle."""
+    rng = np.random.default_rng(40 + max_ctx)
+    ctx = rng.integers(1, max_ctx + 1, size=45)
+    ctx[:3] = [1, max_ctx, max_ctx - 1]
+    wl = W.make_decode("narrow_append", cuda_device, ctx=ctx, num_pages=4096, max_ctx=max_ctx, seed=max_ctx)
+    k, v, old, ref_k, ref_v = _split_step(wl)
+    ref = _reference(wl, ref_k, ref_v)
+    L = wl.layers[0]
+    out = q3attn.paged_decode_append(L.q, k, v, wl.k_cache, wl.v_cache, old, L.block_table, wl.scale, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), f"max_ctx={max_ctx}"
+    assert torch.equal(wl.k_cache, ref_k) and torch.equal(wl.v_cache, ref_v), "pool differs from index_copy_"
+    ok, st = ora.compare(to_np(out), decode_oracle(wl))
+    print(f"[parity] append narrow table {max_ctx} vs oracle {st}", flush=True)
+    assert ok, st
+
+
 def test_append_decode576_full_size(cuda_device):
     """576 rows (58 padded, 131,072-page pool): bitwise equal to index_copy_ + decode; every row against the oracle."""
     wl = W.make_decode("decode576", cuda_device, layers=1, seed=24)
