@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import subprocess
 import sys
 
@@ -28,13 +29,33 @@ CFLAGS = [
 ]
 
 
+def scratch_users(remarks: str) -> list[str]:
+    """Kernels whose resource-usage remarks report scratch (private) memory per lane: a register array the
+    compiler could not keep in VGPRs, which turns every access into a memory round trip."""
+    users, name = [], None
+    for ln in remarks.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", ln)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", ln)
+        if m and int(m.group(1)) > 0:
+            users.append(f"{name} ({m.group(1)} B/lane)")
+    return users
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
-    msg = "\n".join(ln for ln in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in ln)
+    lines = [ln for ln in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in ln]
+    # drop the remarks and the source excerpts the compiler prints under them
+    msg = "\n".join(ln for ln in lines if "remark:" not in ln and not re.match(r"^\s*(\d+\s+)?\|", ln))
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{msg}")
+    spills = scratch_users("\n".join(lines))
+    if spills:
+        raise RuntimeError(f"{src}: kernels using scratch memory: {', '.join(spills)}")
     if msg.strip():
         print(msg, file=sys.stderr)
     return obj

@@ -313,21 +313,24 @@ __device__ __forceinline__ void reset_state(float (&m)[kG], float (&l)[kG], floa
   }
 }
 
-// Merge the online-softmax states held by lanes l and l^mask (mask 16 or 32).
+// Merge the online-softmax states held by lanes l and l^mask (mask 16 or 32, a compile-time constant at every
+// call).  The gfx950 lane swaps (VALU, no LDS crossbar) hand each lane both states, the lower lane's first, so
+// both lanes compute the same merge, and lanes 0..15 the same arithmetic as "own state first".
 __device__ __forceinline__ void merge_lanes(int mask, float (&m)[kG], float (&l)[kG],
                                             float (&acc)[kG][8]) {
+  auto both = [mask](float x) { return mask == 16 ? swap16(x) : swap32(x); };
 #pragma unroll
   for (int h = 0; h < kG; ++h) {
-    const float mo = __shfl_xor(m[h], mask);
-    const float lo = __shfl_xor(l[h], mask);
-    const float mn = fmaxf(m[h], mo);
-    const float ws = fast_exp2(m[h] - mn);
-    const float wo = fast_exp2(mo - mn);
-    l[h] = l[h] * ws + lo * wo;
+    const float2 mm = both(m[h]);
+    const float2 ll = both(l[h]);
+    const float mn = fmaxf(mm.x, mm.y);
+    const float w0 = fast_exp2(mm.x - mn);
+    const float w1 = fast_exp2(mm.y - mn);
+    l[h] = ll.x * w0 + ll.y * w1;
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      const float ao = __shfl_xor(acc[h][d], mask);
-      acc[h][d] = acc[h][d] * ws + ao * wo;
+      const float2 aa = both(acc[h][d]);
+      acc[h][d] = aa.x * w0 + aa.y * w1;
     }
     m[h] = mn;
   }
@@ -797,6 +800,114 @@ __global__ __launch_bounds__(1024) void paged_decode_split_combine_kernel(const 
   });
 }
 
+// ------------------------------------------------------------------------------ narrow tables
+// Tables of at most kOneSplitTokens tokens per row (a.split_tokens = the table's capacity, at most kMaxRowTiles
+// tiles): one workgroup per (row, KV head) with one wave per tile of the capacity, so every tile of the row is in
+// flight at once and the call waits for two round trips: the row's context, the tile's table entry and q (and in
+// the append form the new k/v rows) together, then the tile.  Each wave reduces its tile to one online-softmax
+// state (m, l, acc of both query heads); wave 0 merges the states through LDS and writes the output row.  No
+// partial records in memory, no second kernel.  A wave whose tile lies past the context streams nothing (zero-
+// length loads) and contributes l = 0; a row with nothing to attend writes zeros.
+constexpr int kMaxRowTiles = kOneSplitTokens / kTile;
+constexpr int kRowRec = kG * kD + 2 * kG;  // floats per wave state: acc[kG][kD], m[kG], l[kG]
+
+template <bool kAppend>
+__global__ __launch_bounds__(64 * kMaxRowTiles) void paged_decode_row_kernel(const DecodeArgs a) {
+  __shared__ __align__(16) float rec[kMaxRowTiles][kRowRec];
+  const int b = blockIdx.x;
+  const int g = blockIdx.y;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // tile of this wave
+  const int lane = threadIdx.x & 63;
+  const int grp = lane >> 4;
+  const int dl = (lane & 15) * 8;
+
+  const int t = kTile * w;                 // first token of the tile
+  const int pidx = t / a.page_size;        // < max_pages: the block holds split_tokens / kTile waves
+  const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
+  uint4 q[kG];
+  load_q(a, b, g, dl, q);
+  uint4 kn = make_uint4(0u, 0u, 0u, 0u), vn = kn;
+  if constexpr (kAppend) {
+    const uint32_t dim_off = (uint32_t)(lane & 15) * 16;
+    kn = buffer_load16_s(make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2), dim_off, 0);
+    vn = buffer_load16_s(make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2), dim_off, 0);
+  }
+  const int ctx = row_ctx<kAppend>(a, b);
+
+  TileList L;                              // a one-tile list (the same value in every lane)
+  L.n = t < ctx ? 1 : 0;
+  L.page = page;
+  L.off = t - pidx * a.page_size;
+  L.nvalid = t < ctx ? min(kTile, ctx - t) : 0;
+  const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
+  KVTile T;
+  issue_tile(a, L, lane_off, grp, 0, T);
+
+  // Append form: the tile holding the row's last token takes this step's k/v rows for it (the stale slot is
+  // never used) and stores them into the slot after its loads have landed.
+  const bool tail = kAppend && L.n == 1 && t + kTile >= ctx;
+  const int tn = L.nvalid - 1;
+  if (tail) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i == (tn >> 2) && grp == (tn & 3)) {
+        T.k[i] = kn;
+        T.v[i] = vn;
+      }
+    }
+  }
+  float m[kG], l[kG], acc[kG][8];
+  reset_state(m, l, acc);
+  tile_update(a, L, q, T, 0, grp, m, l, acc);
+  if (tail && grp == (tn & 3) && (unsigned)page < (unsigned)a.num_pages) {
+    const int64_t pbase = (int64_t)page * a.kv_sp;
+    const uint32_t slot_off = (uint32_t)((L.off + 4 * (tn >> 2)) * a.kv_st * 2);
+    buffer_store16_s(kn, make_rsrc(a.kc + pbase, a.page_bytes), lane_off, slot_off);
+    buffer_store16_s(vn, make_rsrc(a.vc + pbase, a.page_bytes), lane_off, slot_off);
+  }
+
+  merge_lanes(16, m, l, acc);
+  merge_lanes(32, m, l, acc);
+  float* r = rec[w];
+  if (grp == 0) {
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+      st16(r + h * kD + dl, make_uint4(__float_as_uint(acc[h][0]), __float_as_uint(acc[h][1]),
+                                       __float_as_uint(acc[h][2]), __float_as_uint(acc[h][3])));
+      st16(r + h * kD + dl + 4, make_uint4(__float_as_uint(acc[h][4]), __float_as_uint(acc[h][5]),
+                                           __float_as_uint(acc[h][6]), __float_as_uint(acc[h][7])));
+    }
+  }
+  if (lane < kG) {
+    r[kG * kD + lane] = lane == 0 ? m[0] : m[1];
+    r[kG * kD + kG + lane] = lane == 0 ? l[0] : l[1];
+  }
+  __syncthreads();
+  if (w != 0) return;
+
+  // Wave 0: lane -> (head h = lane / 32, dims 4*(lane%32)..+4), merging the waves' states.
+  const int nw = blockDim.x >> 6;
+  const int h = lane >> 5;
+  const int d0 = (lane & 31) * 4;
+  float M = kMaxSeed;
+  for (int v = 0; v < nw; ++v) M = fmaxf(M, rec[v][kG * kD + h]);
+  float Ls = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int v = 0; v < nw; ++v) {
+    const float wgt = fast_exp2(rec[v][kG * kD + h] - M);
+    Ls += rec[v][kG * kD + kG + h] * wgt;
+    const uint4 x = ld16(&rec[v][h * kD + d0]);
+    o[0] += __uint_as_float(x.x) * wgt;
+    o[1] += __uint_as_float(x.y) * wgt;
+    o[2] += __uint_as_float(x.z) * wgt;
+    o[3] += __uint_as_float(x.w) * wgt;
+  }
+  const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+  uint2 ov;
+  ov.x = pack_bf16x2(o[0] * inv, o[1] * inv);
+  ov.y = pack_bf16x2(o[2] * inv, o[3] * inv);
+  *reinterpret_cast<uint2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0) = ov;
+}
+
 // ------------------------------------------------------------------------------ host side
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -846,6 +957,7 @@ int sk_effective_grid_host(int grid, int64_t nt) {
 bool use_sk(int batch, int split_tokens) { return split_tokens == 0 && batch <= kSkMaxRows; }
 
 size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int split_tokens) {
+  if (split_tokens == 0 && (int64_t)max_pages * page_size <= kOneSplitTokens) return 0;  // one workgroup per row
   if (use_sk(batch, split_tokens)) {
     return align256((size_t)(batch + 1) * sizeof(int)) +
            (size_t)sk_grid(hkv) * kSkSlots * hkv * kPartFloats * sizeof(float);
@@ -923,8 +1035,9 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   // Tables of at most kOneSplitTokens per row: one workgroup per row streams the whole row and writes its output,
   // one kernel and no partial records.  Stream-K would cut such rows into one-tile pieces and merge them in a second
   // kernel, whose launch is most of such a call.
-  if (split_tokens == 0 && max_ctx <= kOneSplitTokens) split_tokens = (int)((max_ctx + kTile - 1) / kTile * kTile);
-  const bool sk = use_sk(batch, split_tokens);
+  const bool narrow = split_tokens == 0 && max_ctx <= kOneSplitTokens;
+  if (narrow) split_tokens = (int)((max_ctx + kTile - 1) / kTile * kTile);
+  const bool sk = !narrow && use_sk(batch, split_tokens);
   if (!sk && split_tokens == 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
   const int max_splits = sk ? 0 : ceil_div(max_ctx, split_tokens);
   if (!sk && max_splits > kMaxSplits)
@@ -993,6 +1106,17 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   a.grid = 0;
   a.prefix = nullptr;
   a.ws = static_cast<float*>(workspace);
+  if (narrow) {
+    if (append)
+      hipLaunchKernelGGL(paged_decode_row_kernel<true>, dim3(batch, num_kv_heads), dim3(64 * (split_tokens / kTile)),
+                         0, st, a);
+    else
+      hipLaunchKernelGGL(paged_decode_row_kernel<false>, dim3(batch, num_kv_heads), dim3(64 * (split_tokens / kTile)),
+                         0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: row launch failed: %s", who, hipGetErrorString(e));
+    return Q3A_OK;
+  }
   if (append)
     hipLaunchKernelGGL(paged_decode_split_kernel<true>, dim3(batch, max_splits), block, 0, st, a);
   else

@@ -176,9 +176,10 @@ def test_stream_k_many_short_rows(cuda_device):
 
 
 @pytest.mark.parametrize("max_ctx", [16, 64, 128])
-def test_narrow_tables_run_one_workgroup_per_row(cuda_device, max_ctx):
+def test_narrow_tables_single_pass(cuda_device, max_ctx):
     """Block tables of at most 128 tokens per row (the 1-row x 64-token configuration's identity table is 4 pages):
-    one workgroup per row, no second kernel; equal to the stream-K path on a wider table over the same pages."""
+    one workgroup per (row, KV head), one wave per tile, no second kernel; within the bar of the oracle and equal
+    to the stream-K path on a wider table over the same pages."""
     rng = np.random.default_rng(max_ctx)
     ctx = rng.integers(0, max_ctx + 1, size=37)
     ctx[0] = max_ctx

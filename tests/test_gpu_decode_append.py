@@ -104,9 +104,9 @@ def test_append_many_short_rows_stream_k(cuda_device):
 
 
 @pytest.mark.parametrize("max_ctx", [16, 64, 128])
-def test_append_narrow_tables_one_workgroup_per_row(cuda_device, max_ctx):
-    """Tables of at most 128 tokens take one workgroup per row, which stores the new rows itself (no second kernel):
-    bitwise equal to index_copy_ + decode, pool included, and within the bar of the oracle."""
+def test_append_narrow_tables_single_pass(cuda_device, max_ctx):
+    """Tables of at most 128 tokens take the single-pass kernel, whose tail wave stores the new rows itself (no
+    second kernel): bitwise equal to index_copy_ + decode, pool included, and within the bar of the oracle."""
     rng = np.random.default_rng(40 + max_ctx)
     ctx = rng.integers(1, max_ctx + 1, size=45)
     ctx[:3] = [1, max_ctx, max_ctx - 1]
