@@ -73,6 +73,7 @@ struct DecodeArgs {
   float* ws;            // partial records
   int* prefix;          // stream-K: [batch + 1] tile prefix sums
   int batch, hkv, split_tokens, max_splits, grid;
+  int row_per;          // row-parallel path: tiles per wave of the table capacity (the host picks the kernel)
   float scale_log2;
 };
 
@@ -800,70 +801,117 @@ __global__ __launch_bounds__(1024) void paged_decode_split_combine_kernel(const 
   });
 }
 
-// ------------------------------------------------------------------------------ narrow tables
-// Tables of at most kOneSplitTokens tokens per row (a.split_tokens = the table's capacity, at most kMaxRowTiles
-// tiles): one workgroup per (row, KV head) with one wave per tile of the capacity, so every tile of the row is in
-// flight at once and the call waits for two round trips: the row's context, the tile's table entry and q (and in
-// the append form the new k/v rows) together, then the tile.  Each wave reduces its tile to one online-softmax
-// state (m, l, acc of both query heads); wave 0 merges the states through LDS and writes the output row.  No
-// partial records in memory, no second kernel.  A wave whose tile lies past the context streams nothing (zero-
-// length loads) and contributes l = 0; a row with nothing to attend writes zeros.
+// ------------------------------------------------------------------------------ row-parallel path
+// Narrow tables (at most kMaxRowTiles tiles of capacity per row, any batch) and small batches (at most
+// kRowMaxBatch rows, up to kRowMaxWaves * kRowMaxPer tiles): one workgroup per (row, KV head) whose W waves take
+// the row's tiles round-robin (W = the capacity in tiles up to 16, else 8; wave w streams tiles w, w + W, ..., lane i
+// of its list describing tile w + i*W), so a row's tiles are spread over up to 16 waves instead of a chain of
+// workgroups and a combine.  Everything that does not depend on the context is loaded at once: the row's context,
+// the wave's table entries (entries past the context are read but never used), q, and in the append form the new
+// k/v rows (parked in the wave's LDS until the tile that needs them); with one tile per wave (kMulti false) the
+// call then waits for two round trips.  Each wave reduces its tiles to one online-softmax state (m, l, acc of both
+// query heads); wave 0 merges the W states through LDS and writes the row.  No partial records in memory, no second
+// kernel; a row with nothing to attend writes zeros (l = 0).
 constexpr int kMaxRowTiles = kOneSplitTokens / kTile;
+constexpr int kRowMaxWaves = 16;
+constexpr int kRowMaxPer = 8;             // rows of up to kRowMaxWaves * kRowMaxPer tiles = 2,048 tokens
+constexpr int kRowMaxBatch = 64;            // beyond, stream-K (equal at 128-256 rows, ahead when ragged)
 constexpr int kRowRec = kG * kD + 2 * kG;  // floats per wave state: acc[kG][kD], m[kG], l[kG]
+// With several tiles per wave the append form needs more than the 128 registers a 16-wave workgroup allows, so both
+// forms then run 8 waves of up to 16 tiles (the same decomposition: the append form stays bitwise equal to a scatter
+// followed by the plain form).
+constexpr int row_max_waves(bool multi) { return multi ? kRowMaxWaves / 2 : kRowMaxWaves; }
 
-template <bool kAppend>
-__global__ __launch_bounds__(64 * kMaxRowTiles) void paged_decode_row_kernel(const DecodeArgs a) {
-  __shared__ __align__(16) float rec[kMaxRowTiles][kRowRec];
+template <bool kAppend, bool kMulti>
+__global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_kernel(const DecodeArgs a) {
+  __shared__ __align__(16) float rec[kRowMaxWaves][kRowRec];
+  __shared__ __align__(16) uint4 snew[kAppend ? kRowMaxWaves : 1][2][kD / 8];  // per wave: the new k and v rows
   const int b = blockIdx.x;
   const int g = blockIdx.y;
-  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // tile of this wave
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int W = (int)(blockDim.x >> 6);
   const int lane = threadIdx.x & 63;
   const int grp = lane >> 4;
   const int dl = (lane & 15) * 8;
 
-  const int t = kTile * w;                 // first token of the tile
-  const int pidx = t / a.page_size;        // < max_pages: the block holds split_tokens / kTile waves
+  const int cap = a.max_pages * a.page_size;
+  const int t = kTile * (w + lane * W);      // first token of this lane's tile
+  const int pidx = min(t, cap - 1) / a.page_size;
   const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
   uint4 q[kG];
   load_q(a, b, g, dl, q);
-  uint4 kn = make_uint4(0u, 0u, 0u, 0u), vn = kn;
   if constexpr (kAppend) {
     const uint32_t dim_off = (uint32_t)(lane & 15) * 16;
-    kn = buffer_load16_s(make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2), dim_off, 0);
-    vn = buffer_load16_s(make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2), dim_off, 0);
-  }
-  const int ctx = row_ctx<kAppend>(a, b);
-
-  TileList L;                              // a one-tile list (the same value in every lane)
-  L.n = t < ctx ? 1 : 0;
-  L.page = page;
-  L.off = t - pidx * a.page_size;
-  L.nvalid = t < ctx ? min(kTile, ctx - t) : 0;
-  const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
-  KVTile T;
-  issue_tile(a, L, lane_off, grp, 0, T);
-
-  // Append form: the tile holding the row's last token takes this step's k/v rows for it (the stale slot is
-  // never used) and stores them into the slot after its loads have landed.
-  const bool tail = kAppend && L.n == 1 && t + kTile >= ctx;
-  const int tn = L.nvalid - 1;
-  if (tail) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i == (tn >> 2) && grp == (tn & 3)) {
-        T.k[i] = kn;
-        T.v[i] = vn;
-      }
+    const uint4 kn = buffer_load16_s(make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2), dim_off, 0);
+    const uint4 vn = buffer_load16_s(make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2), dim_off, 0);
+    if (lane < kD / 8) {
+      snew[w][0][lane] = kn;
+      snew[w][1][lane] = vn;
     }
   }
+  const int ctx = row_ctx<kAppend>(a, b);
+  const int nrow = (ctx + kTile - 1) / kTile;  // tiles of the row
+
+  TileList L;
+  L.n = nrow > w ? (nrow - w + W - 1) / W : 0;
+  L.page = lane < L.n ? page : -1;
+  L.off = t - pidx * a.page_size;
+  L.nvalid = lane < L.n ? min(kTile, ctx - t) : 0;
+  const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
+
   float m[kG], l[kG], acc[kG][8];
   reset_state(m, l, acc);
-  tile_update(a, L, q, T, 0, grp, m, l, acc);
-  if (tail && grp == (tn & 3) && (unsigned)page < (unsigned)a.num_pages) {
-    const int64_t pbase = (int64_t)page * a.kv_sp;
-    const uint32_t slot_off = (uint32_t)((L.off + 4 * (tn >> 2)) * a.kv_st * 2);
-    buffer_store16_s(kn, make_rsrc(a.kc + pbase, a.page_bytes), lane_off, slot_off);
-    buffer_store16_s(vn, make_rsrc(a.vc + pbase, a.page_bytes), lane_off, slot_off);
+
+  // Append form: the row's last tile (this wave's tile jt if it owns it) holds the new token at nvalid - 1; the 16
+  // lanes holding it take this step's k/v rows instead of the stale slot, and store them after the loop.
+  const int jt = (kAppend && nrow > 0 && (nrow - 1) % W == w) ? (nrow - 1) / W : -1;
+  auto issue = [&](int j, KVTile& T) {
+    issue_tile(a, L, lane_off, grp, j, T);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto consume = [&](KVTile& T, int j) {
+    if constexpr (kAppend) {
+      if (j == jt) {
+        const int tn = readlane(L.nvalid, j) - 1;
+        const uint4 kn = snew[w][0][lane & 15];
+        const uint4 vn = snew[w][1][lane & 15];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (i == (tn >> 2) && grp == (tn & 3)) {
+            T.k[i] = kn;
+            T.v[i] = vn;
+          }
+        }
+      }
+    }
+    tile_update(a, L, q, T, j, grp, m, l, acc);
+  };
+
+  if constexpr (!kMulti) {
+    KVTile A;
+    issue(0, A);
+    consume(A, 0);
+  } else {
+    KVTile A, Bt;
+    issue(0, A);
+    for (int j = 0; j < L.n; j += 2) {
+      issue(j + 1, Bt);
+      consume(A, j);
+      issue(j + 2, A);
+      if (j + 1 < L.n) consume(Bt, j + 1);
+    }
+  }
+  if constexpr (kAppend) {
+    if (jt >= 0) {
+      const int pg = readlane(L.page, jt);
+      const int tn = readlane(L.nvalid, jt) - 1;
+      if (grp == (tn & 3) && (unsigned)pg < (unsigned)a.num_pages) {
+        const int64_t pbase = (int64_t)pg * a.kv_sp;
+        const uint32_t slot_off = (uint32_t)((readlane(L.off, jt) + 4 * (tn >> 2)) * a.kv_st * 2);
+        buffer_store16_s(snew[w][0][lane & 15], make_rsrc(a.kc + pbase, a.page_bytes), lane_off, slot_off);
+        buffer_store16_s(snew[w][1][lane & 15], make_rsrc(a.vc + pbase, a.page_bytes), lane_off, slot_off);
+      }
+    }
   }
 
   merge_lanes(16, m, l, acc);
@@ -885,14 +933,13 @@ __global__ __launch_bounds__(64 * kMaxRowTiles) void paged_decode_row_kernel(con
   __syncthreads();
   if (w != 0) return;
 
-  // Wave 0: lane -> (head h = lane / 32, dims 4*(lane%32)..+4), merging the waves' states.
-  const int nw = blockDim.x >> 6;
+  // Wave 0: lane -> (head h = lane / 32, dims 4*(lane%32)..+4), merging the W states.
   const int h = lane >> 5;
   const int d0 = (lane & 31) * 4;
   float M = kMaxSeed;
-  for (int v = 0; v < nw; ++v) M = fmaxf(M, rec[v][kG * kD + h]);
+  for (int v = 0; v < W; ++v) M = fmaxf(M, rec[v][kG * kD + h]);
   float Ls = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int v = 0; v < nw; ++v) {
+  for (int v = 0; v < W; ++v) {
     const float wgt = fast_exp2(rec[v][kG * kD + h] - M);
     Ls += rec[v][kG * kD + kG + h] * wgt;
     const uint4 x = ld16(&rec[v][h * kD + d0]);
@@ -956,8 +1003,15 @@ int sk_effective_grid_host(int grid, int64_t nt) {
 
 bool use_sk(int batch, int split_tokens) { return split_tokens == 0 && batch <= kSkMaxRows; }
 
+// The row-parallel path: narrow tables at any batch, and small batches of rows up to 2,048 tokens.
+bool use_row(int batch, int64_t max_ctx, int split_tokens) {
+  if (split_tokens != 0) return false;
+  const int64_t cap_tiles = (max_ctx + kTile - 1) / kTile;
+  return cap_tiles <= kMaxRowTiles || (batch <= kRowMaxBatch && cap_tiles <= kRowMaxWaves * kRowMaxPer);
+}
+
 size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int split_tokens) {
-  if (split_tokens == 0 && (int64_t)max_pages * page_size <= kOneSplitTokens) return 0;  // one workgroup per row
+  if (use_row(batch, (int64_t)max_pages * page_size, split_tokens)) return 0;
   if (use_sk(batch, split_tokens)) {
     return align256((size_t)(batch + 1) * sizeof(int)) +
            (size_t)sk_grid(hkv) * kSkSlots * hkv * kPartFloats * sizeof(float);
@@ -1032,12 +1086,14 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
                 (long long)page_extent);
   const int64_t max_ctx = (int64_t)max_pages_per_seq * page_size;
   if (max_ctx > (int64_t)1 << 30) return fail(Q3A_EINVAL, "%s: context capacity too large", who);
-  // Tables of at most kOneSplitTokens per row: one workgroup per row streams the whole row and writes its output,
-  // one kernel and no partial records.  Stream-K would cut such rows into one-tile pieces and merge them in a second
-  // kernel, whose launch is most of such a call.
-  const bool narrow = split_tokens == 0 && max_ctx <= kOneSplitTokens;
-  if (narrow) split_tokens = (int)((max_ctx + kTile - 1) / kTile * kTile);
-  const bool sk = !narrow && use_sk(batch, split_tokens);
+  // Narrow tables and small batches: one workgroup per (row, KV head) streams the row with up to 16 waves and
+  // writes its output, one kernel and no partial records.  Stream-K would cut such rows into short pieces and merge
+  // them in a second kernel, whose launch is most of such a call.
+  const bool row = use_row(batch, max_ctx, split_tokens);
+  const int cap_tiles = (int)((max_ctx + kTile - 1) / kTile);
+  const int row_waves = std::min(cap_tiles, row_max_waves(cap_tiles > kRowMaxWaves));
+  if (row) split_tokens = cap_tiles * kTile;
+  const bool sk = !row && use_sk(batch, split_tokens);
   if (!sk && split_tokens == 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
   const int max_splits = sk ? 0 : ceil_div(max_ctx, split_tokens);
   if (!sk && max_splits > kMaxSplits)
@@ -1075,6 +1131,7 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   a.hkv = num_kv_heads;
   a.split_tokens = split_tokens;
   a.max_splits = max_splits;
+  a.row_per = 0;
   a.scale_log2 = softmax_scale * kLog2e;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1106,13 +1163,20 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   a.grid = 0;
   a.prefix = nullptr;
   a.ws = static_cast<float*>(workspace);
-  if (narrow) {
-    if (append)
-      hipLaunchKernelGGL(paged_decode_row_kernel<true>, dim3(batch, num_kv_heads), dim3(64 * (split_tokens / kTile)),
-                         0, st, a);
-    else
-      hipLaunchKernelGGL(paged_decode_row_kernel<false>, dim3(batch, num_kv_heads), dim3(64 * (split_tokens / kTile)),
-                         0, st, a);
+  if (row) {
+    a.row_per = (cap_tiles + row_waves - 1) / row_waves;
+    const dim3 rgrid(batch, num_kv_heads), rblock(64 * row_waves);
+    if (a.row_per == 1) {
+      if (append)
+        hipLaunchKernelGGL((paged_decode_row_kernel<true, false>), rgrid, rblock, 0, st, a);
+      else
+        hipLaunchKernelGGL((paged_decode_row_kernel<false, false>), rgrid, rblock, 0, st, a);
+    } else {
+      if (append)
+        hipLaunchKernelGGL((paged_decode_row_kernel<true, true>), rgrid, rblock, 0, st, a);
+      else
+        hipLaunchKernelGGL((paged_decode_row_kernel<false, true>), rgrid, rblock, 0, st, a);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: row launch failed: %s", who, hipGetErrorString(e));
     return Q3A_OK;

@@ -57,7 +57,7 @@ def _decode(**kw):
     (dict(sh=-128), "page extent"),
     (dict(q_sh=1 << 30), "q head stride"),
     (dict(q_sh=-128), "q head stride"),
-    (dict(ws_bytes=10, max_pages=16), "workspace"),     # a 256-token table: stream-K, which needs a workspace
+    (dict(ws_bytes=10, max_pages=16, B=65), "workspace"),  # 65 rows of a 256-token table: stream-K, with workspace
     (dict(B=-1), "batch"),
 ])
 def test_paged_decode_rejects_bad_arguments(kw, frag):
@@ -81,6 +81,11 @@ def test_workspace_and_default_split():
     assert L.q3a_paged_decode_workspace_bytes(576, 16, 8, 128, 113, 16, split) == 576 * n_splits * 8 * 528
     # one split: no workspace
     assert L.q3a_paged_decode_workspace_bytes(4, 16, 8, 128, 4, 16, 64) == 0
+    # the row-parallel path (tables up to 128 tokens, or up to 64 rows of up to 2,048 tokens): no workspace
+    assert L.q3a_paged_decode_workspace_bytes(4096, 16, 8, 128, 8, 16, 0) == 0
+    assert L.q3a_paged_decode_workspace_bytes(64, 16, 8, 128, 128, 16, 0) == 0
+    assert L.q3a_paged_decode_workspace_bytes(65, 16, 8, 128, 128, 16, 0) > 0
+    assert L.q3a_paged_decode_workspace_bytes(64, 16, 8, 128, 129, 16, 0) > 0
     # small batches get smaller splits (more workgroups)
     assert L.q3a_paged_decode_default_split(1, 8, 4, 16) == 16
 

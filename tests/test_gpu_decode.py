@@ -44,9 +44,15 @@ def test_decode_1x64_single_row(cuda_device):
     assert_parity(out, decode_oracle(wl), "decode1x64")
 
 
-@pytest.mark.parametrize("split", [0, 32, 64, 128, 1024])
-def test_ragged_contexts_all_splits(cuda_device, split):
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=5)
+# Tables wider than 2,048 tokens take stream-K at any batch; up to 64 rows of narrower tables take the
+# row-parallel kernel.  The tests below run the small ragged batches through both.
+SK_CTX = 2064
+PATHS = [pytest.param(1800, id="row"), pytest.param(SK_CTX, id="sk")]
+
+
+@pytest.mark.parametrize("split,max_ctx", [(0, 1800), (0, SK_CTX), (32, 1800), (64, 1800), (128, 1800), (1024, 1800)])
+def test_ragged_contexts_all_splits(cuda_device, split, max_ctx):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=5)
     out = run(wl, split=split)
     ref = decode_oracle(wl)
     assert_parity(out, ref, f"ragged split={split}")
@@ -61,25 +67,29 @@ def test_short_contexts(cuda_device, split):
     assert_parity(run(wl, split=split), decode_oracle(wl), f"short split={split}")
 
 
-def test_ctx1_is_exact_v_row(cuda_device):
-    wl = W.make_decode("one", cuda_device, ctx=np.array([1, 1, 1]), num_pages=64, max_ctx=64, seed=9)
+@pytest.mark.parametrize("max_ctx", [64, SK_CTX])
+def test_ctx1_is_exact_v_row(cuda_device, max_ctx):
+    wl = W.make_decode("one", cuda_device, ctx=np.array([1, 1, 1]), num_pages=512, max_ctx=max_ctx, seed=9)
     out = run(wl)
     bt = wl.layers[0].block_table[:, 0].long()
     want = wl.v_cache[bt, 0]                                   # [B, Hkv, D]
     assert torch.equal(out, want.repeat_interleave(2, dim=1))
 
 
-def test_reference_layout_page256_identity(cuda_device):
-    """The reference's own pool geometry: 256-token pages, identity table, seat_len 768
-    (engine/talker.py:23-31, 42)."""
+@pytest.mark.parametrize("seat_len", [768, 2304])
+def test_reference_layout_page256_identity(cuda_device, seat_len):
+    """The reference's own pool geometry: 256-token pages, identity table, seat_len 768 (engine/talker.py:23-31, 42;
+    2,304 takes the stream-K path)."""
     ctx = np.array([1, 77, 255, 256, 257, 420, 767, 768])
-    wl = W.make_decode("ref", cuda_device, ctx=ctx, num_pages=8 * 3, max_ctx=768, page=256, identity=True, seed=2)
+    wl = W.make_decode("ref", cuda_device, ctx=ctx, num_pages=8 * seat_len // 256, max_ctx=seat_len, page=256,
+                       identity=True, seed=2)
     assert_parity(run(wl), decode_oracle(wl), "page256")
 
 
-def test_stale_nan_slots_and_garbage_table_entries(cuda_device):
+@pytest.mark.parametrize("max_ctx", PATHS)
+def test_stale_nan_slots_and_garbage_table_entries(cuda_device, max_ctx):
     """Slots past ctx in a row's last page and table entries past its last page are never read."""
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=6)
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=6)
     clean = run(wl)
     bt = wl.layers[0].block_table.clone()
     k, v = wl.k_cache.clone(), wl.v_cache.clone()
@@ -95,8 +105,9 @@ def test_stale_nan_slots_and_garbage_table_entries(cuda_device):
     assert torch.equal(clean, dirty)
 
 
-def test_out_of_range_page_ids_do_not_fault(cuda_device):
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array([40, 40]), num_pages=64, max_ctx=64, seed=3)
+@pytest.mark.parametrize("max_ctx", [64, SK_CTX])
+def test_out_of_range_page_ids_do_not_fault(cuda_device, max_ctx):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array([40, 40]), num_pages=512, max_ctx=max_ctx, seed=3)
     bt = wl.layers[0].block_table.clone()
     bt[0, 1] = -1
     bt[1, 0] = 1 << 30
@@ -104,8 +115,9 @@ def test_out_of_range_page_ids_do_not_fault(cuda_device):
     assert torch.isfinite(out.float()).all()
 
 
-def test_page_table_permutation_invariance(cuda_device):
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=8)
+@pytest.mark.parametrize("max_ctx", PATHS)
+def test_page_table_permutation_invariance(cuda_device, max_ctx):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=8)
     a = run(wl)
     perm = torch.randperm(4096, generator=torch.Generator().manual_seed(1)).to(cuda_device)
     inv = torch.argsort(perm)
@@ -113,8 +125,9 @@ def test_page_table_permutation_invariance(cuda_device):
     assert torch.equal(a, b)
 
 
-def test_strided_cache_and_query(cuda_device):
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED[:12]), num_pages=512, max_ctx=256, seed=10)
+@pytest.mark.parametrize("max_ctx", [256, SK_CTX])
+def test_strided_cache_and_query(cuda_device, max_ctx):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED[:12]), num_pages=2048, max_ctx=max_ctx, seed=10)
     NP, P, H, D = wl.k_cache.shape
     kb = torch.zeros(NP, P, H, D + 8, dtype=torch.bfloat16, device=cuda_device)
     vb = torch.zeros_like(kb)
@@ -157,11 +170,32 @@ def test_decode576_full_size(cuda_device):
 @pytest.mark.parametrize("ctx", [[1], [0, 17, 0], [0, 0], [5, 1800], [2000 // 16 * 16]])
 def test_stream_k_tiny_workloads(cuda_device, ctx):
     """Fewer tiles than stream-K workgroups: most workgroups own nothing and rows span several
-    one-tile workgroups."""
+    one-tile workgroups (tables of 2,064 tokens: past the row-parallel path's 2,048)."""
     ctx = np.array(ctx)
-    wl = W.make_decode("tiny", cuda_device, ctx=ctx, num_pages=512, max_ctx=2000, seed=int(ctx.sum()) % 97)
+    wl = W.make_decode("tiny", cuda_device, ctx=ctx, num_pages=512, max_ctx=2064, seed=int(ctx.sum()) % 97)
     out = run(wl)
     assert_parity(out, decode_oracle(wl), f"tiny {ctx.tolist()}")
+
+
+@pytest.mark.parametrize("max_ctx,ctx", [
+    (256, [256, 255, 100, 0]),                 # 16 waves, one tile each
+    (272, [272, 17, 1]),                       # 8 waves, three tiles each
+    (2048, [0, 1, 17, 1000, 2048]),            # 8 waves, sixteen tiles each
+    (1024, list(range(0, 1024, 16))),          # 64 rows, the batch limit of the path
+])
+def test_row_parallel_small_batches(cuda_device, max_ctx, ctx):
+    """Up to 64 rows of up to 2,048 tokens: one workgroup per (row, KV head), the row's tiles spread round-robin
+    over up to 16 waves and merged in LDS; within the bar of the oracle and equal to the stream-K path on a table
+    widened past the path's limit."""
+    ctx = np.array(ctx)
+    wl = W.make_decode("row_small", cuda_device, ctx=ctx, num_pages=4096, max_ctx=max_ctx, seed=max_ctx + len(ctx))
+    out = run(wl)
+    assert_parity(out, decode_oracle(wl), f"row path {max_ctx} {ctx.tolist()}")
+    L = wl.layers[0]
+    wide = torch.full((wl.batch, 129), -1, dtype=torch.int32, device=cuda_device)
+    wide[:, : L.block_table.shape[1]] = L.block_table
+    ok, st = ora.compare(to_np(run(wl, bt=wide)), to_np(out), max_abs=8e-3, mean_abs=2e-4)
+    assert ok, st
 
 
 def test_stream_k_many_short_rows(cuda_device):
@@ -221,13 +255,14 @@ def test_flash_attn_num_splits(cuda_device, num_splits):
     assert_parity(out[:, 0], decode_oracle(wl), f"num_splits={num_splits}")
 
 
-@pytest.mark.parametrize("split", [0, 32])
+@pytest.mark.parametrize("split,max_ctx", [(0, SK_CTX), (32, 1800)])
 @pytest.mark.parametrize("v_scale", [1.0 / 4096, 1.0, 3.0e5])
-def test_partial_records_keep_precision_at_extreme_v(cuda_device, split, v_scale):
+def test_partial_records_keep_precision_at_extreme_v(cuda_device, split, max_ctx, v_scale):
     """Rows cut into several segments are merged from 16-bit partial records: fp16 o for ordinary values, bf16
     when a record's largest |o| is below 2^-6 (V ~ 2.4e-4) or above 2^15 (V ~ 3e5).  Either way the result stays
-    within the bf16 output's own rounding of the oracle (relative to the largest |o|)."""
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=8)
+    within the bf16 output's own rounding of the oracle (relative to the largest |o|).  Split 0 on a table wide
+    enough for the stream-K path, whose partial records these are."""
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=8)
     v = (wl.v_cache.float() * v_scale).to(torch.bfloat16)
     wl.v_cache = v
     out = run(wl, split=split, v=v).float().cpu().numpy()

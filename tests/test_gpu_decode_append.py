@@ -58,9 +58,14 @@ def _reference(wl, ref_k, ref_v, layer=0, split=0):
     return q3attn.paged_decode(L.q, ref_k, ref_v, wl.cache_seqlens, L.block_table, wl.scale, split)
 
 
-@pytest.mark.parametrize("split", [0, 32, 1024])
-def test_append_matches_index_copy_then_decode(cuda_device, split):
-    wl = W.make_decode("append", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=21)
+# Tables wider than 2,048 tokens take stream-K at any batch; up to 64 rows of narrower tables take the
+# row-parallel kernel.
+SK_CTX = 2064
+
+
+@pytest.mark.parametrize("split,max_ctx", [(0, 1800), (0, SK_CTX), (32, 1800), (1024, 1800)])
+def test_append_matches_index_copy_then_decode(cuda_device, split, max_ctx):
+    wl = W.make_decode("append", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=21)
     k, v, old, ref_k, ref_v = _split_step(wl)
     ref = _reference(wl, ref_k, ref_v, split=split)
     L = wl.layers[0]
@@ -74,9 +79,10 @@ def test_append_matches_index_copy_then_decode(cuda_device, split):
     assert ok, st
 
 
-def test_flash_attn_kvcache_k_v_form_strided_v(cuda_device):
+@pytest.mark.parametrize("max_ctx", [1800, SK_CTX])
+def test_flash_attn_kvcache_k_v_form_strided_v(cuda_device, max_ctx):
     """The flash-attn call form (k=, v= with cache_seqlens = tokens before the append), v a strided view."""
-    wl = W.make_decode("append", cuda_device, ctx=np.array(RAGGED[1:]), num_pages=4096, max_ctx=1800, seed=22)
+    wl = W.make_decode("append", cuda_device, ctx=np.array(RAGGED[1:]), num_pages=4096, max_ctx=max_ctx, seed=22)
     k, v, old, ref_k, ref_v = _split_step(wl, v_view=True)
     ref = _reference(wl, ref_k, ref_v)
     L = wl.layers[0]
@@ -123,6 +129,24 @@ def test_append_narrow_tables_single_pass(cuda_device, max_ctx):
     assert ok, st
 
 
+@pytest.mark.parametrize("max_ctx,ctx", [(272, [272, 17, 1]), (2048, [1, 17, 1000, 2048, 640])])
+def test_append_row_parallel_small_batches(cuda_device, max_ctx, ctx):
+    """Small batches of long tables: the row-parallel kernel with 8 waves of several tiles each, the same
+    decomposition as the plain form; the wave owning each row's last tile stores the new rows.  Bitwise equal to
+    index_copy_ + decode, pool included, and within the bar of the oracle."""
+    wl = W.make_decode("row_append", cuda_device, ctx=np.array(ctx), num_pages=4096, max_ctx=max_ctx, seed=max_ctx)
+    k, v, old, ref_k, ref_v = _split_step(wl)
+    ref = _reference(wl, ref_k, ref_v)
+    L = wl.layers[0]
+    out = q3attn.paged_decode_append(L.q, k, v, wl.k_cache, wl.v_cache, old, L.block_table, wl.scale, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), f"max_ctx={max_ctx}"
+    assert torch.equal(wl.k_cache, ref_k) and torch.equal(wl.v_cache, ref_v), "pool differs from index_copy_"
+    ok, st = ora.compare(to_np(out), decode_oracle(wl))
+    print(f"[parity] append row path {max_ctx} vs oracle {st}", flush=True)
+    assert ok, st
+
+
 def test_append_decode576_full_size(cuda_device):
     """576 rows (58 padded, 131,072-page pool): bitwise equal to index_copy_ + decode; every row against the oracle."""
     wl = W.make_decode("decode576", cuda_device, layers=1, seed=24)
@@ -159,9 +183,10 @@ def test_append_rows_past_capacity_are_skipped(cuda_device):
     assert out[2].float().abs().sum().item() > 0
 
 
-def test_append_in_graph_replays(cuda_device):
+@pytest.mark.parametrize("max_ctx", [1800, SK_CTX])
+def test_append_in_graph_replays(cuda_device, max_ctx):
     """Captured into a HIP graph (as the talker frame is) and replayed: every replay equals the eager call."""
-    wl = W.make_decode("append", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=26)
+    wl = W.make_decode("append", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=26)
     k, v, old, ref_k, ref_v = _split_step(wl)
     L = wl.layers[0]
     eager = q3attn.paged_decode_append(L.q, k, v, wl.k_cache, wl.v_cache, old, L.block_table, wl.scale, 0)

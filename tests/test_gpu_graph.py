@@ -11,9 +11,10 @@ from q3attn import workloads as W
 pytestmark = pytest.mark.gpu
 
 
-def test_graph_replay_matches_eager(cuda_device):
-    wl = W.make_decode("g", cuda_device, ctx=np.array([0, 1, 33, 200, 700, 64, 1500, 3]), num_pages=1024,
-                       max_ctx=1800, layers=3, seed=12)
+@pytest.mark.parametrize("max_ctx", [1800, 2064])     # the row-parallel and the stream-K decode
+def test_graph_replay_matches_eager(cuda_device, max_ctx):
+    wl = W.make_decode("g", cuda_device, ctx=np.array([0, 1, 33, 200, 700, 64, 1500, 3]), num_pages=2048,
+                       max_ctx=max_ctx, layers=3, seed=12)
     qs, K, V = W.make_cp(32, cuda_device, seed=12)
 
     def frame():

@@ -32,6 +32,10 @@ DECODE_CASES = [
     dict(hkv=8, page=32, B=100, max_ctx=120, split=16, append=True, pad=8),
     dict(hkv=4, page=256, B=3, max_ctx=1000, split=1024, append=False, pad=0),
     dict(hkv=8, page=16, B=1, max_ctx=2000, split=0, append=True, pad=0),
+    # stream-K at small batches (tables past 2,048 tokens) and past 64 rows
+    dict(hkv=2, page=32, B=17, max_ctx=2100, split=0, append=True, pad=8),
+    dict(hkv=16, page=16, B=9, max_ctx=2100, split=0, append=False, pad=0),
+    dict(hkv=1, page=16, B=70, max_ctx=300, split=0, append=False, pad=0),
 ]
 
 

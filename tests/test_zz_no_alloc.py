@@ -42,7 +42,7 @@ def test_noalloc_matches_workspace_entry_point_twice(cuda_device):
     del big
     torch.cuda.empty_cache()
     rng = np.random.default_rng(32)
-    ctx = rng.integers(0, 700, size=37)
+    ctx = rng.integers(0, 700, size=80)    # more than 64 rows: the stream-K path, which uses the scratch
     small = W.make_decode("small", cuda_device, ctx=ctx, num_pages=4096, max_ctx=700, seed=32)
     print(f"[noalloc] call 2: {small.batch} rows, {int(small.ctx.sum())} tokens", flush=True)
     out2, want2 = _case(small)
