@@ -244,13 +244,69 @@ def bench_decode(args, dev, name, cpu_budget_s: float = 12.0):
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic() if name == "decode576" else None,
-            "kernel": "paged decode call (stream-K decode kernel + combine kernel), per call inside the graph",
+            "kernel": decode_kernel_name(wl, args.split) + ", per call inside the graph",
             "bytes_per_call": nbytes,
         },
         "cpu_baseline": cpu,
     })
     if append is not None:
         rec["append_form"] = append
+    return rec
+
+
+def decode_kernel_name(wl, split):
+    """The kernels one decode call of this workload launches (the library needs no workspace exactly when it takes
+    the row-parallel path, for split 0)."""
+    from q3attn import _lib
+
+    L = wl.layers[0]
+    ws = _lib.lib().q3a_paged_decode_workspace_bytes(wl.batch, 16, wl.k_cache.shape[2], 128,
+                                                     L.block_table.shape[1], wl.page_size, split)
+    if split:
+        return "paged decode call (fixed-split decode kernel + combine kernel)"
+    if ws == 0:
+        return "paged decode call (row-parallel kernel, one launch)"
+    return "paged decode call (stream-K decode kernel + combine kernel)"
+
+
+SMALL_SHAPES = ((1, 64), (1, 256), (1, 1024), (1, 1800), (4, 1024), (8, 512), (16, 1024), (16, 1800), (32, 512),
+                (32, 1024), (32, 1800), (64, 256), (64, 512), (64, 1024))
+
+
+def bench_decode_small(args, dev):
+    """Decode at small batches: every row of B rows at the same context length, 28 layer calls per graph replay
+    over one pool with per-layer random tables.  Each shape runs twice on the same pages: with a 2,048-token table
+    (the row-parallel kernel, the library's choice up to 64 rows) and with a 2,064-token table (past that kernel's
+    limit: stream-K decode + combine)."""
+    import numpy as np
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    shapes = {}
+    for B, ctx in SMALL_SHAPES:
+        res = {}
+        for path, max_ctx in (("row_parallel", 2048), ("stream_k", 2064)):
+            wl = W.make_decode("small", dev, ctx=np.full(B, ctx), num_pages=max(256, B * 130 * 2), max_ctx=max_ctx,
+                               layers=LAYERS, seed=args.seed + 1)
+            _, frame_ms, _ = time_graph(dev, lambda: [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens,
+                                                                          L.block_table, wl.scale, 0)
+                                                      for L in wl.layers], args.steps, args.warmup)
+            res[path] = round(statistics.median(frame_ms) * 1e3 / LAYERS, 2)
+            res[path + "_kernel"] = decode_kernel_name(wl, 0)
+            del wl
+            torch.cuda.empty_cache()
+        shapes[f"{B}x{ctx}"] = res
+        log(f"[bench] small batch {B} x {ctx}: row-parallel {res['row_parallel']:.2f} us/call, "
+            f"stream-K {res['stream_k']:.2f} us/call")
+    mean_row = statistics.mean(r["row_parallel"] for r in shapes.values())
+    rec = base_record("paged decode attn µs/call at small batches (mean over shapes), 1×MI355X", round(mean_row, 2),
+                      "us/call", args, mean_row * LAYERS / 1e3, False, {
+                          "workload": "talker paged decode attention at 1-64 rows of 64-1,800 tokens each, GQA 16/8, "
+                                      "head_dim 128, bf16, 16-token pages, 28 layer calls per step",
+                          "shapes": [f"{B}x{c}" for B, c in SMALL_SHAPES], "parallelism": "single GPU"})
+    rec["per_shape_us_per_call"] = shapes
     return rec
 
 
@@ -546,9 +602,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="decode576",
-                    choices=["decode576", "decode256", "decode1x64", "cp512", "prefill32", "admit"],
-                    help="c5 (default, the headline metric), c3 decode, c2 code predictor, c4 prefill, "
-                         "admit fast-admission prefill")
+                    choices=["decode576", "decode256", "decode1x64", "decode-small", "cp512", "prefill32", "admit"],
+                    help="c5 (default, the headline metric), c3 decode, c1 decode, decode at small batches (row-parallel "
+                         "kernel vs stream-K), c2 code predictor, c4 prefill, admit fast-admission prefill")
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-append", action="store_true", help="skip the KV-append comparison of the decode bench")
@@ -561,8 +617,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the decode attention shards by seat with no exchange; see the design notes). "
-              "Run with --gpus 1.", file=sys.stderr)
+              "(the decode attention shards by seat with no exchange). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
@@ -588,6 +643,8 @@ def main() -> int:
                     if "cpu_baseline" in rec["other_workloads"].get(k, {}):
                         per[k] = rec["other_workloads"][k]["cpu_baseline"]
                 rec["cpu_baseline"]["per_config"] = per
+    elif args.workload == "decode-small":
+        rec = bench_decode_small(args, dev)
     elif args.workload == "cp512":
         rec = bench_cp(args, dev)
     elif args.workload == "admit":
