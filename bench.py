@@ -571,7 +571,7 @@ def other_workloads(args, dev):
 
     lite = copy.copy(args)
     lite.steps, lite.warmup, lite.no_cpu_baseline, lite.no_append = 20, 3, True, True
-    lite.min_warm_s = 0.3
+    lite.min_warm_s = 1.0                 # the GPU sat idle during the CPU baseline before: let clocks ramp
     dec = copy.copy(lite)
     dec.no_cpu_baseline = args.no_cpu_baseline
     out = {}
