@@ -20,7 +20,9 @@
 // straddle a range boundary leave partial records (fp32 m, l and the normalised o in 16 bits) in at
 // most two slots per workgroup; the combine kernel merges them and writes zeros for ctx == 0 rows.
 // Alternative (split_tokens > 0): one workgroup per (row, fixed-size split), partials merged by
-// the same kind of combine.
+// the same kind of combine.  Narrow tables (at most 128 tokens) and small batches (at most 64 rows of up
+// to 2,048 tokens) take the row-parallel kernel instead: one workgroup per (row, KV head), the row's tiles
+// spread over its waves and merged in LDS, one launch.
 //
 // Append form (flash_attn_with_kvcache with k=, v=; replaces the index_copy_ pair of
 // engine/talker.py:72-73 before the call at :77): cache_seqlens counts the tokens already cached,
@@ -82,7 +84,8 @@ struct KVTile {
   uint4 v[4];
 };
 
-// Up to 64 consecutive tiles of one wave, described lane-wise.
+// Up to 64 tiles of one wave, described lane-wise: consecutive tiles in the stream-K and fixed-split kernels,
+// every W-th tile of a row in the row-parallel kernel.
 struct TileList {
   int page;    // lane i: page index of tile i
   int off;     // lane i: token offset of tile i inside its page
