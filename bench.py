@@ -483,6 +483,7 @@ def bench_prefill(args, dev):
     tflops = w0.flops() / (call_us * 1e-6) / 1e12
     gbps = w0.algorithmic_bytes() / (call_us * 1e-6) / 1e9
     log(f"[bench] c4 prefill: {call_us:.1f} us/call, {tflops:.1f} TFLOP/s, {gbps:.0f} GB/s algorithmic")
+    prompt_step = None if args.no_append else bench_prefill_append(args, dev, wls)
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.torch_cpu import prefill_rows
@@ -509,7 +510,55 @@ def bench_prefill(args, dev):
                              "mfma_tflops": round(tflops, 2), "mfma_peak_tflops": 2500.0,
                              "flops_per_call": w0.flops(), "bytes_per_call": w0.algorithmic_bytes()},
                 "cpu_baseline": cpu})
+    if prompt_step is not None:
+        rec["prompt_step"] = prompt_step
     return rec
+
+
+def bench_prefill_append(args, dev, wls):
+    """Extra information beside the prefill line: the talker's whole prompt step per layer as the engine runs it
+    (two index_copy_ scatters of k and v into the pool, engine/talker.py:161-162, then the attention over the packed
+    k/v, :169) against prefill_append, which writes the pool inside the attention launch.  The pages are the ones
+    the workload's table gives each sequence, so the frame rewrites identical values and stays replayable."""
+    import numpy as np
+    import torch
+
+    import q3attn
+
+    steps = []
+    for wl in wls:
+        bt = wl.block_table.cpu().numpy().astype(np.int64)
+        page = wl.k_cache.shape[1]
+        slot = np.concatenate([bt[s_, np.arange(L) // page] * page + np.arange(L) % page
+                               for s_, L in enumerate(wl.lens)])
+        steps.append((wl, torch.from_numpy(slot).to(dev)))
+
+    def packed():
+        return [q3attn.flash_attn_varlen_func(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len, wl.max_len,
+                                              softmax_scale=wl.scale, causal=True) for wl, _ in steps]
+
+    def scatter_then_prefill():
+        out = []
+        for wl, slot in steps:
+            wl.k_cache.view(-1, wl.k.shape[1], wl.k.shape[2]).index_copy_(0, slot, wl.k)
+            wl.v_cache.view(-1, wl.v.shape[1], wl.v.shape[2]).index_copy_(0, slot, wl.v)
+            out.append(q3attn.flash_attn_varlen_func(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len,
+                                                     wl.max_len, softmax_scale=wl.scale, causal=True))
+        return out
+
+    def fused():
+        return [q3attn.prefill_append(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len, wl.k_cache,
+                                      wl.v_cache, wl.block_table, wl.scale, True) for wl, _ in steps]
+
+    res = {}
+    for name, fn in (("packed_prefill", packed), ("index_copy_then_prefill", scatter_then_prefill),
+                     ("prefill_append", fused)):
+        _, fr, _ = time_graph(dev, fn, args.steps, args.warmup, getattr(args, "min_warm_s", 0.0))
+        res[name + "_us_per_layer_call"] = round(statistics.mean(fr) * 1e3 / LAYERS, 2)
+    log(f"[bench] prompt step: prefill_append {res['prefill_append_us_per_layer_call']:.1f} us/layer call; "
+        f"index_copy_ x2 + prefill {res['index_copy_then_prefill_us_per_layer_call']:.1f}; packed prefill alone "
+        f"{res['packed_prefill_us_per_layer_call']:.1f}")
+    return res
 
 
 def bench_admit(args, dev):
@@ -563,7 +612,8 @@ def bench_admit(args, dev):
 def other_workloads(args, dev):
     """Short runs of the other configurations beside the headline (20 graph replays each; `--workload NAME` gives the
     full line of each): the 256-row and 1-row x 64-token decodes (with their CPU baselines unless --no-cpu-baseline),
-    the 512-row code predictor, the 32-sequence prefill and the fast-admission prefill.  A failure is recorded in place
+    the 512-row code predictor, the 32-sequence prefill (with the prompt-step comparison) and the fast-admission
+    prefill.  A failure is recorded in place
     of the numbers and does not affect the headline."""
     import copy
 
@@ -574,16 +624,18 @@ def other_workloads(args, dev):
     lite.min_warm_s = 1.0                 # the GPU sat idle during the CPU baseline before: let clocks ramp
     dec = copy.copy(lite)
     dec.no_cpu_baseline = args.no_cpu_baseline
+    pre = copy.copy(lite)
+    pre.no_append = False                 # the prompt-step comparison (fused pool write) is part of this line
     out = {}
     for name, fn in (("decode256", lambda: bench_decode(dec, dev, "decode256", cpu_budget_s=6.0)),
                      ("decode1x64", lambda: bench_decode(dec, dev, "decode1x64", cpu_budget_s=2.0)),
                      ("cp512", lambda: bench_cp(lite, dev)),
-                     ("prefill32", lambda: bench_prefill(lite, dev)), ("admission_prefill", lambda: bench_admit(lite, dev))):
+                     ("prefill32", lambda: bench_prefill(pre, dev)), ("admission_prefill", lambda: bench_admit(lite, dev))):
         try:
             r = fn()
             keep = {k: r[k] for k in ("us_per_layer_call", "us_per_call", "hbm_gbps", "pct_hbm_peak", "tflops",
-                                      "three_launch_us_per_step", "cold_us_per_call", "launch_floor_us_per_call")
-                    if k in r}
+                                      "three_launch_us_per_step", "cold_us_per_call", "launch_floor_us_per_call",
+                                      "prompt_step") if k in r}
             keep["us_per_step"] = r["value"]
             keep["roofline_frac"] = r["roofline"]["frac"]
             keep["roofline_unit"] = r["roofline"]["unit"]
@@ -607,7 +659,8 @@ def main() -> int:
                          "kernel vs stream-K), c2 code predictor, c4 prefill, admit fast-admission prefill")
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-append", action="store_true", help="skip the KV-append comparison of the decode bench")
+    ap.add_argument("--no-append", action="store_true",
+                    help="skip the KV-append comparisons (decode: fused append; prefill: the prompt step)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-extra", action="store_true",
                     help="576-row decode only: skip the short GPU-only runs of the other workloads (other_workloads field)")

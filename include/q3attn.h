@@ -25,8 +25,9 @@ extern "C" {
 #define Q3A_ELAUNCH (-5)  /* the HIP runtime refused the launch */
 #define Q3A_ESPACE (-28)  /* workspace smaller than q3a_paged_decode_workspace_bytes() */
 
-/* ABI version of this header (bumped on any signature change); q3a_abi_version() returns the library's. */
-#define Q3A_ABI_VERSION 2
+/* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
+ * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append. */
+#define Q3A_ABI_VERSION 3
 int q3a_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -185,6 +186,29 @@ int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int
                 int max_pages_per_seq, const int32_t* cu_seqlens_k, void* out, int64_t o_stride_t,
                 int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
                 int head_dim, float softmax_scale, int causal, void* stream);
+
+/*
+ * Talker prefill with the prompt's K/V written into the page pool in the same launch.
+ *
+ * Replaces the two index_copy_ scatters of engine/talker.py:161-162 (k and v of every prompt token into the pool at
+ * the seat's positions 0 .. L-1) together with the attention at engine/talker.py:169.  The attention is
+ * q3a_prefill's on the packed k/v (same arguments and result, bit for bit); in addition, the K and V rows of each
+ * query token i of sequence s (key position p = Lk - Lq + i, Lq/Lk from cu_seqlens_q/k; p = i for a whole prompt)
+ * are stored into k_cache/v_cache [num_pages, page_size, Hkv, D] (strides kv_stride_page/tok/head, shared by the
+ * two pools) at page block_table[s][p / page_size], offset p % page_size.  Positions past max_pages_per_seq pages
+ * and page ids outside [0, num_pages) are not written.  k/v are the packed [Tk, Hkv, D] rows (token and head
+ * strides as in q3a_prefill).  page_size a power of two >= 16; the caches 16-byte aligned, strides multiples of 8
+ * elements, token stride >= D, page stride >= page_size * token stride.  The pool rows this call writes must not
+ * alias the packed k/v it reads.
+ */
+int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
+                       const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                       int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_k,
+                       void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                       int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                       int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_t,
+                       int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
+                       int head_dim, float softmax_scale, int causal, void* stream);
 
 /*
  * Prefix + new prefill attention on dense [S, R, H, D] tensors (MFMA): the layout flash_attn_func takes at

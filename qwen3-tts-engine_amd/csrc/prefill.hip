@@ -62,6 +62,14 @@ struct PrefillArgs {
   int causal;
   int hkv;
   float scale_log2;
+  // Append form (q3a_prefill_append): each query token's K and V rows of its KV head are also written into a page
+  // pool at the token's position in its sequence.  pk == nullptr: no write.
+  uint16_t* pk;
+  uint16_t* pv;
+  int64_t p_sp, p_st, p_sh;
+  const int32_t* pbt;
+  int64_t pbt_sb;
+  int p_pages, p_shift, p_max_pages;
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -128,9 +136,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // Element offsets of the sequence's first query/output row and first packed key row.
   int Lq, Lk;
   int64_t qbase, obase, kbase;  // kbase: the first key row of the operand this wave copies
+  int k0 = 0;
   if (a.cu_q != nullptr) {
     const int q0 = a.cu_q[s];
-    const int k0 = a.cu_k[s];
+    k0 = a.cu_k[s];
     Lq = a.cu_q[s + 1] - q0;
     Lk = a.cu_k[s + 1] - k0;
     qbase = (int64_t)q0 * a.q_st;
@@ -160,6 +169,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       uint4 x = make_uint4(0u, 0u, 0u, 0u);
       if (qvalid) x = ld16(a.q + qbase + (int64_t)tq * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
       qb[hh][kk] = as_bf16x8(x);
+    }
+  }
+
+  // Append form: the K and V rows of this workgroup's query tokens (positions Lk - Lq + token of the packed
+  // sequence) for KV head g, loaded here so they share the prologue's round trip and stored into the pool after it.
+  // Lane (r = lane >> 4, c = lane & 15) moves dims 8c..8c+7 of token 16 wave + 4i + r of the query tile.
+  uint4 wk[4], wv[4];
+  int64_t wdst[4];
+  if (a.pk != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wk[i] = make_uint4(0u, 0u, 0u, 0u);
+      wv[i] = wk[i];
+      wdst[i] = -1;
+      const int t = qt * kQT + wave * 16 + 4 * i + (lane >> 4);
+      const int pos = Lk - Lq + t;
+      const int pi = pos >> a.p_shift;
+      if (t < Lq && pos >= 0 && pi < a.p_max_pages) {
+        const int page = a.pbt[(int64_t)s * a.pbt_sb + pi];
+        const int64_t row = (int64_t)(k0 + pos);
+        wk[i] = ld16(a.k + row * a.k_st + (int64_t)g * a.k_sh + 8 * (lane & 15));
+        wv[i] = ld16(a.v + row * a.v_st + (int64_t)g * a.v_sh + 8 * (lane & 15));
+        if ((unsigned)page < (unsigned)a.p_pages)
+          wdst[i] = (int64_t)page * a.p_sp + (int64_t)(pos & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)g * a.p_sh +
+                    8 * (lane & 15);
+      }
     }
   }
 
@@ -340,6 +375,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   if (ntiles > 0) issue(0, sK0, sV0);
   wait_vmem();
   __syncthreads();
+  if (a.pk != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (wdst[i] >= 0) {
+        st16(a.pk + wdst[i], wk[i]);
+        st16(a.pv + wdst[i], wv[i]);
+      }
+    }
+  }
   for (int t = 0; t < ntiles; t += 2) {
     if (t + 1 < ntiles) issue(t + 1, sK1, sV1);
     compute(t, sK0, sV0);
@@ -619,6 +663,66 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
   a.scale_log2 = softmax_scale * kLog2e;
   a.hkv = num_kv_heads;
   return launch(a, num_seqs, max_seqlen_q, stream, "prefill");
+}
+
+extern "C" int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
+                                  const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                                  int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_k,
+                                  void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                                  int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                                  int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_t,
+                                  int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
+                                  int head_dim, float softmax_scale, int causal, void* stream) {
+  const char* who = "prefill_append";
+  if (num_seqs < 0 || max_seqlen_q < 0) return fail(Q3A_EINVAL, "%s: negative num_seqs/max_seqlen_q", who);
+  if (num_seqs == 0 || max_seqlen_q == 0) return Q3A_OK;
+  if (!cu_seqlens_q || !cu_seqlens_k || !k_cache || !v_cache || !block_table)
+    return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, k_stride_tok, k_stride_head, v_stride_tok,
+                        v_stride_head, o_stride_t, o_stride_h, num_q_heads, num_kv_heads, head_dim, who);
+  if (rc != Q3A_OK) return rc;
+  if (page_size < 16 || (page_size & (page_size - 1)) != 0)
+    return fail(Q3A_EINVAL, "%s: page_size %d must be a power of two >= 16", who, page_size);
+  if (num_pages <= 0 || max_pages_per_seq <= 0)
+    return fail(Q3A_EINVAL, "%s: num_pages and max_pages_per_seq must be > 0", who);
+  if (((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 != 0)
+    return fail(Q3A_EINVAL, "%s: k_cache/v_cache must be 16-byte aligned", who);
+  if ((kv_stride_page | kv_stride_tok | kv_stride_head) % 8 != 0 || kv_stride_tok < head_dim || kv_stride_head < 0 ||
+      kv_stride_page < (int64_t)page_size * kv_stride_tok)
+    return fail(Q3A_EINVAL, "%s: cache strides (page %lld, token %lld, head %lld) unsupported", who,
+                (long long)kv_stride_page, (long long)kv_stride_tok, (long long)kv_stride_head);
+
+  PrefillArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.cu_q = cu_seqlens_q;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.k_st = k_stride_tok;
+  a.k_sh = k_stride_head;
+  a.v_st = v_stride_tok;
+  a.v_sh = v_stride_head;
+  a.bt = nullptr;                  // attention reads the packed k/v
+  a.cu_k = cu_seqlens_k;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_st = o_stride_t;
+  a.o_sh = o_stride_h;
+  a.causal = causal ? 1 : 0;
+  a.scale_log2 = softmax_scale * kLog2e;
+  a.hkv = num_kv_heads;
+  a.pk = static_cast<uint16_t*>(k_cache);
+  a.pv = static_cast<uint16_t*>(v_cache);
+  a.p_sp = kv_stride_page;
+  a.p_st = kv_stride_tok;
+  a.p_sh = kv_stride_head;
+  a.pbt = block_table;
+  a.pbt_sb = bt_stride_b;
+  a.p_pages = num_pages;
+  a.p_shift = 0;
+  while ((1 << a.p_shift) < page_size) ++a.p_shift;
+  a.p_max_pages = max_pages_per_seq;
+  return launch(a, num_seqs, max_seqlen_q, stream, who);
 }
 
 extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,

@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (must precede the library load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -79,6 +79,16 @@ SIGNATURES = {
         _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (page, tok, head)
         _c_int, _c_int, _c_vp, _c_i64, _c_int,                 # num_pages, page_size, block_table, bt stride, max pages
         _c_vp, _c_vp, _c_i64, _c_i64,                          # cu_seqlens_k, out, o_stride_t, o_stride_h
+        _c_int, _c_int, _c_int, _c_int, _c_int,                # num_seqs, max_seqlen_q, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
+    ]),
+    "q3a_prefill_append": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_vp,                          # q, q_stride_t, q_stride_h, cu_seqlens_q
+        _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,          # k, k strides (tok, head), v, v strides (tok, head)
+        _c_vp,                                                 # cu_seqlens_k
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k_cache, v_cache, cache strides (page, tok, head)
+        _c_int, _c_int, _c_vp, _c_i64, _c_int,                 # num_pages, page_size, block_table, bt stride, max pages
+        _c_vp, _c_i64, _c_i64,                                 # out, o_stride_t, o_stride_h
         _c_int, _c_int, _c_int, _c_int, _c_int,                # num_seqs, max_seqlen_q, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
     ]),

@@ -3,7 +3,8 @@
 ``flash_attn_varlen_func`` keeps the signature the talker uses at engine/talker.py:169 and ``flash_attn_func``
 the one at engine/arrivals.py:148 (bottom-right causal for a K/V prefix longer than the queries).  Both also
 accept the paged KV pool through ``block_table`` (the layout the talker writes at engine/talker.py:161-162),
-so prefill can read K/V back from the pool.  GPU only.
+so prefill can read K/V back from the pool.  ``prefill_append`` also writes the prompt's K/V into the pool
+(engine/talker.py:161-162) in the same launch.  GPU only.
 """
 from __future__ import annotations
 
@@ -86,6 +87,55 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     _unsupported(dropout_p, window_size, softcap, alibi_slopes, return_attn_probs)
     scale = softmax_scale if softmax_scale is not None else q.shape[-1] ** -0.5
     return prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table, int(max_seqlen_q), float(scale), bool(causal))
+
+
+@torch.library.custom_op("q3attn::prefill_append", mutates_args=("k_cache", "v_cache"))
+def prefill_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                   cu_seqlens_k: torch.Tensor, max_seqlen_q: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                   block_table: torch.Tensor, softmax_scale: float, causal: bool = True) -> torch.Tensor:
+    """The talker's prompt step in one launch: the K and V rows of every query token (packed k/v [Tk, Hkv, D]) go
+    into the paged pool [num_pages, page, Hkv, D] at the token's position in its sequence, through block_table
+    [n, max_pages] (engine/talker.py:161-162 scatters them with index_copy_ at seat * seat_len + position), and the
+    result is flash_attn_varlen_func(q, k, v, ...) over the packed k/v (engine/talker.py:169), bit for bit."""
+    _req(q.is_cuda, "q3attn.prefill_append: tensors must be on a GPU (there is no CPU path)")
+    for name, t in (("k", k), ("v", v), ("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k),
+                    ("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table)):
+        _req(t.device == q.device, f"q3attn.prefill_append: {name} is on {t.device}, q on {q.device}")
+    _req(all(t.dtype == torch.bfloat16 for t in (q, k, v, k_cache, v_cache)),
+         "q3attn.prefill_append: q, k, v and the caches must be bfloat16")
+    _req(q.dim() == 3 and q.stride(-1) == 1, "q3attn.prefill_append: q must be [tokens, heads, head_dim], dim contiguous")
+    _req(k.dim() == 3 and k.shape == v.shape and k.stride(-1) == 1 and v.stride(-1) == 1,
+         "q3attn.prefill_append: k and v must be packed [tokens, kv_heads, head_dim] with a contiguous head_dim")
+    _req(k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride()
+         and k_cache.stride(-1) == 1 and k_cache.shape[2:] == k.shape[1:],
+         "q3attn.prefill_append: k_cache and v_cache must be [num_pages, page, kv_heads, head_dim] with equal strides")
+    _req(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32 and cu_seqlens_q.is_contiguous()
+         and cu_seqlens_k.is_contiguous() and cu_seqlens_q.shape == cu_seqlens_k.shape,
+         "q3attn.prefill_append: cu_seqlens_q/k must be contiguous int32 [n+1]")
+    n = cu_seqlens_q.shape[0] - 1
+    _req(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == max(n, 0)
+         and block_table.stride(1) == 1, "q3attn.prefill_append: block_table must be int32 [n, max_pages] with contiguous rows")
+    T, Hq, D = q.shape
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if n <= 0 or T == 0:
+        return out.zero_() if T else out
+    num_pages, page, Hkv, _ = k_cache.shape
+    rc = lib().q3a_prefill_append(
+        q.data_ptr(), q.stride(0), q.stride(1), cu_seqlens_q.data_ptr(),
+        k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cu_seqlens_k.data_ptr(),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        num_pages, page, block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        out.data_ptr(), out.stride(0), out.stride(1),
+        n, int(max_seqlen_q), Hq, Hkv, D, float(softmax_scale), 1 if causal else 0,
+        torch.cuda.current_stream(q.device).cuda_stream)
+    check(rc, "q3a_prefill_append")
+    return out
+
+
+@prefill_append.register_fake
+def _prefill_append_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, k_cache, v_cache, block_table,
+                         softmax_scale, causal=True):
+    return torch.empty_like(q, memory_format=torch.contiguous_format)
 
 
 @torch.library.custom_op("q3attn::prefill_dense", mutates_args=())

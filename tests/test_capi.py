@@ -251,6 +251,33 @@ def test_prefill_rejects_bad_arguments(kw, frag):
     assert frag in _lib.lib().q3a_last_error().decode()
 
 
+def _prefill_append(**kw):
+    a = dict(q=16, q_st=2048, q_sh=128, cu_q=16, k=16, k_st=1024, k_sh=128, v=16, v_st=4096, v_sh=128, cu_k=16,
+             kc=16, vc=16, c_sp=16384, c_st=1024, c_sh=128, num_pages=8, page=16, bt=16, bt_sb=4, max_pages=4,
+             out=16, o_st=2048, o_sh=128, n=2, max_q=40, Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
+    a.update(kw)
+    return _lib.lib().q3a_prefill_append(a["q"], a["q_st"], a["q_sh"], a["cu_q"], a["k"], a["k_st"], a["k_sh"],
+                                         a["v"], a["v_st"], a["v_sh"], a["cu_k"], a["kc"], a["vc"], a["c_sp"],
+                                         a["c_st"], a["c_sh"], a["num_pages"], a["page"], a["bt"], a["bt_sb"],
+                                         a["max_pages"], a["out"], a["o_st"], a["o_sh"], a["n"], a["max_q"], a["Hq"],
+                                         a["Hkv"], a["D"], a["scale"], a["causal"], None)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(kc=None), "null pointer"), (dict(bt=None), "null pointer"), (dict(cu_k=None), "null pointer"),
+    (dict(page=48), "power of two"), (dict(page=8), "power of two"), (dict(num_pages=0), "num_pages"),
+    (dict(vc=8), "aligned"), (dict(c_st=64), "cache strides"), (dict(c_sp=1024), "cache strides"),
+    (dict(c_sh=-128), "cache strides"), (dict(D=64), "head_dim"), (dict(v_st=4100), "strides"),
+])
+def test_prefill_append_rejects_bad_arguments(kw, frag):
+    assert _prefill_append(**kw) < 0
+    assert frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_prefill_append_empty_is_a_noop():
+    assert _prefill_append(n=0) == 0 and _prefill_append(max_q=0) == 0
+
+
 def test_prefill_empty_is_a_noop():
     assert _prefill(n=0) == 0 and _prefill(max_q=0) == 0
 
