@@ -173,11 +173,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   }
 
   // Append form: the K and V rows of this workgroup's query tokens (positions Lk - Lq + token of the packed
-  // sequence) for KV head g, loaded here so they share the prologue's round trip and stored into the pool after it.
-  // Lane (r = lane >> 4, c = lane & 15) moves dims 8c..8c+7 of token 16 wave + 4i + r of the query tile.
+  // sequence) for KV head g go into the pool.  Below, in general, they are loaded here so they share the prologue's
+  // round trip and stored into the pool after it (lane (r = lane >> 4, c = lane & 15) moves dims 8c..8c+7 of token
+  // 16 wave + 4i + r of the query tile).
   uint4 wk[4], wv[4];
   int64_t wdst[4];
-  if (a.pk != nullptr) {
+  // With causal masking and a K/V prefix that is a whole number of 32-key tiles (a prompt has none), the query
+  // tokens' rows are the last one or two key tiles the workgroup streams; they are stored from LDS after the loop,
+  // and the prologue only fetches the table entries of those positions (lane i: page kown0 / page_size + i).
+  const bool pool_from_lds = a.pk != nullptr && a.causal && Lk >= Lq && ((Lk - Lq) & (kKT - 1)) == 0;
+  const int kown0 = Lk - Lq + qt * kQT;
+  int pwo = -1;
+  if (pool_from_lds) {
+    const int pi = (kown0 >> a.p_shift) + lane;
+    if (lane < 8 && pi < a.p_max_pages) pwo = a.pbt[(int64_t)s * a.pbt_sb + pi];
+  }
+  if (a.pk != nullptr && !pool_from_lds) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       wk[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -375,7 +386,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   if (ntiles > 0) issue(0, sK0, sV0);
   wait_vmem();
   __syncthreads();
-  if (a.pk != nullptr) {
+  if (a.pk != nullptr && !pool_from_lds) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (wdst[i] >= 0) {
@@ -394,6 +405,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     compute(t + 1, sK1, sV1);
     wait_vmem();
     __syncthreads();
+  }
+
+  if (pool_from_lds) {
+    // Token kown0 + tl's K (part 0) and V (part 1) rows, chunk ch, from the stage its tile was copied into (tile t
+    // sits in stage t & 1; its LDS slot c holds global chunk c ^ (row & 15)).
+    const int kown1 = min(Lk, kown0 + kQT);
+    const int pi0 = kown0 >> a.p_shift;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int idx = tid + 256 * it;
+      const int tl = idx >> 5;
+      const int part = (idx >> 4) & 1;
+      const int ch = idx & 15;
+      const int key = kown0 + tl;
+      const int pi = key >> a.p_shift;
+      const int page = __shfl(pwo, min(pi - pi0, 63));
+      if (key < kown1 && pi < a.p_max_pages && (unsigned)page < (unsigned)a.p_pages) {
+        const int t = key >> 5;
+        const int row = key & (kKT - 1);
+        const uint8_t* stg = part == 0 ? ((t & 1) ? sK1 : sK0) : ((t & 1) ? sV1 : sV0);
+        const uint4 x = ld16(stg + row * kRowB + ((ch ^ (row & 15)) << 4));
+        uint16_t* dst = (part == 0 ? a.pk : a.pv) + (int64_t)page * a.p_sp +
+                        (int64_t)(key & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)g * a.p_sh + 8 * ch;
+        st16(dst, x);
+      }
+    }
   }
 
   // The 4 lanes of a token hold partial sums over disjoint keys.
