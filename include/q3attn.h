@@ -26,8 +26,8 @@ extern "C" {
 #define Q3A_ESPACE (-28)  /* workspace smaller than q3a_paged_decode_workspace_bytes() */
 
 /* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
- * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append. */
-#define Q3A_ABI_VERSION 3
+ * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope. */
+#define Q3A_ABI_VERSION 4
 int q3a_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -94,6 +94,36 @@ int q3a_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_
                             int64_t o_stride_b, int64_t o_stride_h, void* workspace, size_t workspace_bytes,
                             int batch, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
                             int split_tokens, void* stream);
+
+/*
+ * q3a_paged_decode_append with the talker's q/k producers fused in: q and k_new arrive as the raw projections and
+ * are RMS-normalised and rotated inside the call.
+ *
+ * Replaces, per layer, rope(rms(q, qn)) and rope(rms(k, kn)) (engine/talker.py:69-70, the functions of
+ * engine/ops.py:51-60), the index_copy_ pair (:72-73) and the attention (:77).
+ *
+ *   q [B, Hq, D], k_new/v_new [B, Hkv, D]   raw bf16 projections (v is used as given), strides as in
+ *                                           q3a_paged_decode_append (k_new/v_new heads packed)
+ *   q_norm_w, k_norm_w [D] bf16             RMSNorm weights
+ *   cos, sin [B, D] bf16                    each row's RoPE table row (the new token's position), row stride
+ *                                           cs_stride_b, dims contiguous
+ *   eps                                     RMSNorm epsilon (1e-6 in the talker)
+ *
+ * For each head row x: y = bf16(x * rsqrt(mean(x^2) + eps)) * w, then bf16(y * cos + rot(y) * sin) with
+ * rot(y) = (-y[D/2:], y[:D/2]), evaluated in fp32 and rounded once.  The normalised k row is what the slot receives
+ * and what the new token is attended with.  Everything else is q3a_paged_decode_append.  Needs split_tokens == 0,
+ * head_dim 128 and, above 64 rows, at most 8 KV heads; the norm weights and cos/sin rows 16-byte aligned.
+ */
+int q3a_paged_decode_append_rope(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
+                                 int64_t kn_stride_b, const void* v_new, int64_t vn_stride_b, const void* q_norm_w,
+                                 const void* k_norm_w, const void* cos, const void* sin, int64_t cs_stride_b,
+                                 float eps, void* k_cache, void* v_cache, int64_t kv_stride_page,
+                                 int64_t kv_stride_tok, int64_t kv_stride_head, int num_pages, int page_size,
+                                 const int32_t* cache_seqlens, const int32_t* block_table, int64_t bt_stride_b,
+                                 int max_pages_per_seq, void* out, int64_t o_stride_b, int64_t o_stride_h,
+                                 void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
+                                 int num_kv_heads, int head_dim, float softmax_scale, int split_tokens,
+                                 void* stream);
 
 /*
  * q3a_paged_decode without a workspace argument: it allocates nothing and takes no caller buffer beyond q, the

@@ -77,6 +77,14 @@ struct DecodeArgs {
   int batch, hkv, split_tokens, max_splits, grid;
   int row_per;          // row-parallel path: tiles per wave of the table capacity (the host picks the kernel)
   float scale_log2;
+  // Norm/rope form (kRope instantiations): q and the new k rows arrive raw and are normalised and rotated in the
+  // kernel (qk_norm_rope16/64): RMSNorm weights [kD] bf16, each row's RoPE cos/sin [kD] bf16 at row stride rs_sb.
+  const uint16_t* qn_w;
+  const uint16_t* kn_w;
+  const uint16_t* rcos;
+  const uint16_t* rsin;
+  int64_t rs_sb;
+  float eps;
 };
 
 struct KVTile {
@@ -202,6 +210,18 @@ __device__ __forceinline__ void stage_new_rows(const DecodeArgs& a, int b, int g
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2);
   lds_copy4(rk, st + kStageNew, (uint32_t)lane * 4);
   lds_copy4(rv, st + kStageNew + kD * 2, (uint32_t)lane * 4);
+}
+
+// Norm/rope form: the row's RoPE cos and sin rows (256 B each) follow at kStageRope, copied with every tile (out
+// of bounds unless the tile opens a segment or ends its row), so each tile adds the same two operations to vmcnt.
+constexpr int kStageRope = 1024;
+constexpr int kStageBytesRope = 1536;
+constexpr int kWaitGroupRope = 0x0F70 | 11;  // s_waitcnt vmcnt(11): the smallest tile group is 8 + 1 + 2 operations
+
+__device__ __forceinline__ void stage_rope(const DecodeArgs& a, int b, int lane, bool valid, uint8_t* st) {
+  const uint32_t n = valid ? kD * 2 : 0u;
+  lds_copy4(make_rsrc(a.rcos + (int64_t)b * a.rs_sb, n), st + kStageRope, (uint32_t)lane * 4);
+  lds_copy4(make_rsrc(a.rsin + (int64_t)b * a.rs_sb, n), st + kStageRope + kD * 2, (uint32_t)lane * 4);
 }
 
 // Append form, the last tile of a row, read after the next tile was issued: as take_new_token, with the new
@@ -496,18 +516,25 @@ constexpr int kLast = 2;      // tile closes a segment
 constexpr int kRowStart = 4;  // tile is tile 0 of its row
 constexpr int kRowEnd = 8;    // tile is the last tile of its row
 
-template <bool kAppend>
+template <bool kAppend, bool kRope = false>
 __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs a) {
+  static_assert(kAppend || !kRope, "the norm/rope form is an append form");
+  // The norm/rope form's larger stages are sized for 8 KV heads (the host rejects more), so two workgroups still
+  // share a CU's LDS.
+  constexpr int kSt = kRope ? kStageBytesRope : kStageBytes;
+  constexpr int kW = kRope ? 8 : kMaxWaves;
   __shared__ int s_ctx[kSkMaxRows];
   __shared__ int s_prefix[kSkMaxRows + 1];
   __shared__ int s_wsum[16];
   // Segment staging, one array per tile parity (see stage_q).
-  __shared__ __align__(16) uint8_t s_stage0[kMaxWaves * kStageBytes];
-  __shared__ __align__(16) uint8_t s_stage1[kMaxWaves * kStageBytes];
+  __shared__ __align__(16) uint8_t s_stage0[kW * kSt];
+  __shared__ __align__(16) uint8_t s_stage1[kW * kSt];
+  // Norm/rope form: the q-norm and k-norm weights.
+  __shared__ __align__(16) uint16_t s_nw[kRope ? 2 : 1][kD];
   // The record of a wave's first segment when that segment is a partial one (the tail of a row cut at the range
   // start), written to the workspace only after the tile loop: in a 576-row, 296k-token call these writes cost
   // 4.5 us inside the read stream and ~1.5 us less at the end of the range.
-  __shared__ __align__(16) float s_first[kMaxWaves][kPartFloats];
+  __shared__ __align__(16) float s_first[kW][kPartFloats];
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
   const int g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform KV head
@@ -515,6 +542,13 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   const int grp = lane >> 4;
   const int dl = (lane & 15) * 8;
   const int B = a.batch;
+
+  if constexpr (kRope) {
+    if (tid < 2 * kD / 8) {
+      const uint16_t* w = tid < kD / 8 ? a.qn_w : a.kn_w;
+      st16(&s_nw[tid / (kD / 8)][(tid % (kD / 8)) * 8], ld16(w + (tid % (kD / 8)) * 8));
+    }
+  }
 
   // Prologue: tiles per row and their exclusive prefix sum (block-wide scan).
   const int per = (B + nthr - 1) / nthr;
@@ -554,8 +588,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
   float* part = a.ws + (int64_t)blockIdx.x * kSkSlots * a.hkv * kPartFloats;
 
-  uint8_t* const st0 = s_stage0 + g * kStageBytes;
-  uint8_t* const st1 = s_stage1 + g * kStageBytes;
+  uint8_t* const st0 = s_stage0 + g * kSt;
+  uint8_t* const st1 = s_stage1 + g * kSt;
   uint4 q[kG];
   float m[kG], l[kG], acc[kG][8];
   reset_state(m, l, acc);
@@ -609,7 +643,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         // (issued before tile j+1's) has landed.  Tile j+1's group, and the append form's slot stores of
         // the previous tile, are younger; the count is the smallest group (8 loads and the q copy), so
         // the wait is exact when the younger operations are one such group and conservative otherwise.
-        __builtin_amdgcn_s_waitcnt(kWaitGroup);
+        __builtin_amdgcn_s_waitcnt(kRope ? kWaitGroupRope : kWaitGroup);
         __asm__ volatile("" ::: "memory");
       }
       if (fl & kFirst) {
@@ -637,28 +671,67 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     };
 
     auto issue = [&](int j, KVTile& T, uint8_t* st) {
-      issue_tile(a, L, lane_off, grp, j, T);
       const int jj = j < L.n ? j : 0;
       const int fl = j < L.n ? readlane(vflags, jj) : 0;
       const int row = readlane(vrow, jj);
-      stage_q(a, row, g, lane, (fl & kFirst) != 0, st);
-      if constexpr (kAppend) {
-        if (fl & kRowEnd) stage_new_rows(a, row, g, lane, st);
-      }
+      auto stage = [&]() {
+        stage_q(a, row, g, lane, (fl & kFirst) != 0, st);
+        if constexpr (kRope) stage_rope(a, row, lane, (fl & (kFirst | kRowEnd)) != 0, st);
+        if constexpr (kAppend) {
+          if (fl & kRowEnd) stage_new_rows(a, row, g, lane, st);
+        }
+      };
+      // The norm/rope form copies the stage ahead of the tile's loads, so prep() can wait for it with those loads
+      // still in flight.
+      if constexpr (kRope) stage();
+      issue_tile(a, L, lane_off, grp, j, T);
+      if constexpr (!kRope) stage();
       // Keep the whole tile's loads ahead of the consumer: no instruction of the next tile_update may
       // be scheduled between them (that would wait for the current tile in the middle of the issue).
       __builtin_amdgcn_sched_barrier(0);
     };
+    // Norm/rope form: once the tile before j has been consumed (its registers are free), the q rows tile j opens a
+    // segment with and the k row it ends its row with are normalised and rotated in place in tile j's stage, so
+    // process() reads them as the plain append form does.  Only tile j's 8 loads are younger than its stage.
+    auto prep = [&](int j, uint8_t* st) {
+      if constexpr (kRope) {
+        if (j >= L.n) return;
+        const int fl = readlane(vflags, j);
+        if (!(fl & (kFirst | kRowEnd))) return;
+        __builtin_amdgcn_s_waitcnt(0x0F70 | 8);
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* c = st + kStageRope + dl * 2;
+        const uint8_t* sn = c + kD * 2;
+        if (fl & kFirst) {
+#pragma unroll
+          for (int h = 0; h < kG; ++h) {
+            const uint4 y = qk_norm_rope16_lds(ld16(st + h * kD * 2 + dl * 2),
+                                               reinterpret_cast<const uint8_t*>(&s_nw[0][dl]), c, sn, a.eps);
+            if (grp == 0) st16(st + h * kD * 2 + dl * 2, y);
+          }
+        }
+        if (fl & kRowEnd) {
+          const uint4 y = qk_norm_rope16_lds(ld16(st + kStageNew + dl * 2),
+                                             reinterpret_cast<const uint8_t*>(&s_nw[kRope ? 1 : 0][dl]), c, sn, a.eps);
+          if (grp == 0) st16(st + kStageNew + dl * 2, y);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
 
     KVTile A, Bt;
     issue(0, A, st0);
+    prep(0, st0);
     for (int j = 0; j < L.n; j += 2) {
       open_segment(j);
       issue(j + 1, Bt, st1);
       process(A, j, st0);
+      prep(j + 1, st1);
       if (j + 1 < L.n) open_segment(j + 1);
       issue(j + 2, A, st0);
       if (j + 1 < L.n) process(Bt, j + 1, st1);
+      prep(j + 2, st0);
     }
   }
   if (first_deferred && lane < kPartFloats / 4) st16(part + g * kPartFloats + lane * 4, ld16(&s_first[g][lane * 4]));
@@ -675,7 +748,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
 // kernel, which runs without a read stream to disturb: the same 2.1 MB of 256 B stores cost ~5 us inside the decode
 // kernel's read stream (576 rows, 296k tokens).  Its loads are issued beside the merge's (the slot's page id next
 // to the record loads) and the stores come last, so the slot write adds no round trip to the merge's chain.
-template <bool kAppend>
+template <bool kAppend, bool kRope = false>
 __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
@@ -691,6 +764,10 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const Dec
     c = a.seqlens[b];
     kw = reinterpret_cast<const uint32_t*>(a.k_new + (int64_t)b * a.kn_sb + g * kD)[lane];
     vw = reinterpret_cast<const uint32_t*>(a.v_new + (int64_t)b * a.vn_sb + g * kD)[lane];
+    if constexpr (kRope)  // the same bits the decode kernel attended with (qk_norm_rope16)
+      kw = qk_norm_rope64(kw, reinterpret_cast<const uint32_t*>(a.kn_w)[lane],
+                          reinterpret_cast<const uint32_t*>(a.rcos + (int64_t)b * a.rs_sb)[lane],
+                          reinterpret_cast<const uint32_t*>(a.rsin + (int64_t)b * a.rs_sb)[lane], a.eps);
     if (c >= 0 && c < a.max_pages * a.page_size) page = a.bt[(int64_t)b * a.bt_sb + c / a.page_size];
   }
   auto store_slot = [&]() {
@@ -825,8 +902,9 @@ constexpr int kRowRec = kG * kD + 2 * kG;  // floats per wave state: acc[kG][kD]
 // followed by the plain form).
 constexpr int row_max_waves(bool multi) { return multi ? kRowMaxWaves / 2 : kRowMaxWaves; }
 
-template <bool kAppend, bool kMulti>
+template <bool kAppend, bool kMulti, bool kRope = false>
 __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_kernel(const DecodeArgs a) {
+  static_assert(kAppend || !kRope, "the norm/rope form is an append form");
   __shared__ __align__(16) float rec[kRowMaxWaves][kRowRec];
   __shared__ __align__(16) uint4 snew[kAppend ? kRowMaxWaves : 1][2][kD / 8];  // per wave: the new k and v rows
   const int b = blockIdx.x;
@@ -843,10 +921,19 @@ __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_k
   const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
   uint4 q[kG];
   load_q(a, b, g, dl, q);
+  uint4 rc = make_uint4(0u, 0u, 0u, 0u), rs = rc;
+  if constexpr (kRope) {
+    rc = ld16(a.rcos + (int64_t)b * a.rs_sb + dl);
+    rs = ld16(a.rsin + (int64_t)b * a.rs_sb + dl);
+    const uint4 w = ld16(a.qn_w + dl);
+#pragma unroll
+    for (int h = 0; h < kG; ++h) q[h] = qk_norm_rope16(q[h], w, rc, rs, a.eps);
+  }
   if constexpr (kAppend) {
     const uint32_t dim_off = (uint32_t)(lane & 15) * 16;
-    const uint4 kn = buffer_load16_s(make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2), dim_off, 0);
+    uint4 kn = buffer_load16_s(make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2), dim_off, 0);
     const uint4 vn = buffer_load16_s(make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2), dim_off, 0);
+    if constexpr (kRope) kn = qk_norm_rope16(kn, ld16(a.kn_w + dl), rc, rs, a.eps);
     if (lane < kD / 8) {
       snew[w][0][lane] = kn;
       snew[w][1][lane] = vn;
@@ -974,18 +1061,20 @@ int default_split(int batch, int hkv, int max_pages, int page_size) {
 // Workgroups of the stream-K kernel the current device holds at once (cached per device).
 // The workspace is sized for the larger of the two forms, so one buffer serves both.  Entries are atomics: two
 // host threads may fill the same entry at once (both store the same value).
-int sk_grid_of(int hkv, bool append) {
-  static std::atomic<int> cache[64][17][2];
+// form: 0 plain, 1 append, 2 append with the q/k norm and rope.
+int sk_grid_of(int hkv, int form) {
+  static std::atomic<int> cache[64][17][3];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kSkMaxGrid;
-  std::atomic<int>& c = cache[dev][hkv][append ? 1 : 0];
+  std::atomic<int>& c = cache[dev][hkv][form];
   const int cached = c.load(std::memory_order_relaxed);
   if (cached > 0) return cached;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return kSkMaxGrid;
   const hipError_t e =
-      append ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true>, 64 * hkv, 0)
-             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<false>, 64 * hkv, 0);
+      form == 2   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true, true>, 64 * hkv, 0)
+      : form == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true>, 64 * hkv, 0)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<false>, 64 * hkv, 0);
   if (e != hipSuccess) return kSkMaxGrid;
   int g = cus * (per_cu > 0 ? per_cu : 1);
   g = g < 1 ? 1 : (g > kSkMaxGrid ? kSkMaxGrid : g);
@@ -994,8 +1083,8 @@ int sk_grid_of(int hkv, bool append) {
 }
 
 int sk_grid(int hkv) {
-  const int g0 = sk_grid_of(hkv, false), g1 = sk_grid_of(hkv, true);
-  return g0 > g1 ? g0 : g1;
+  const int g0 = sk_grid_of(hkv, 0), g1 = sk_grid_of(hkv, 1), g2 = hkv <= 8 ? sk_grid_of(hkv, 2) : 0;
+  return std::max(g0, std::max(g1, g2));
 }
 
 // Host copy of sk_effective_grid for a tile-count bound (non-decreasing in the count).
@@ -1046,6 +1135,16 @@ extern "C" size_t q3a_paged_decode_workspace_bytes(int batch, int num_q_heads, i
   return workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, split_tokens);
 }
 
+// The norm/rope form's extra inputs (q3a_paged_decode_append_rope).
+struct NormRope {
+  const void* q_norm_w;
+  const void* k_norm_w;
+  const void* cos;
+  const void* sin;
+  int64_t cs_stride_b;
+  float eps;
+};
+
 static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_new,
                          int64_t kn_stride_b, const void* v_new, int64_t vn_stride_b, const void* k_cache,
                          const void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head,
@@ -1053,7 +1152,7 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
                          int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_b,
                          int64_t o_stride_h, void* workspace, size_t workspace_bytes_, int batch, int num_q_heads,
                          int num_kv_heads, int head_dim, float softmax_scale, int split_tokens, void* stream,
-                         const char* who) {
+                         const char* who, const NormRope* nr = nullptr) {
   const bool append = k_new != nullptr;
   if (batch < 0) return fail(Q3A_EINVAL, "%s: batch %d < 0", who, batch);
   if (batch == 0) return Q3A_OK;
@@ -1106,6 +1205,20 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     return fail(Q3A_ESPACE, "%s: workspace %zu bytes < %zu needed", who, workspace_bytes_, need);
   if (need > 0 && (uintptr_t)workspace % 16 != 0)
     return fail(Q3A_EINVAL, "%s: workspace must be 16-byte aligned", who);
+  if (nr != nullptr) {
+    if (!append) return fail(Q3A_EINVAL, "%s: the norm/rope form needs k_new/v_new", who);
+    if (!row && !sk) return fail(Q3A_EINVAL, "%s: the norm/rope form needs split_tokens == 0 and batch <= %d", who,
+                                 kSkMaxRows);
+    if (sk && num_kv_heads > 8)
+      return fail(Q3A_EINVAL, "%s: the norm/rope form supports at most 8 KV heads (got %d)", who, num_kv_heads);
+    if (!nr->q_norm_w || !nr->k_norm_w || !nr->cos || !nr->sin)
+      return fail(Q3A_EINVAL, "%s: null norm weight or cos/sin pointer", who);
+    if (((uintptr_t)nr->q_norm_w | (uintptr_t)nr->k_norm_w | (uintptr_t)nr->cos | (uintptr_t)nr->sin) % 16 != 0 ||
+        nr->cs_stride_b % 8 != 0 || nr->cs_stride_b < 0)
+      return fail(Q3A_EINVAL, "%s: norm weights and cos/sin rows must be 16-byte aligned (row stride %lld)", who,
+                  (long long)nr->cs_stride_b);
+    if (!(nr->eps >= 0.f) || nr->eps > 1.f) return fail(Q3A_EINVAL, "%s: eps %g outside [0, 1]", who, (double)nr->eps);
+  }
 
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -1136,6 +1249,13 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   a.max_splits = max_splits;
   a.row_per = 0;
   a.scale_log2 = softmax_scale * kLog2e;
+  const bool rope = nr != nullptr;
+  a.qn_w = rope ? static_cast<const uint16_t*>(nr->q_norm_w) : nullptr;
+  a.kn_w = rope ? static_cast<const uint16_t*>(nr->k_norm_w) : nullptr;
+  a.rcos = rope ? static_cast<const uint16_t*>(nr->cos) : nullptr;
+  a.rsin = rope ? static_cast<const uint16_t*>(nr->sin) : nullptr;
+  a.rs_sb = rope ? nr->cs_stride_b : 0;
+  a.eps = rope ? nr->eps : 0.f;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 block(64 * num_kv_heads);
@@ -1145,17 +1265,21 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     // workgroups past sk_effective_grid of the actual count exit after the prologue (every workgroup computes the
     // same effective grid from a.grid, so bounding a.grid here changes no range when the bound holds).
     const int64_t nt_bound = (int64_t)batch * ceil_div(max_ctx, kTile);
-    a.grid = sk_grid_of(num_kv_heads, append);
+    a.grid = sk_grid_of(num_kv_heads, rope ? 2 : (append ? 1 : 0));
     a.grid = sk_effective_grid_host(a.grid, nt_bound);
     a.prefix = static_cast<int*>(workspace);
     a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256((size_t)(batch + 1) * sizeof(int)));
-    if (append)
+    if (rope)
+      hipLaunchKernelGGL((paged_decode_sk_kernel<true, true>), dim3(a.grid), block, 0, st, a);
+    else if (append)
       hipLaunchKernelGGL(paged_decode_sk_kernel<true>, dim3(a.grid), block, 0, st, a);
     else
       hipLaunchKernelGGL(paged_decode_sk_kernel<false>, dim3(a.grid), block, 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: stream-K launch failed: %s", who, hipGetErrorString(e));
-    if (append)
+    if (rope)
+      hipLaunchKernelGGL((paged_decode_sk_combine_kernel<true, true>), dim3(batch), block, 0, st, a);
+    else if (append)
       hipLaunchKernelGGL(paged_decode_sk_combine_kernel<true>, dim3(batch), block, 0, st, a);
     else
       hipLaunchKernelGGL(paged_decode_sk_combine_kernel<false>, dim3(batch), block, 0, st, a);
@@ -1170,12 +1294,16 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     a.row_per = (cap_tiles + row_waves - 1) / row_waves;
     const dim3 rgrid(batch, num_kv_heads), rblock(64 * row_waves);
     if (a.row_per == 1) {
-      if (append)
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_row_kernel<true, false, true>), rgrid, rblock, 0, st, a);
+      else if (append)
         hipLaunchKernelGGL((paged_decode_row_kernel<true, false>), rgrid, rblock, 0, st, a);
       else
         hipLaunchKernelGGL((paged_decode_row_kernel<false, false>), rgrid, rblock, 0, st, a);
     } else {
-      if (append)
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_row_kernel<true, true, true>), rgrid, rblock, 0, st, a);
+      else if (append)
         hipLaunchKernelGGL((paged_decode_row_kernel<true, true>), rgrid, rblock, 0, st, a);
       else
         hipLaunchKernelGGL((paged_decode_row_kernel<false, true>), rgrid, rblock, 0, st, a);
@@ -1231,6 +1359,23 @@ extern "C" int q3a_paged_decode_append(const void* q, int64_t q_stride_b, int64_
                        block_table, bt_stride_b, max_pages_per_seq, out, o_stride_b, o_stride_h, workspace,
                        workspace_bytes_, batch, num_q_heads, num_kv_heads, head_dim, softmax_scale, split_tokens,
                        stream, "paged_decode_append");
+}
+
+extern "C" int q3a_paged_decode_append_rope(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_new, int64_t kn_stride_b, const void* v_new,
+    int64_t vn_stride_b, const void* q_norm_w, const void* k_norm_w, const void* cos, const void* sin,
+    int64_t cs_stride_b, float eps, void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+    int64_t kv_stride_head, int num_pages, int page_size, const int32_t* cache_seqlens, const int32_t* block_table,
+    int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_b, int64_t o_stride_h, void* workspace,
+    size_t workspace_bytes_, int batch, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
+    int split_tokens, void* stream) {
+  if (!k_new || !v_new) return fail(Q3A_EINVAL, "paged_decode_append_rope: null k_new/v_new");
+  const NormRope nr{q_norm_w, k_norm_w, cos, sin, cs_stride_b, eps};
+  return launch_decode(q, q_stride_b, q_stride_h, k_new, kn_stride_b, v_new, vn_stride_b, k_cache, v_cache,
+                       kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, cache_seqlens,
+                       block_table, bt_stride_b, max_pages_per_seq, out, o_stride_b, o_stride_h, workspace,
+                       workspace_bytes_, batch, num_q_heads, num_kv_heads, head_dim, softmax_scale, split_tokens,
+                       stream, "paged_decode_append_rope", &nr);
 }
 
 // ------------------------------------------------------------------------------ allocation-free entry point

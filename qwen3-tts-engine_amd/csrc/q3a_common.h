@@ -151,6 +151,98 @@ __device__ __forceinline__ float sum_xor16(float x) { const float2 r = swap16(x)
 __device__ __forceinline__ float max_xor32(float x) { const float2 r = swap32(x); return fmaxf(r.x, r.y); }
 __device__ __forceinline__ float max_xor16(float x) { const float2 r = swap16(x); return fmaxf(r.x, r.y); }
 
+// ---------------------------------------------------------------------------------- qk-norm + RoPE
+// One 128-dim bf16 head row x, its RMSNorm weight w and the row's RoPE cos/sin (engine/ops.py:51-60, the talker's
+// q/k producers at engine/talker.py:69-70):
+//   y = bf16(x * rsqrt(mean(x^2) + eps)) * w        (normalise in fp32, round to bf16, scale)
+//   o = bf16(y * cos + rot(y) * sin),  rot(y) = (-y[64:], y[:64])
+// The rope is evaluated in fp32 and rounded once, as the compiled talker evaluates the fused rms -> rope chain; its
+// products are exact in fp32 (bf16 x bf16 x bf16 needs at most 24 significant bits).  The sum of squares follows one
+// binary tree over the dims in index order (pairs, pairs of pairs, ...), so the 16-lane layout (8 dims per lane,
+// used where a row meets the tile engine) and the 64-lane layout (2 dims per lane, used where a row is stored) give
+// the same bits.  All lanes of the wave must be active.
+constexpr int kDppRor8 = 0x128;  // row_ror:8 (lane i <- lane i^8 within each 16 lanes)
+
+__device__ __forceinline__ float rms_rsqrt(float sumsq, float eps) {
+  return __builtin_amdgcn_rsqf(sumsq * (1.0f / 128.0f) + eps);
+}
+
+// Lane l of each aligned 16-lane group holds dims 8*(l%16)..+8 of its row (x, w, cos, sin alike).
+__device__ __forceinline__ uint4 qk_norm_rope16(uint4 x, uint4 w, uint4 c, uint4 s, float eps) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ws[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t cs[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_lo(xs[i]);
+    v[2 * i + 1] = bf16_hi(xs[i]);
+  }
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = v[2 * i] * v[2 * i] + v[2 * i + 1] * v[2 * i + 1];
+  const float r = rms_rsqrt(row16_sum((p[0] + p[1]) + (p[2] + p[3])), eps);
+  const bool lo = (threadIdx.x & 8) == 0;  // dims 0..63: rot = -y[d + 64]
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float y[2], out[2];
+    y[0] = round_bf16(v[2 * i] * r) * bf16_lo(ws[i]);
+    y[1] = round_bf16(v[2 * i + 1] * r) * bf16_hi(ws[i]);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float yp = dpp_f32<kDppRor8>(y[e]);
+      const float cv = e ? bf16_hi(cs[i]) : bf16_lo(cs[i]);
+      const float sv = e ? bf16_hi(ss[i]) : bf16_lo(ss[i]);
+      out[e] = fmaf(y[e], cv, (lo ? -yp : yp) * sv);
+    }
+    o[i] = pack_bf16x2(out[0], out[1]);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// qk_norm_rope16 with the weight and cos/sin chunks read from LDS a word at a time (the lane's 16 B chunk at w, c,
+// s), for kernels whose tile pipeline leaves few registers free: same arithmetic, same bits.
+__device__ __forceinline__ uint4 qk_norm_rope16_lds(uint4 x, const uint8_t* w, const uint8_t* c, const uint8_t* s,
+                                                    float eps) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v0 = bf16_lo(xs[i]), v1 = bf16_hi(xs[i]);
+    p[i] = v0 * v0 + v1 * v1;
+  }
+  const float r = rms_rsqrt(row16_sum((p[0] + p[1]) + (p[2] + p[3])), eps);
+  const bool lo = (threadIdx.x & 8) == 0;
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t ww = *reinterpret_cast<const uint32_t*>(w + 4 * i);
+    const uint32_t cw = *reinterpret_cast<const uint32_t*>(c + 4 * i);
+    const uint32_t sw = *reinterpret_cast<const uint32_t*>(s + 4 * i);
+    const float y0 = round_bf16(bf16_lo(xs[i]) * r) * bf16_lo(ww);
+    const float y1 = round_bf16(bf16_hi(xs[i]) * r) * bf16_hi(ww);
+    const float p0 = dpp_f32<kDppRor8>(y0), p1 = dpp_f32<kDppRor8>(y1);
+    o[i] = pack_bf16x2(fmaf(y0, bf16_lo(cw), (lo ? -p0 : p0) * bf16_lo(sw)),
+                       fmaf(y1, bf16_hi(cw), (lo ? -p1 : p1) * bf16_hi(sw)));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Lane l holds dims 2l, 2l+1 of the row.
+__device__ __forceinline__ uint32_t qk_norm_rope64(uint32_t x, uint32_t w, uint32_t c, uint32_t s, float eps) {
+  const float v0 = bf16_lo(x), v1 = bf16_hi(x);
+  const float p = row16_sum(v0 * v0 + v1 * v1);
+  const float r = rms_rsqrt(sum_xor32(sum_xor16(p)), eps);
+  const float y0 = round_bf16(v0 * r) * bf16_lo(w);
+  const float y1 = round_bf16(v1 * r) * bf16_hi(w);
+  const float2 e0 = swap32(y0), e1 = swap32(y1);  // (lane l & ~32's value, lane l | 32's value)
+  const bool lo = (threadIdx.x & 32) == 0;
+  const float yp0 = lo ? e0.y : e0.x, yp1 = lo ? e1.y : e1.x;
+  const float o0 = fmaf(y0, bf16_lo(c), (lo ? -yp0 : yp0) * bf16_lo(s));
+  const float o1 = fmaf(y1, bf16_hi(c), (lo ? -yp1 : yp1) * bf16_hi(s));
+  return pack_bf16x2(o0, o1);
+}
+
 }  // namespace q3a
 
 // ---------------------------------------------------------------------------------- host side

@@ -3,6 +3,7 @@
 Entry points (each a drop-in for the reference call it names):
   * ``flash_attn_with_kvcache`` / ``paged_decode``  -- talker decode attention (engine/talker.py:77)
   * ``paged_decode_append`` (``k=``/``v=`` form)   -- KV append + decode (engine/talker.py:72-73, :77)
+  * ``paged_decode_append_rope``                     -- q/k RMSNorm + RoPE, KV append and decode (engine/talker.py:69-77)
   * ``cp_attn`` / ``cp_attn_append``                 -- code-predictor attention (engine/cp_attn.py:33-39;
                                                        slot write fused: engine/code_predictor.py:58)
   * ``flash_attn_varlen_func`` / ``flash_attn_func``  -- prefill (engine/talker.py:169, engine/arrivals.py:148)
@@ -13,6 +14,6 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 from ._lib import LIB_PATH, Q3AttnError, lib  # noqa: F401
 from .cp_attn import cp_attn, cp_attn_append, cp_attn_append_op, cp_attn_op  # noqa: F401
-from .ops import flash_attn_with_kvcache, paged_decode, paged_decode_append  # noqa: F401
+from .ops import flash_attn_with_kvcache, paged_decode, paged_decode_append, paged_decode_append_rope  # noqa: F401
 from .pages import PagePool, PoolExhausted  # noqa: F401
 from .prefill import flash_attn_func, flash_attn_varlen_func, prefill, prefill_append, prefill_dense  # noqa: F401

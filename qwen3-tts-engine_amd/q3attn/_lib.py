@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (must precede the library load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -38,6 +38,18 @@ SIGNATURES = {
     "q3a_paged_decode_append": (_c_int, [
         _c_vp, _c_i64, _c_i64,                      # q, q_stride_b, q_stride_h
         _c_vp, _c_i64, _c_vp, _c_i64,               # k_new, kn_stride_b, v_new, vn_stride_b
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,       # k_cache, v_cache, kv strides (page, tok, head)
+        _c_int, _c_int,                             # num_pages, page_size
+        _c_vp, _c_vp, _c_i64, _c_int,               # cache_seqlens, block_table, bt_stride_b, max_pages
+        _c_vp, _c_i64, _c_i64,                      # out, o_stride_b, o_stride_h
+        _c_vp, _c_size,                             # workspace, workspace_bytes
+        _c_int, _c_int, _c_int, _c_int,             # batch, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                    # softmax_scale, split_tokens, stream
+    ]),
+    "q3a_paged_decode_append_rope": (_c_int, [
+        _c_vp, _c_i64, _c_i64,                      # q, q_stride_b, q_stride_h
+        _c_vp, _c_i64, _c_vp, _c_i64,               # k_new, kn_stride_b, v_new, vn_stride_b
+        _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_float,  # q_norm_w, k_norm_w, cos, sin, cs_stride_b, eps
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,       # k_cache, v_cache, kv strides (page, tok, head)
         _c_int, _c_int,                             # num_pages, page_size
         _c_vp, _c_vp, _c_i64, _c_int,               # cache_seqlens, block_table, bt_stride_b, max_pages

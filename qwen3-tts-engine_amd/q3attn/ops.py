@@ -147,6 +147,70 @@ def _paged_decode_append_fake(q, k, v, k_cache, v_cache, cache_seqlens, block_ta
     return q.new_empty(q.shape)
 
 
+def _rope_rows(x: torch.Tensor, B: int, D: int, dev, name: str) -> torch.Tensor:
+    """cos/sin of each row's new position: [B, D] or the talker's [B, 1, D] (engine/talker.py:108)."""
+    _req(x.device == dev and x.dtype == torch.bfloat16, f"q3attn.paged_decode_append_rope: {name} must be bfloat16 "
+         "on q's device")
+    if x.dim() == 3:
+        _req(x.shape[1] == 1, f"q3attn.paged_decode_append_rope: {name} must be [B, {D}] or [B, 1, {D}]")
+        x = x[:, 0]
+    _req(tuple(x.shape) == (B, D) and x.stride(1) == 1,
+         f"q3attn.paged_decode_append_rope: {name} must be [B, {D}] with contiguous rows")
+    _req(x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0,
+         f"q3attn.paged_decode_append_rope: {name} rows must be 16-byte aligned")
+    return x
+
+
+@torch.library.custom_op("q3attn::paged_decode_append_rope", mutates_args=("k_cache", "v_cache"))
+def paged_decode_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
+                             k_norm_w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
+                             v_cache: torch.Tensor, cache_seqlens: torch.Tensor, block_table: torch.Tensor,
+                             softmax_scale: float, eps: float = 1e-6) -> torch.Tensor:
+    """The talker's per-layer attention block in one launch (engine/talker.py:69-77): q and k arrive as the raw
+    projections (views of the qkv output), are RMS-normalised with q_norm_w / k_norm_w and rotated with each row's
+    cos/sin (engine/ops.py:51-60), k and v are written at position p = cache_seqlens[b] of row b, and the attention of
+    q[b] over tokens 0..p is returned, as paged_decode_append does for already-normalised q and k."""
+    _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table)
+    B, Hq, D = q.shape
+    num_pages, page, Hkv, _ = k_cache.shape
+    dev = q.device
+    _req(k.device == dev and v.device == dev, "q3attn.paged_decode_append_rope: k, v must be on q's device")
+    k3 = _new_rows(k, B, Hkv, D, "k")
+    v3 = _new_rows(v, B, Hkv, D, "v")
+    for name, w in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w)):
+        _req(w.device == dev and w.dtype == torch.bfloat16 and tuple(w.shape) == (D,) and w.is_contiguous()
+             and w.data_ptr() % 16 == 0, f"q3attn.paged_decode_append_rope: {name} must be a contiguous, "
+             f"16-byte aligned bfloat16 [{D}] tensor on q's device")
+    c2 = _rope_rows(cos, B, D, dev, "cos")
+    s2 = _rope_rows(sin, B, D, dev, "sin")
+    _req(c2.stride(0) == s2.stride(0), "q3attn.paged_decode_append_rope: cos and sin must share a row stride")
+    max_pages = block_table.shape[1]
+    out = torch.empty((B, Hq, D), dtype=q.dtype, device=dev)
+    if B == 0:
+        return out
+    L = lib()
+    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, 0)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    rc = L.q3a_paged_decode_append_rope(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k3.data_ptr(), k3.stride(0), v3.data_ptr(), v3.stride(0),
+        q_norm_w.data_ptr(), k_norm_w.data_ptr(), c2.data_ptr(), s2.data_ptr(), c2.stride(0), float(eps),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        num_pages, page,
+        cache_seqlens.data_ptr(), block_table.data_ptr(), block_table.stride(0), max_pages,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), ws_bytes,
+        B, Hq, Hkv, D, float(softmax_scale), 0, _stream(dev))
+    check(rc, "q3a_paged_decode_append_rope")
+    return out
+
+
+@paged_decode_append_rope.register_fake
+def _paged_decode_append_rope_fake(q, k, v, q_norm_w, k_norm_w, cos, sin, k_cache, v_cache, cache_seqlens,
+                                   block_table, softmax_scale, eps=1e-6):
+    return q.new_empty(q.shape)
+
+
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
                             cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None,
                             block_table=None, softmax_scale=None, causal=False, window_size=(-1, -1),

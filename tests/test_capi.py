@@ -171,6 +171,48 @@ def test_paged_decode_append_rejects_bad_arguments(kw, frag):
     assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
 
 
+@pytest.mark.parametrize("kw,frag", [
+    (dict(qn=None), "norm weight"), (dict(cs=None), "cos/sin"), (dict(cs=24), "16-byte aligned"),
+    (dict(cs_sb=100), "16-byte aligned"), (dict(eps=-1.0), "eps"), (dict(split=64), "split_tokens == 0"),
+    (dict(B=65, max_pages=256, Hkv=16, Hq=32), "at most 8 KV heads"), (dict(kn=None), "k_new"),
+    (dict(page=24), "page_size"),
+])
+def test_paged_decode_append_rope_rejects_bad_arguments(kw, frag):
+    a = dict(q=16, q_sb=2048, q_sh=128, kn=16, kn_sb=1024, vn=16, vn_sb=4096, qn=16, knw=16, cs=16, cs_sb=128,
+             eps=1e-6, k=16, v=16, sp=16384, st=1024, sh=128, num_pages=8, page=16, seqlens=16, bt=16, bt_sb=4,
+             max_pages=4, out=16, o_sb=2048, o_sh=128, ws=16, ws_bytes=1 << 30, B=2, Hq=16, Hkv=8, D=128,
+             scale=0.088, split=0)
+    a.update(kw)
+    rc = _lib.lib().q3a_paged_decode_append_rope(
+        a["q"], a["q_sb"], a["q_sh"], a["kn"], a["kn_sb"], a["vn"], a["vn_sb"], a["qn"], a["knw"], a["cs"], a["cs"],
+        a["cs_sb"], a["eps"], a["k"], a["v"], a["sp"], a["st"], a["sh"], a["num_pages"], a["page"], a["seqlens"],
+        a["bt"], a["bt_sb"], a["max_pages"], a["out"], a["o_sb"], a["o_sh"], a["ws"], a["ws_bytes"], a["B"], a["Hq"],
+        a["Hkv"], a["D"], a["scale"], a["split"], None)
+    assert rc < 0 and frag in _lib.lib().q3a_last_error().decode(), _lib.lib().q3a_last_error().decode()
+
+
+def test_paged_decode_append_rope_python_checks():
+    """The torch op validates the norm weights and the cos/sin rows before calling the library."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        q = torch.empty(3, 16, 128, dtype=torch.bfloat16)
+        kc = torch.empty(10, 16, 8, 128, dtype=torch.bfloat16)
+        kv = torch.empty(3, 8, 128, dtype=torch.bfloat16)
+        w = torch.empty(128, dtype=torch.bfloat16)
+        cs = torch.empty(3, 1, 128, dtype=torch.bfloat16)
+        o = torch.ops.q3attn.paged_decode_append_rope(q, kv, kv, w, w, cs, cs, kc, kc, torch.empty(3, dtype=torch.int32),
+                                                      torch.empty(3, 4, dtype=torch.int32), 0.1, 1e-6)
+        assert o.shape == (3, 16, 128) and o.dtype == torch.bfloat16
+    q = torch.zeros(3, 16, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(10, 16, 8, 128, dtype=torch.bfloat16)
+    kv = torch.zeros(3, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):   # CPU tensors are refused before any weight check
+        q3attn.paged_decode_append_rope(q, kv, kv, torch.zeros(128, dtype=torch.bfloat16),
+                                        torch.zeros(128, dtype=torch.bfloat16), torch.zeros(3, 128, dtype=torch.bfloat16),
+                                        torch.zeros(3, 128, dtype=torch.bfloat16), kc, kc,
+                                        torch.zeros(3, dtype=torch.int32), torch.zeros(3, 4, dtype=torch.int32), 0.1)
+
+
 def test_fake_impl_traces_shapes():
     """The custom ops carry fake implementations, so torch.compile / export can trace through them
     without running the kernels."""
