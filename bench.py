@@ -353,8 +353,73 @@ def bench_decode_append(args, dev, wl):
     a = statistics.mean(fr_fused) * 1e3 / LAYERS
     b = statistics.mean(fr_split) * 1e3 / LAYERS
     log(f"[bench] append form: fused {a:.1f} us/layer call; index_copy_ x2 + decode {b:.1f} us/layer call")
-    return {"fused_us_per_layer_call": round(a, 2), "index_copy_then_decode_us_per_layer_call": round(b, 2),
-            "fused_us_per_step": round(a * LAYERS, 1), "index_copy_then_decode_us_per_step": round(b * LAYERS, 1)}
+    rec = {"fused_us_per_layer_call": round(a, 2), "index_copy_then_decode_us_per_layer_call": round(b, 2),
+           "fused_us_per_step": round(a * LAYERS, 1), "index_copy_then_decode_us_per_step": round(b * LAYERS, 1)}
+    rec["norm_rope_form"] = bench_decode_rope(args, dev, wl, steps, old)
+    return rec
+
+
+def bench_decode_rope(args, dev, wl, steps, old):
+    """The talker's whole attention block per layer (engine/talker.py:69-77): q/k RMSNorm + RoPE, the K/V append and
+    the decode, three ways over the same frame: paged_decode_append_rope (one launch); paged_decode_append on q and k
+    normalised beforehand (the attention and append alone, what the producers cost nothing in); and the producers as
+    eager torch ops (engine/ops.py:51-60) followed by paged_decode_append.  The raw rows are the append form's; the
+    slots the frame rewrites are restored afterwards."""
+    import numpy as np
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    rng = np.random.default_rng(3)
+    qn = torch.from_numpy(rng.uniform(0.5, 1.5, 128).astype(np.float32)).to(dev).to(torch.bfloat16)
+    kn = torch.from_numpy(rng.uniform(0.5, 1.5, 128).astype(np.float32)).to(dev).to(torch.bfloat16)
+    cos_t, sin_t = W.rope_tables(int(wl.ctx.max()) + 1, dev)
+    pos = torch.from_numpy(np.maximum(wl.ctx - 1, 0)).to(dev)
+    cos = cos_t[pos].to(torch.bfloat16)[:, None, :]
+    sin = sin_t[pos].to(torch.bfloat16)[:, None, :]
+    kflat = wl.k_cache.view(-1, wl.k_cache.shape[2], wl.k_cache.shape[3])
+    vflat = wl.v_cache.view(-1, wl.v_cache.shape[2], wl.v_cache.shape[3])
+    saved = [(slot, kflat.index_select(0, slot), vflat.index_select(0, slot)) for (_, slot, _, _) in steps]
+
+    def rms(x, w, eps=1e-6):
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+        return w * xf.to(x.dtype)
+
+    def rope(x):
+        h = x.shape[-1] // 2
+        return x * cos + torch.cat((-x[..., h:], x[..., :h]), dim=-1) * sin
+
+    def fused():
+        return [q3attn.paged_decode_append_rope(L.q, k, v, qn, kn, cos, sin, wl.k_cache, wl.v_cache, old,
+                                                L.block_table, wl.scale) for (L, _, k, v) in steps]
+
+    def append_only():
+        return [q3attn.paged_decode_append(L.q, k, v, wl.k_cache, wl.v_cache, old, L.block_table, wl.scale)
+                for (L, _, k, v) in steps]
+
+    def eager_producers():
+        return [q3attn.paged_decode_append(rope(rms(L.q, qn)), rope(rms(k, kn)), v, wl.k_cache, wl.v_cache, old,
+                                           L.block_table, wl.scale) for (L, _, k, v) in steps]
+
+    res = {}
+    for name, fn in (("append_on_normalised", append_only), ("fused", fused), ("torch_producers_then_append",
+                                                                                eager_producers)):
+        # The layers share one pool, so a layer can read a slot another layer rewrites: one untimed frame first
+        # leaves every slot at the value the frame writes, and the replays then see the state the eager frame saw.
+        fn()
+        torch.cuda.synchronize()
+        _, fr, _ = time_graph(dev, fn, args.steps, args.warmup)
+        res[f"{name}_us_per_layer_call"] = round(statistics.mean(fr) * 1e3 / LAYERS, 2)
+    for slot, k, v in saved:
+        kflat.index_copy_(0, slot, k)
+        vflat.index_copy_(0, slot, v)
+    torch.cuda.synchronize()
+    log(f"[bench] norm/rope form: fused {res['fused_us_per_layer_call']:.1f} us/layer call; append on normalised "
+        f"q/k {res['append_on_normalised_us_per_layer_call']:.1f}; torch producers + append "
+        f"{res['torch_producers_then_append_us_per_layer_call']:.1f}")
+    return res
 
 
 def bench_cp(args, dev):

@@ -212,16 +212,14 @@ __device__ __forceinline__ void stage_new_rows(const DecodeArgs& a, int b, int g
   lds_copy4(rv, st + kStageNew + kD * 2, (uint32_t)lane * 4);
 }
 
-// Norm/rope form: the row's RoPE cos and sin rows (256 B each) follow at kStageRope, copied with every tile (out
-// of bounds unless the tile opens a segment or ends its row), so each tile adds the same two operations to vmcnt.
+// Norm/rope form: the row's RoPE cos and sin rows (256 B each) follow at kStageRope, copied with the tiles that
+// open a segment or end their row.
 constexpr int kStageRope = 1024;
 constexpr int kStageBytesRope = 1536;
-constexpr int kWaitGroupRope = 0x0F70 | 11;  // s_waitcnt vmcnt(11): the smallest tile group is 8 + 1 + 2 operations
 
-__device__ __forceinline__ void stage_rope(const DecodeArgs& a, int b, int lane, bool valid, uint8_t* st) {
-  const uint32_t n = valid ? kD * 2 : 0u;
-  lds_copy4(make_rsrc(a.rcos + (int64_t)b * a.rs_sb, n), st + kStageRope, (uint32_t)lane * 4);
-  lds_copy4(make_rsrc(a.rsin + (int64_t)b * a.rs_sb, n), st + kStageRope + kD * 2, (uint32_t)lane * 4);
+__device__ __forceinline__ void stage_rope(const DecodeArgs& a, int b, int lane, uint8_t* st) {
+  lds_copy4(make_rsrc(a.rcos + (int64_t)b * a.rs_sb, kD * 2), st + kStageRope, (uint32_t)lane * 4);
+  lds_copy4(make_rsrc(a.rsin + (int64_t)b * a.rs_sb, kD * 2), st + kStageRope + kD * 2, (uint32_t)lane * 4);
 }
 
 // Append form, the last tile of a row, read after the next tile was issued: as take_new_token, with the new
@@ -638,12 +636,13 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     // array of tile j's parity, which tile j+1's copies do not touch.
     auto process = [&](KVTile& T, int j, const uint8_t* st) {
       const int fl = readlane(vflags, j);
-      if (fl & (kAppend ? (kFirst | kRowEnd) : kFirst)) {
+      if (!kRope && (fl & (kAppend ? (kFirst | kRowEnd) : kFirst))) {
         // The compiler does not order LDS reads after these copies by itself: wait until tile j's group
         // (issued before tile j+1's) has landed.  Tile j+1's group, and the append form's slot stores of
         // the previous tile, are younger; the count is the smallest group (8 loads and the q copy), so
-        // the wait is exact when the younger operations are one such group and conservative otherwise.
-        __builtin_amdgcn_s_waitcnt(kRope ? kWaitGroupRope : kWaitGroup);
+        // the wait is exact when the younger operations are one such group and conservative otherwise.  (The
+        // norm/rope form's prep() has already waited for this stage and rewritten it.)
+        __builtin_amdgcn_s_waitcnt(kWaitGroup);
         __asm__ volatile("" ::: "memory");
       }
       if (fl & kFirst) {
@@ -676,7 +675,9 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       const int row = readlane(vrow, jj);
       auto stage = [&]() {
         stage_q(a, row, g, lane, (fl & kFirst) != 0, st);
-        if constexpr (kRope) stage_rope(a, row, lane, (fl & (kFirst | kRowEnd)) != 0, st);
+        if constexpr (kRope) {
+          if (fl & (kFirst | kRowEnd)) stage_rope(a, row, lane, st);
+        }
         if constexpr (kAppend) {
           if (fl & kRowEnd) stage_new_rows(a, row, g, lane, st);
         }
