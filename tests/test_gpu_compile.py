@@ -21,7 +21,8 @@ import torch.nn.functional as F
 import q3attn
 from helpers import to_np
 from oracle import attention as ora
-from test_gpu_reference_layouts import HD, NKV, NQ, SCALE, Proj, check, rope_bf16
+from synthetic_talker import rms, rope
+from test_gpu_reference_layouts import HD, NH, NK, NKV, NQ, SCALE, Proj, check, rope_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -236,3 +237,62 @@ def test_compiled_code_predictor_post_with_fused_slot_write(cuda_device):
             torch.cuda.synchronize()
             assert torch.equal(static[1], o) and torch.equal(static[0], y)
             assert torch.equal(Ks[l, :B, :, p], k)
+
+
+def test_compiled_decode_rope_form(cuda_device):
+    """engine/talker.py:66-77 with the q/k producers, the scatters and the attention in paged_decode_append_rope: the
+    compiled layer projects, then hands the raw q/k/v views of the projection to the op.  The op writes the caller's
+    pools in place (no pool-sized buffer); the output is within the parity bar of the oracle fed with the reference's
+    own producers (engine/ops.py:51-60 via the test's restatement), the written k rows within the rounding bound of
+    those producers, and a graph captured from the compiled function replays bit for bit."""
+    from torch._inductor.utils import run_and_get_code
+
+    dev = cuda_device
+    torch._dynamo.reset()
+    kc, vc = _pools(dev, 10)
+    kc_before = kc.clone()
+    proj = Proj(dev, 11)
+    cos_t, sin_t = rope_bf16(64 * PAGE, dev)
+    B = 24
+    x, pos, slot, ctx, bt = _frame_inputs(dev, B, 12)
+    cos, sin = cos_t[pos][:, None, :], sin_t[pos][:, None, :]
+
+    def layer(x, cos, sin, ctx, bt):
+        qkv = F.linear(rms(x, proj.ln1), proj.qkv)
+        o = q3attn.paged_decode_append_rope(qkv[:, :NQ].view(B, NH, HD), qkv[:, NQ:NQ + NK].view(B, NKV, HD),
+                                            qkv[:, NQ + NK:].view(B, NKV, HD), proj.qn, proj.kn, cos, sin, kc, vc,
+                                            ctx - 1, bt, SCALE)
+        return o, qkv
+
+    step = torch.compile(layer, dynamic=False)
+    (o, qkv), codes = run_and_get_code(step, x, cos, sin, ctx, bt)
+    torch.cuda.synchronize()
+    assert not _big_allocations(codes, kc.numel() // 4), "the fused op must not be functionalised into a copy"
+    # the reference's producers (engine/ops.py:51-60 as eager torch ops) on the compiled layer's own projection
+    q_ref = rope(rms(qkv[:, :NQ].view(B, NH, HD), proj.qn), cos, sin)
+    k_ref = rope(rms(qkv[:, NQ:NQ + NK].view(B, NKV, HD), proj.kn), cos, sin)
+    v_ref = qkv[:, NQ + NK:].view(B, NKV, HD)
+    assert torch.equal(vc.view(-1, NKV, HD)[slot], v_ref), "v rows must be stored as given"
+    got_k = kc.view(-1, NKV, HD)[slot].float()
+    dk = (got_k - k_ref.float()).abs()
+    assert bool((dk <= k_ref.float().abs() * 2.0 ** -6 + 2.0 ** -6).all()), float(dk.max())
+    untouched = torch.ones(NUM_PAGES * PAGE, dtype=torch.bool, device=dev)
+    untouched[slot] = False
+    assert torch.equal(kc.view(-1, NKV, HD)[untouched], kc_before.view(-1, NKV, HD)[untouched])
+    kc_ref = kc.clone()
+    kc_ref.view(-1, NKV, HD)[slot] = k_ref
+    ref = ora.paged_decode(to_np(q_ref), to_np(kc_ref), to_np(vc), ctx.cpu().numpy(), bt.cpu().numpy(), SCALE)
+    check(o, ref, "compiled norm/rope decode")
+    (o2, _), delta = _peak_delta(lambda: step(x, cos, sin, ctx, bt))
+    print(f"[compile] decode norm/rope: peak allocation {delta / 2**20:.1f} MiB (pool {kc.numel() * 2 / 2**20:.0f} MiB)",
+          flush=True)
+    assert delta < kc.numel() * 2 // 4
+    assert torch.equal(o2, o)
+    pool = kc.clone()
+    g, static = _capture(lambda: step(x, cos, sin, ctx, bt), dev)
+    for _ in range(3):
+        kc.view(-1, NKV, HD)[slot] = float("nan")          # the replay must rewrite the slots
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static[0], o)
+        assert torch.equal(kc, pool)
