@@ -323,13 +323,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx[hh] = fmaxf(mx[hh], st[hh][kb][i]);
     }
-#pragma unroll
-    for (int hh = 0; hh < kG; ++hh) mx[hh] = max_xor16(max_xor32(mx[hh])) * a.scale_log2;
     // Lazy rescale: keep the running max while no token's tile max exceeds it by more than 8 (log2 units), so
     // p = exp2(s * scale - m) <= 256 is exact enough in bf16/fp32 and (l, acc) are rescaled only when a max grows
     // past that margin; one wave vote covers both heads (a head whose max did not grow gets alpha = 1 or a
-    // smaller exact shift).  The first tile always sets the max.
-    if (__any(mx[0] > m[0] + 8.f || mx[1] > m[1] + 8.f)) {
+    // smaller exact shift).  The first tile always sets the max.  The vote tests each lane's own maximum (a token's
+    // tile max exceeds the margin iff one of its 4 lanes' does), so the cross-lane reduction runs only when a max
+    // grows.
+    if (__any(mx[0] * a.scale_log2 > m[0] + 8.f || mx[1] * a.scale_log2 > m[1] + 8.f)) {
+#pragma unroll
+      for (int hh = 0; hh < kG; ++hh) mx[hh] = max_xor16(max_xor32(mx[hh])) * a.scale_log2;
 #pragma unroll
       for (int hh = 0; hh < kG; ++hh) {
         const float mn = fmaxf(m[hh], mx[hh]);
