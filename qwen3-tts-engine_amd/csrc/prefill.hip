@@ -435,20 +435,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
   }
 
-  // The 4 lanes of a token hold partial sums over disjoint keys.
+  // The 4 lanes of a token hold partial sums over disjoint keys.  The output goes out through LDS as whole 256 B
+  // head rows (16 B per lane): written straight from the accumulator layout each lane would store 8 B pieces, 32 B
+  // of a token row per 4 lanes, which the L2 has to merge.  Each wave stages its 16 tokens x 2 heads (8 KiB) in one
+  // of the tile arrays, free once every wave has passed the loop's last barrier (the pool stores above still read
+  // them, hence the barrier in that form).  16 B chunks are XOR-swizzled by token, so neither side conflicts.
+  if (pool_from_lds) __syncthreads();
+  uint8_t* const so = wave == 0 ? sK0 : (wave == 1 ? sV0 : (wave == 2 ? sK1 : sV1));
 #pragma unroll
   for (int hh = 0; hh < kG; ++hh) {
     const float lt = sum_xor32(sum_xor16(l[hh]));
-    if (qvalid) {
-      const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      uint16_t* o = a.out + obase + (int64_t)tq * a.o_st + (kG * g + hh) * a.o_sh + 4 * g4;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        uint2 w;
-        w.x = pack_bf16x2(acc[hh][db][0] * inv, acc[hh][db][1] * inv);
-        w.y = pack_bf16x2(acc[hh][db][2] * inv, acc[hh][db][3] * inv);
-        *reinterpret_cast<uint2*>(o + db * 16) = w;
-      }
+    for (int db = 0; db < 8; ++db) {
+      uint2 w;
+      w.x = pack_bf16x2(acc[hh][db][0] * inv, acc[hh][db][1] * inv);
+      w.y = pack_bf16x2(acc[hh][db][2] * inv, acc[hh][db][3] * inv);
+      const int chunk = 2 * db + (g4 >> 1);
+      *reinterpret_cast<uint2*>(so + hh * 16 * kRowB + col * kRowB + ((chunk ^ col) << 4) + (g4 & 1) * 8) = w;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < 4 * kG; ++it) {
+    const int hh = it >> 2;
+    const int t = 4 * (it & 3) + (lane >> 4);      // token of the wave's 16
+    const int c = lane & 15;                       // 16 B chunk of its 256 B row
+    const int token = qt * kQT + wave * 16 + t;
+    if (token < Lq) {
+      const uint4 x = ld16(so + hh * 16 * kRowB + t * kRowB + ((c ^ t) << 4));
+      st16(a.out + obase + (int64_t)token * a.o_st + (kG * g + hh) * a.o_sh + 8 * c, x);
     }
   }
 }
