@@ -9,10 +9,10 @@
 // (the K.index_copy_ / V.index_copy_ of engine/code_predictor.py:58) by the same wave that attends,
 // which uses the new rows straight from registers.
 //
-// One wave per (row, KV head).  Scores: lane l takes slot l/4 and a quarter of the head
-// dimension (4 x 16 B loads; the 4 lanes of a slot read 64 contiguous bytes per instruction) and
-// reduces with two quad DPP steps; q is loaded once per wave and handed to those lanes with
-// ds_bpermute.  P.V: lane l owns output dims 2l, 2l+1 of both query heads and walks the slots up to
+// One wave per (row, KV head).  Scores: lane l takes slots l/8 and 8 + l/8 and an eighth of the head
+// dimension of each (4 x 16 B loads; the 8 lanes of a slot pair read 128 contiguous bytes, a whole
+// cache line, per instruction) and reduces with three DPP steps; q is loaded once per wave and handed
+// to those lanes with ds_bpermute.  P.V: lane l owns output dims 2l, 2l+1 of both query heads and walks the slots up to
 // n_live rounded up to a multiple of 4 (one instantiation per multiple); each slot is one 256 B
 // coalesced load and the slot's probability is broadcast with v_readlane.  All loads of the wave are issued before the first use, without branches: the
 // scratch rows go through a buffer descriptor whose extent ends at the last row read, so the loads
@@ -61,18 +61,16 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   const int b = __builtin_amdgcn_readfirstlane(wave / a.hkv);
   const int g = __builtin_amdgcn_readfirstlane(wave - b * a.hkv);
   const int lane = threadIdx.x & 63;
-  const int slot = lane >> 2;
-  const int c = lane & 3;
-  const bool live = slot < a.n_live;
+  // Lane (s8, c) = (lane >> 3, lane & 7) holds slots s8 and 8 + s8, dims 8c..8c+7 and 64+8c..64+8c+7 of each, so
+  // every K load instruction reads 8 slots x 128 contiguous bytes: whole 128 B lines.
+  const int s8 = lane >> 3;
+  const int c = lane & 7;
+  const bool liveA = s8 < a.n_live;
+  const bool liveB = 8 + s8 < a.n_live;
 
   uint16_t* kb = a.k + (int64_t)b * a.k_sb + (int64_t)g * a.k_sh;
   uint16_t* vb = a.v + (int64_t)b * a.v_sb + (int64_t)g * a.v_sh;
   const uint16_t* qb = a.q + (int64_t)b * a.q_sb + (int64_t)(kG * g) * kD;
-  // The scratch rows read are 0..n_read-1: all live slots, or in the append form all but the last, which
-  // comes from this step's k/v rows (and is stored into the scratch here; it is never read back from the
-  // scratch, so the write and the reads of this wave cannot race).  Every load is unconditional: rows past
-  // n_read fail the descriptor's bounds and read as zeros without touching memory, so slots >= n_live are
-  // never read and no branch or early wait sits between the loads.
   const int last = a.n_live - 1;
   const int n_read = kAppend ? last : a.n_live;
   const uint32_t krow_b = (uint32_t)a.k_ss * 2;
@@ -80,17 +78,13 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, n_read > 0 ? (uint32_t)(n_read - 1) * krow_b + kD * 2 : 0u);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, n_read > 0 ? (uint32_t)(n_read - 1) * vrow_b + kD * 2 : 0u);
 
-  // Lane (slot, c) holds dims 32*i + 8*c .. +8 for i = 0..3, of K[slot] and of both query heads.  q (and in
-  // the append form the new k row) is loaded once, one 16 B chunk per lane, and handed to the lanes that need
-  // it with ds_bpermute: loading it per lane would return the same 512 B sixteen times over (8 KiB per wave,
-  // the largest share of the kernel's vector-memory data return).
-  uint4 kr[4], qr[kG][4];
+  uint4 kr[4], qr[kG][2];
   uint32_t vr[kNV], vn = 0u;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(qb, kG * kD * 2);
   const uint4 qc = buffer_load16(rq, lane < kG * 16 ? (uint32_t)lane * 16 : kOutOfRange);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) kr[i] = buffer_load16(rk, (uint32_t)slot * krow_b + (32 * i + 8 * c) * 2);
-  // Append form: lanes 0..15 hold this step's k row, lane l its dims 8l..8l+7.
+  for (int j = 0; j < 4; ++j)
+    kr[j] = buffer_load16(rk, (uint32_t)(s8 + 8 * (j >> 1)) * krow_b + (uint32_t)(8 * c + 64 * (j & 1)) * 2);
   const __amdgpu_buffer_rsrc_t rkn =
       kAppend ? make_rsrc(a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD, kD * 2) : rk;
   const __amdgpu_buffer_rsrc_t rvn =
@@ -101,50 +95,65 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   for (int s = 0; s < kNV; ++s)
     vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, (int)((uint32_t)s * vrow_b), 0);
   if constexpr (kAppend) vn = __builtin_amdgcn_raw_buffer_load_b32(rvn, lane * 4, 0, 0);
-  // Every load is in flight before any is waited for.
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int h = 0; h < kG; ++h)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qr[h][i] = bpermute16(qc, 16 * h + 4 * i + c);
+  for (int h = 0; h < kG; ++h) {
+    qr[h][0] = bpermute16(qc, 16 * h + c);
+    qr[h][1] = bpermute16(qc, 16 * h + 8 + c);
+  }
   if constexpr (kAppend) {
-    // Slot `last` takes the new k/v rows (its scratch row was not read: out of the descriptor's bounds).
-    const bool mine = slot == last;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 kn = bpermute16(knc, 4 * i + c);
-      if (mine) kr[i] = kn;
+    const uint4 kn0 = bpermute16(knc, c), kn1 = bpermute16(knc, 8 + c);
+    if (s8 == last) {
+      kr[0] = kn0;
+      kr[1] = kn1;
+    }
+    if (8 + s8 == last) {
+      kr[2] = kn0;
+      kr[3] = kn1;
     }
 #pragma unroll
     for (int s = 0; s < kNV; ++s)
       if (s == last) vr[s] = vn;
-    // Slot `last` of the scratch, written with vector buffer stores (lanes 16..63 of the k store are out of
-    // bounds).
     const __amdgpu_buffer_rsrc_t wk = make_rsrc(kb + (int64_t)last * a.k_ss, kD * 2);
     const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.v_ss, kD * 2);
     buffer_store16_s(knc, wk, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange, 0u);
     __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, 0);
   }
 
-  float p[kG];
+  auto dot16 = [](const uint4& q0, const uint4& k0, const uint4& q1, const uint4& k1) {
+    float x = dot2_bf16(q0.x, k0.x, 0.f);
+    x = dot2_bf16(q0.y, k0.y, x);
+    x = dot2_bf16(q0.z, k0.z, x);
+    x = dot2_bf16(q0.w, k0.w, x);
+    x = dot2_bf16(q1.x, k1.x, x);
+    x = dot2_bf16(q1.y, k1.y, x);
+    x = dot2_bf16(q1.z, k1.z, x);
+    return dot2_bf16(q1.w, k1.w, x);
+  };
+  float pa[kG], pb[kG];
 #pragma unroll
   for (int h = 0; h < kG; ++h) {
-    float x = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x = dot2_bf16(qr[h][i].x, kr[i].x, x);
-      x = dot2_bf16(qr[h][i].y, kr[i].y, x);
-      x = dot2_bf16(qr[h][i].z, kr[i].z, x);
-      x = dot2_bf16(qr[h][i].w, kr[i].w, x);
-    }
-    x = quad_sum(x);
-    x = live ? x * a.scale_log2 : -INFINITY;
-    // Max and sum over the 16 slots: quad-uniform values, 4 quads per row, 4 rows per wave.
-    const float mx = max_xor32(max_xor16(quads_max(x)));
-    const float e = fast_exp2(x - mx);
-    const float z = sum_xor32(sum_xor16(quads_sum(e)));
-    // z >= 1 (the max slot contributes exp2(0)), so the reciprocal is well conditioned.
-    p[h] = round_bf16(e * __builtin_amdgcn_rcpf(z));
+    float xa = dot16(qr[h][0], kr[0], qr[h][1], kr[1]);
+    float xb = dot16(qr[h][0], kr[2], qr[h][1], kr[3]);
+    // sum over the 8 lanes of a slot pair (xor 1, xor 2, then the quads' halves)
+    xa = quad_sum(xa);
+    xa += dpp_f32<kDppHalfMirror>(xa);
+    xb = quad_sum(xb);
+    xb += dpp_f32<kDppHalfMirror>(xb);
+    xa = liveA ? xa * a.scale_log2 : -INFINITY;
+    xb = liveB ? xb * a.scale_log2 : -INFINITY;
+    // max and sum over the 16 slots: 8-lane-uniform values, 8 groups per wave
+    float mx = fmaxf(xa, xb);
+    mx = fmaxf(mx, dpp_f32<kDppRor8>(mx));
+    mx = max_xor32(max_xor16(mx));
+    const float ea = fast_exp2(xa - mx);
+    const float eb = fast_exp2(xb - mx);
+    float z = ea + eb;
+    z += dpp_f32<kDppRor8>(z);
+    z = sum_xor32(sum_xor16(z));
+    const float r = __builtin_amdgcn_rcpf(z);
+    pa[h] = round_bf16(ea * r);
+    pb[h] = round_bf16(eb * r);
   }
 
   float o[kG][2];
@@ -156,8 +165,9 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
     const float hi = bf16_hi(vr[s]);
 #pragma unroll
     for (int h = 0; h < kG; ++h) {
+      const float src = s < 8 ? pa[h] : pb[h];
       const float ps = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[h]), 4 * s));
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src), 8 * (s & 7)));
       o[h][0] = fmaf(ps, lo, o[h][0]);
       o[h][1] = fmaf(ps, hi, o[h][1]);
     }
