@@ -234,3 +234,44 @@ def test_varlen_many_sequences(cuda_device, hkv, causal):
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(static, out)
+
+
+@pytest.mark.parametrize("case", ["64 seqs", "ties", "one long", "grouped", "grouped, max_seqlen above longest"])
+def test_varlen_work_orders(cuda_device, case):
+    """Both work orders of the tiled kernel: all sequences' query tiles longest first (grids of up to about three
+    rounds of resident workgroups), and groups of sequences one after another (larger grids: 45 sequences of up
+    to 500 tokens, a partial last group, zero-length sequences, and a max_seqlen_q above every length so that
+    whole query-tile rows are empty).  Equal lengths and one long sequence among short ones.  Within the bar of
+    the oracle."""
+    rng = np.random.default_rng(len(case))
+    lens = {"64 seqs": rng.integers(0, 200, 64),
+            "ties": np.array([128, 64, 128, 1, 128, 64, 0, 65] * 3),
+            "one long": np.array([5, 17, 700, 3, 64, 1]),
+            "grouped": rng.integers(0, 500, 45),
+            "grouped, max_seqlen above longest": rng.integers(1, 300, 45)}[case]
+    lens[0] = max(lens[0], 1)
+    hkv = 8
+    T = int(lens.sum())
+    g = torch.Generator(device=cuda_device).manual_seed(len(case))
+    q = torch.randn(T, 2 * hkv, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    k = torch.randn(T, hkv, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    v = torch.randn(T, hkv, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=cuda_device)
+    max_q = int(lens.max()) + (200 if "above" in case else 0)
+    out = q3attn.flash_attn_varlen_func(q, k, v, cu, cu, max_q, max_q, softmax_scale=128 ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    ref = ora.prefill_varlen(to_np(q), to_np(k), to_np(v), cu.cpu().numpy(), 128 ** -0.5)
+    check(out, ref, f"work order: {case}")
+
+
+@pytest.mark.parametrize("S,L", [(5, 300), (40, 640)])
+def test_dense_work_order(cuda_device, S, L):
+    """The dense form with key ranges past the short-range kernel, in both work orders (40 x 640 runs in groups of
+    4 sequences), against the oracle."""
+    g = torch.Generator(device=cuda_device).manual_seed(S * 100 + L)
+    q = torch.randn(S, L, 16, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    K = torch.randn(S, L, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    V = torch.randn(S, L, 8, 128, generator=g, device=cuda_device).to(torch.bfloat16)
+    out = q3attn.flash_attn_func(q, K, V, softmax_scale=128 ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    check(out, ora.prefill_prefix(to_np(q), to_np(K), to_np(V), 128 ** -0.5), f"dense S={S} L={L}")
