@@ -63,8 +63,12 @@ def _run_both(dev, q, k, v, cu_q, cu_k, max_q, bt_np, page, num_pages, scale, ca
     ([1, 7, 16, 17, 33, 64, 65, 150, 3], 16, False),
     ([77, 300, 5], 256, True),                 # the reference's own pool: 256-token pages, identity seats
     (None, 16, False),                         # the 32-sequence prefill workload (U[150, 400] tokens)
+    ("grouped", 16, False),                    # 48 sequences of up to 500 tokens: the grouped work order
 ])
 def test_prefill_append_matches_scatter_then_prefill(cuda_device, lens, page, identity):
+    if lens == "grouped":
+        lens = np.random.default_rng(13).integers(1, 500, 48)
+        lens[0] = 499
     lens = W.prefill_lengths("prefill32") if lens is None else np.array(lens)
     wl = W.make_prefill(cuda_device, lens, seed=11, paged=False)
     cu = wl.cu_seqlens.cpu().numpy()
