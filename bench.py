@@ -647,6 +647,7 @@ def bench_admit(args, dev):
     call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
     tflops = w0.flops() / (call_us * 1e-6) / 1e12
     log(f"[bench] admission prefill S={S} R={R} n={n}: {call_us:.2f} us/call, {tflops:.1f} TFLOP/s")
+    admission_step = None if args.no_append else bench_admit_append(args, dev, wls)
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.torch_cpu import prefill_prefix_rows
@@ -671,7 +672,55 @@ def bench_admit(args, dev):
                              "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
                              "flops_per_call": w0.flops()},
                 "cpu_baseline": cpu})
+    if admission_step is not None:
+        rec["admission_step"] = admission_step
     return rec
+
+
+def bench_admit_append(args, dev, wls):
+    """Extra information beside the admission line: the admission layer step as the engine runs it (two index_copy_
+    scatters of every K and V row into the seat's cache positions, engine/arrivals.py:144-145, then flash_attn_func
+    on the dense K/V, :148) against prefill_dense_append, which writes the pool inside the attention launch.  Each
+    layer has its own 256-page pool (16-token pages) and random table; every replay rewrites identical values."""
+    import numpy as np
+    import torch
+
+    import q3attn
+
+    S, n = wls[0].k.shape[0], wls[0].k.shape[1]
+    P, page, num_pages = -(-n // 16), 16, 256
+    steps = []
+    for l, wl in enumerate(wls):
+        bt = np.random.default_rng(1000 + l).permutation(num_pages)[: S * P].reshape(S, P).astype(np.int32)
+        flat = np.concatenate([bt[s_, np.arange(n) // page] * page + np.arange(n) % page for s_ in range(S)])
+        kc = torch.zeros(num_pages, page, 8, 128, dtype=torch.bfloat16, device=dev)
+        steps.append((wl, kc, torch.zeros_like(kc), torch.from_numpy(bt).to(dev), torch.from_numpy(flat).to(dev)))
+
+    def dense():
+        return [q3attn.flash_attn_func(wl.q, wl.k, wl.v, softmax_scale=wl.scale, causal=True)
+                for wl, _, _, _, _ in steps]
+
+    def scatter_then_prefill():
+        out = []
+        for wl, kc, vc, _, flat in steps:
+            kc.view(-1, 8, 128).index_copy_(0, flat, wl.k.reshape(-1, 8, 128))
+            vc.view(-1, 8, 128).index_copy_(0, flat, wl.v.reshape(-1, 8, 128))
+            out.append(q3attn.flash_attn_func(wl.q, wl.k, wl.v, softmax_scale=wl.scale, causal=True))
+        return out
+
+    def fused():
+        return [q3attn.prefill_dense_append(wl.q, wl.k, wl.v, kc, vc, bt, wl.scale, True, 0)
+                for wl, kc, vc, bt, _ in steps]
+
+    res = {}
+    for name, fn in (("flash_attn_func", dense), ("index_copy_then_prefill", scatter_then_prefill),
+                     ("prefill_dense_append", fused)):
+        _, fr, _ = time_graph(dev, fn, args.steps, args.warmup, getattr(args, "min_warm_s", 0.0))
+        res[name + "_us_per_layer_call"] = round(statistics.mean(fr) * 1e3 / LAYERS, 2)
+    log(f"[bench] admission step: prefill_dense_append {res['prefill_dense_append_us_per_layer_call']:.2f} us/layer "
+        f"call; index_copy_ x2 + prefill {res['index_copy_then_prefill_us_per_layer_call']:.2f}; prefill alone "
+        f"{res['flash_attn_func_us_per_layer_call']:.2f}")
+    return res
 
 
 def other_workloads(args, dev):
@@ -690,17 +739,17 @@ def other_workloads(args, dev):
     dec = copy.copy(lite)
     dec.no_cpu_baseline = args.no_cpu_baseline
     pre = copy.copy(lite)
-    pre.no_append = False                 # the prompt-step comparison (fused pool write) is part of this line
+    pre.no_append = False                 # the prompt/admission-step comparisons (fused pool writes) are part of these
     out = {}
     for name, fn in (("decode256", lambda: bench_decode(dec, dev, "decode256", cpu_budget_s=6.0)),
                      ("decode1x64", lambda: bench_decode(dec, dev, "decode1x64", cpu_budget_s=2.0)),
                      ("cp512", lambda: bench_cp(lite, dev)),
-                     ("prefill32", lambda: bench_prefill(pre, dev)), ("admission_prefill", lambda: bench_admit(lite, dev))):
+                     ("prefill32", lambda: bench_prefill(pre, dev)), ("admission_prefill", lambda: bench_admit(pre, dev))):
         try:
             r = fn()
             keep = {k: r[k] for k in ("us_per_layer_call", "us_per_call", "hbm_gbps", "pct_hbm_peak", "tflops",
                                       "three_launch_us_per_step", "cold_us_per_call", "launch_floor_us_per_call",
-                                      "prompt_step") if k in r}
+                                      "prompt_step", "admission_step") if k in r}
             keep["us_per_step"] = r["value"]
             keep["roofline_frac"] = r["roofline"]["frac"]
             keep["roofline_unit"] = r["roofline"]["unit"]

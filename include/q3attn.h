@@ -26,8 +26,9 @@ extern "C" {
 #define Q3A_ESPACE (-28)  /* workspace smaller than q3a_paged_decode_workspace_bytes() */
 
 /* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
- * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope. */
-#define Q3A_ABI_VERSION 4
+ * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope.
+ * 5: q3a_prefill_dense_append. */
+#define Q3A_ABI_VERSION 5
 int q3a_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -258,6 +259,30 @@ int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int
                       void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs,
                       int seqlen_q, int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
                       float softmax_scale, int causal, void* stream);
+
+/*
+ * Fast-admission prefill with the sequences' K/V written into the page pool in the same launch.
+ *
+ * Replaces the two index_copy_ scatters of engine/arrivals.py:144-145 (every row of K = cat(prefix, new) and of V
+ * into the seat's cache positions 0 .. n-1) together with the attention at engine/arrivals.py:148.  The attention is
+ * q3a_prefill_dense's on the dense k/v (same arguments and result, bit for bit); in addition, rows first_row ..
+ * seqlen_k - 1 of sequence s's K and V (key j at k + s * k_stride_s + j * k_stride_t) are stored into
+ * k_cache/v_cache [num_pages, page_size, Hkv, D] (strides kv_stride_page/tok/head, shared by the two pools) at page
+ * block_table[s][j / page_size], offset j % page_size.  first_row = 0 writes every row (the engine's call);
+ * seqlen_k - seqlen_q writes the new tokens' rows only (a prefix already in the pool).  0 <= first_row <=
+ * max(0, seqlen_k - seqlen_q).  Positions past max_pages_per_seq pages and page ids outside [0, num_pages) are not
+ * written.  With num_seqs == 0 or seqlen_q == 0 nothing is computed or written.  Pool requirements as in
+ * q3a_prefill_append; the pool rows this call writes must not alias the k/v it reads.
+ */
+int q3a_prefill_dense_append(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
+                             const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
+                             const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
+                             void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                             int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                             int64_t bt_stride_b, int max_pages_per_seq, int first_row, void* out,
+                             int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int seqlen_q,
+                             int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                             int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -65,14 +65,17 @@ struct PrefillArgs {
   int causal;
   int hkv;
   float scale_log2;
-  // Append form (q3a_prefill_append): each query token's K and V rows of its KV head are also written into a page
-  // pool at the token's position in its sequence.  pk == nullptr: no write.
+  // Append forms (q3a_prefill_append, q3a_prefill_dense_append): each query token's K and V rows of its KV head are
+  // also written into a page pool at the token's position in its sequence.  pk == nullptr: no write.  p_first >= 0
+  // (dense form): the prefix rows p_first .. Lk - Lq - 1 are written as well (by the first query tile's workgroup,
+  // or, in the short-key kernel, with every other row from the LDS copy); -1: the query tokens' rows only.
   uint16_t* pk;
   uint16_t* pv;
   int64_t p_sp, p_st, p_sh;
   const int32_t* pbt;
   int64_t pbt_sb;
   int p_pages, p_shift, p_max_pages;
+  int p_first;
   // Grouped order (prefill_kernel<true>): sequences in groups of 2^grp_shift, nqt query tiles per sequence.
   int nseq;
   int nqt;
@@ -158,21 +161,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // Element offsets of the sequence's first query/output row and first packed key row.
   int Lq, Lk;
   int64_t qbase, obase, kbase;  // kbase: the first key row of the operand this wave copies
-  int k0 = 0;
+  int64_t krow0, vrow0;         // the first K and V rows (append form)
   if (a.cu_q != nullptr) {
     const int q0 = a.cu_q[s];
-    k0 = a.cu_k[s];
+    const int k0 = a.cu_k[s];
     Lq = a.cu_q[s + 1] - q0;
     Lk = a.cu_k[s + 1] - k0;
     qbase = (int64_t)q0 * a.q_st;
     obase = (int64_t)q0 * a.o_st;
     kbase = (int64_t)k0 * c_st;
+    krow0 = (int64_t)k0 * a.k_st;
+    vrow0 = (int64_t)k0 * a.v_st;
   } else {
     Lq = a.dense_lq;
     Lk = a.dense_lk;
     qbase = (int64_t)s * a.q_ss;
     obase = (int64_t)s * a.o_ss;
     kbase = (int64_t)s * (copies_k ? a.k_ss : a.v_ss);
+    krow0 = (int64_t)s * a.k_ss;
+    vrow0 = (int64_t)s * a.v_ss;
   }
   if (qt * kQT >= Lq) return;
   if (a.bt != nullptr) Lk = min(Lk, a.max_pages * a.page_size);
@@ -194,42 +201,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
   }
 
-  // Append form: the K and V rows of this workgroup's query tokens (positions Lk - Lq + token of the packed
-  // sequence) for KV head g go into the pool.  Below, in general, they are loaded here so they share the prologue's
-  // round trip and stored into the pool after it (lane (r = lane >> 4, c = lane & 15) moves dims 8c..8c+7 of token
-  // 16 wave + 4i + r of the query tile).
+  // Append forms: K and V rows of KV head g go into the pool.  Packed (q3a_prefill_append): the rows of this
+  // workgroup's query tokens (positions Lk - Lq + token).  Dense (q3a_prefill_dense_append, p_first >= 0): rows
+  // p_first .. Lk - 1 in chunks of 64, chunk c taken by the sequence's query tile c mod nqt, so the prefix rows that
+  // no query token owns are spread over the sequence's workgroups too.  In general the rows are loaded here, so they
+  // share the prologue's round trip, and stored into the pool after it (lane (r = lane >> 4, c = lane & 15) moves
+  // dims 8c..8c+7 of row base + 16 wave + 4i + r); a dense workgroup's further chunks follow the prologue.
   uint4 wk[4], wv[4];
   int64_t wdst[4];
+  const bool chunked = a.pk != nullptr && a.p_first >= 0;
+  const int nqt_seq = kGrouped ? a.nqt : (int)gridDim.z;
   // With causal masking and a K/V prefix that is a whole number of 32-key tiles (a prompt has none), the query
   // tokens' rows are the last one or two key tiles the workgroup streams; they are stored from LDS after the loop,
   // and the prologue only fetches the table entries of those positions (lane i: page kown0 / page_size + i).
-  const bool pool_from_lds = a.pk != nullptr && a.causal && Lk >= Lq && ((Lk - Lq) & (kKT - 1)) == 0;
+  const bool pool_from_lds = a.pk != nullptr && !chunked && a.causal && Lk >= Lq && ((Lk - Lq) & (kKT - 1)) == 0;
   const int kown0 = Lk - Lq + qt * kQT;
   int pwo = -1;
   if (pool_from_lds) {
     const int pi = (kown0 >> a.p_shift) + lane;
     if (lane < 8 && pi < a.p_max_pages) pwo = a.pbt[(int64_t)s * a.pbt_sb + pi];
   }
-  if (a.pk != nullptr && !pool_from_lds) {
+  auto load_rows = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       wk[i] = make_uint4(0u, 0u, 0u, 0u);
       wv[i] = wk[i];
       wdst[i] = -1;
-      const int t = qt * kQT + wave * 16 + 4 * i + (lane >> 4);
-      const int pos = Lk - Lq + t;
+      const int pos = base + wave * 16 + 4 * i + (lane >> 4);
       const int pi = pos >> a.p_shift;
-      if (t < Lq && pos >= 0 && pi < a.p_max_pages) {
+      if (pos >= 0 && pos < Lk && pi < a.p_max_pages) {
         const int page = a.pbt[(int64_t)s * a.pbt_sb + pi];
-        const int64_t row = (int64_t)(k0 + pos);
-        wk[i] = ld16(a.k + row * a.k_st + (int64_t)g * a.k_sh + 8 * (lane & 15));
-        wv[i] = ld16(a.v + row * a.v_st + (int64_t)g * a.v_sh + 8 * (lane & 15));
+        wk[i] = ld16(a.k + krow0 + (int64_t)pos * a.k_st + (int64_t)g * a.k_sh + 8 * (lane & 15));
+        wv[i] = ld16(a.v + vrow0 + (int64_t)pos * a.v_st + (int64_t)g * a.v_sh + 8 * (lane & 15));
         if ((unsigned)page < (unsigned)a.p_pages)
           wdst[i] = (int64_t)page * a.p_sp + (int64_t)(pos & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)g * a.p_sh +
                     8 * (lane & 15);
       }
     }
-  }
+  };
+  auto store_rows = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (wdst[i] >= 0) {
+        st16(a.pk + wdst[i], wk[i]);
+        st16(a.pv + wdst[i], wv[i]);
+      }
+    }
+  };
+  if (a.pk != nullptr && !pool_from_lds) load_rows(chunked ? a.p_first + qt * kQT : kown0);
 
   int kend = Lk;
   if (a.causal) {
@@ -411,11 +430,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   wait_vmem();
   __syncthreads();
   if (a.pk != nullptr && !pool_from_lds) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (wdst[i] >= 0) {
-        st16(a.pk + wdst[i], wk[i]);
-        st16(a.pv + wdst[i], wv[i]);
+    store_rows();
+    if (chunked) {
+      for (int c = qt + nqt_seq; a.p_first + c * kQT < Lk; c += nqt_seq) {
+        load_rows(a.p_first + c * kQT);
+        store_rows();
       }
     }
   }
@@ -523,6 +542,13 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
   const int Lk = a.dense_lk;
   const int64_t qbase = (int64_t)s * a.q_ss, obase = (int64_t)s * a.o_ss;
 
+  // Append form: rows p_first .. Lk - 1 of this KV head go into the pool from the LDS copy, K by the workgroup of
+  // query head 0 and V by that of query head 1 (first query block only).  Lane i holds table entry i (Lk <= 128
+  // keys span at most 8 pages of >= 16); it is loaded beside the copies, so it adds no round trip.
+  const bool app = a.pk != nullptr && (blockIdx.z >> 1) == 0;
+  int pwo = -1;
+  if (app && lane < min(kResMaxTiles * kKT / 16, a.p_max_pages)) pwo = a.pbt[(int64_t)s * a.pbt_sb + lane];
+
   // Copies: the 16-key groups of K and V (2 per tile and operand) are dealt round-robin to the waves; four
   // direct-to-LDS loads each, same layout and swizzle as the tiled kernel.
   const int ngroups = 4 * ntiles;
@@ -556,6 +582,24 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
   }
   wait_vmem();
   __syncthreads();
+  if (app) {
+    // LDS slot c of key row r holds global chunk c ^ (r & 15) (the copy's swizzle).  The loop bound is uniform
+    // across the workgroup so that every lane takes part in the table shuffle.
+    const uint8_t* src = hh == 0 ? sK : sV;
+    uint16_t* const dst = hh == 0 ? a.pk : a.pv;
+    const int nch = (Lk - a.p_first) * 16;
+    for (int c0 = 0; c0 < nch; c0 += (int)blockDim.x) {
+      const int idx = c0 + tid;
+      const int r = a.p_first + (idx >> 4);
+      const int ch = idx & 15;
+      const int pi = r >> a.p_shift;
+      const int page = __shfl(pwo, min(pi, 63));
+      if (idx < nch && pi < a.p_max_pages && (unsigned)page < (unsigned)a.p_pages)
+        st16(dst + (int64_t)page * a.p_sp + (int64_t)(r & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)g * a.p_sh +
+                 8 * ch,
+             ld16(src + r * kRowB + ((ch ^ (r & 15)) << 4)));
+    }
+  }
   if (tg * kResQ >= Lq) return;                 // a wave with no query token (after the barrier: it copied)
 
   const int jlim = a.causal ? min(Lk - 1, Lk - Lq + tq) : Lk - 1;
@@ -724,6 +768,41 @@ static int launch(const PrefillArgs& args, int num_seqs, int max_seqlen_q, void*
   return Q3A_OK;
 }
 
+// Pool-side checks shared by the append entry points.
+static int check_pool(const void* k_cache, const void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                      int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                      int max_pages_per_seq, int head_dim, const char* who) {
+  if (!k_cache || !v_cache || !block_table) return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  if (page_size < 16 || (page_size & (page_size - 1)) != 0)
+    return fail(Q3A_EINVAL, "%s: page_size %d must be a power of two >= 16", who, page_size);
+  if (num_pages <= 0 || max_pages_per_seq <= 0)
+    return fail(Q3A_EINVAL, "%s: num_pages and max_pages_per_seq must be > 0", who);
+  if (((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 != 0)
+    return fail(Q3A_EINVAL, "%s: k_cache/v_cache must be 16-byte aligned", who);
+  if ((kv_stride_page | kv_stride_tok | kv_stride_head) % 8 != 0 || kv_stride_tok < head_dim || kv_stride_head < 0 ||
+      kv_stride_page < (int64_t)page_size * kv_stride_tok)
+    return fail(Q3A_EINVAL, "%s: cache strides (page %lld, token %lld, head %lld) unsupported", who,
+                (long long)kv_stride_page, (long long)kv_stride_tok, (long long)kv_stride_head);
+  return Q3A_OK;
+}
+
+static void set_pool(PrefillArgs& a, void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                     int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                     int64_t bt_stride_b, int max_pages_per_seq, int first_row) {
+  a.pk = static_cast<uint16_t*>(k_cache);
+  a.pv = static_cast<uint16_t*>(v_cache);
+  a.p_sp = kv_stride_page;
+  a.p_st = kv_stride_tok;
+  a.p_sh = kv_stride_head;
+  a.pbt = block_table;
+  a.pbt_sb = bt_stride_b;
+  a.p_pages = num_pages;
+  a.p_shift = 0;
+  while ((1 << a.p_shift) < page_size) ++a.p_shift;
+  a.p_max_pages = max_pages_per_seq;
+  a.p_first = first_row;
+}
+
 extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
                            const void* k, int64_t k_stride_page, int64_t k_stride_tok, int64_t k_stride_head,
                            const void* v, int64_t v_stride_page, int64_t v_stride_tok, int64_t v_stride_head,
@@ -787,21 +866,13 @@ extern "C" int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_s
   const char* who = "prefill_append";
   if (num_seqs < 0 || max_seqlen_q < 0) return fail(Q3A_EINVAL, "%s: negative num_seqs/max_seqlen_q", who);
   if (num_seqs == 0 || max_seqlen_q == 0) return Q3A_OK;
-  if (!cu_seqlens_q || !cu_seqlens_k || !k_cache || !v_cache || !block_table)
-    return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  if (!cu_seqlens_q || !cu_seqlens_k) return fail(Q3A_EINVAL, "%s: null pointer argument", who);
   int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, k_stride_tok, k_stride_head, v_stride_tok,
                         v_stride_head, o_stride_t, o_stride_h, num_q_heads, num_kv_heads, head_dim, who);
   if (rc != Q3A_OK) return rc;
-  if (page_size < 16 || (page_size & (page_size - 1)) != 0)
-    return fail(Q3A_EINVAL, "%s: page_size %d must be a power of two >= 16", who, page_size);
-  if (num_pages <= 0 || max_pages_per_seq <= 0)
-    return fail(Q3A_EINVAL, "%s: num_pages and max_pages_per_seq must be > 0", who);
-  if (((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 != 0)
-    return fail(Q3A_EINVAL, "%s: k_cache/v_cache must be 16-byte aligned", who);
-  if ((kv_stride_page | kv_stride_tok | kv_stride_head) % 8 != 0 || kv_stride_tok < head_dim || kv_stride_head < 0 ||
-      kv_stride_page < (int64_t)page_size * kv_stride_tok)
-    return fail(Q3A_EINVAL, "%s: cache strides (page %lld, token %lld, head %lld) unsupported", who,
-                (long long)kv_stride_page, (long long)kv_stride_tok, (long long)kv_stride_head);
+  rc = check_pool(k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
+                  max_pages_per_seq, head_dim, who);
+  if (rc != Q3A_OK) return rc;
 
   PrefillArgs a{};
   a.q = static_cast<const uint16_t*>(q);
@@ -822,37 +893,26 @@ extern "C" int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_s
   a.causal = causal ? 1 : 0;
   a.scale_log2 = softmax_scale * kLog2e;
   a.hkv = num_kv_heads;
-  a.pk = static_cast<uint16_t*>(k_cache);
-  a.pv = static_cast<uint16_t*>(v_cache);
-  a.p_sp = kv_stride_page;
-  a.p_st = kv_stride_tok;
-  a.p_sh = kv_stride_head;
-  a.pbt = block_table;
-  a.pbt_sb = bt_stride_b;
-  a.p_pages = num_pages;
-  a.p_shift = 0;
-  while ((1 << a.p_shift) < page_size) ++a.p_shift;
-  a.p_max_pages = max_pages_per_seq;
+  set_pool(a, k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
+           bt_stride_b, max_pages_per_seq, -1);
   return launch(a, num_seqs, max_seqlen_q, stream, who);
 }
 
-extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
-                                 const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
-                                 const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
-                                 void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs,
-                                 int seqlen_q, int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
-                                 float softmax_scale, int causal, void* stream) {
-  if (num_seqs < 0 || seqlen_q < 0 || seqlen_k < 0)
-    return fail(Q3A_EINVAL, "prefill_dense: negative num_seqs/seqlen_q/seqlen_k");
-  if (num_seqs == 0 || seqlen_q == 0) return Q3A_OK;
+// The dense form with an optional pool write (a.pk set by the caller).
+static int prefill_dense_impl(PrefillArgs& a, const void* q, int64_t q_stride_s, int64_t q_stride_t,
+                              int64_t q_stride_h, const void* k, int64_t k_stride_s, int64_t k_stride_t,
+                              int64_t k_stride_h, const void* v, int64_t v_stride_s, int64_t v_stride_t,
+                              int64_t v_stride_h, void* out, int64_t o_stride_s, int64_t o_stride_t,
+                              int64_t o_stride_h, int num_seqs, int seqlen_q, int seqlen_k, int num_q_heads,
+                              int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream,
+                              const char* who) {
   int rc = check_common(q, k, v, out, q_stride_t, q_stride_h, k_stride_t, k_stride_h, v_stride_t, v_stride_h,
-                        o_stride_t, o_stride_h, num_q_heads, num_kv_heads, head_dim, "prefill_dense");
+                        o_stride_t, o_stride_h, num_q_heads, num_kv_heads, head_dim, who);
   if (rc != Q3A_OK) return rc;
   if ((q_stride_s | k_stride_s | v_stride_s | o_stride_s) % 8 != 0 || q_stride_s < 0 || k_stride_s < 0 ||
       v_stride_s < 0 || o_stride_s < 0)
-    return fail(Q3A_EINVAL, "prefill_dense: sequence strides must be non-negative multiples of 8 elements");
+    return fail(Q3A_EINVAL, "%s: sequence strides must be non-negative multiples of 8 elements", who);
 
-  PrefillArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_t;
   a.q_sh = q_stride_h;
@@ -884,13 +944,58 @@ extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_st
     const int nblk = (ngroups + kResMaxGroups - 1) / kResMaxGroups;
     const int waves = ngroups < kResMaxGroups ? ngroups : kResMaxGroups;
     if ((int64_t)num_seqs * num_kv_heads > 0x7fffffff || 2 * nblk > 65535)
-      return fail(Q3A_EINVAL, "prefill_dense: grid too large (%d seqs x %d KV heads x %d query blocks)", num_seqs,
+      return fail(Q3A_EINVAL, "%s: grid too large (%d seqs x %d KV heads x %d query blocks)", who, num_seqs,
                   num_kv_heads, nblk);
     hipLaunchKernelGGL(prefill_resident_kernel, dim3(num_seqs * num_kv_heads, 1, 2 * nblk), dim3(64 * waves), 0,
                        static_cast<hipStream_t>(stream), a, ntiles);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "prefill_dense: launch failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
     return Q3A_OK;
   }
-  return launch(a, num_seqs, seqlen_q, stream, "prefill_dense");
+  return launch(a, num_seqs, seqlen_q, stream, who);
+}
+
+extern "C" int q3a_prefill_dense(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
+                                 const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
+                                 const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
+                                 void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs,
+                                 int seqlen_q, int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim,
+                                 float softmax_scale, int causal, void* stream) {
+  if (num_seqs < 0 || seqlen_q < 0 || seqlen_k < 0)
+    return fail(Q3A_EINVAL, "prefill_dense: negative num_seqs/seqlen_q/seqlen_k");
+  if (num_seqs == 0 || seqlen_q == 0) return Q3A_OK;
+  PrefillArgs a{};
+  return prefill_dense_impl(a, q, q_stride_s, q_stride_t, q_stride_h, k, k_stride_s, k_stride_t, k_stride_h, v,
+                            v_stride_s, v_stride_t, v_stride_h, out, o_stride_s, o_stride_t, o_stride_h, num_seqs,
+                            seqlen_q, seqlen_k, num_q_heads, num_kv_heads, head_dim, softmax_scale, causal, stream,
+                            "prefill_dense");
+}
+
+extern "C" int q3a_prefill_dense_append(const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
+                                        const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
+                                        const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
+                                        void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                                        int64_t kv_stride_head, int num_pages, int page_size,
+                                        const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq,
+                                        int first_row, void* out, int64_t o_stride_s, int64_t o_stride_t,
+                                        int64_t o_stride_h, int num_seqs, int seqlen_q, int seqlen_k, int num_q_heads,
+                                        int num_kv_heads, int head_dim, float softmax_scale, int causal,
+                                        void* stream) {
+  const char* who = "prefill_dense_append";
+  if (num_seqs < 0 || seqlen_q < 0 || seqlen_k < 0)
+    return fail(Q3A_EINVAL, "%s: negative num_seqs/seqlen_q/seqlen_k", who);
+  if (first_row < 0 || first_row > std::max(0, seqlen_k - seqlen_q))
+    return fail(Q3A_EINVAL, "%s: first_row %d must lie in [0, max(0, seqlen_k - seqlen_q) = %d]", who, first_row,
+                std::max(0, seqlen_k - seqlen_q));
+  if (num_seqs == 0 || seqlen_q == 0) return Q3A_OK;
+  int rc = check_pool(k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size,
+                      block_table, max_pages_per_seq, head_dim, who);
+  if (rc != Q3A_OK) return rc;
+  PrefillArgs a{};
+  set_pool(a, k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
+           bt_stride_b, max_pages_per_seq, first_row);
+  return prefill_dense_impl(a, q, q_stride_s, q_stride_t, q_stride_h, k, k_stride_s, k_stride_t, k_stride_h, v,
+                            v_stride_s, v_stride_t, v_stride_h, out, o_stride_s, o_stride_t, o_stride_h, num_seqs,
+                            seqlen_q, seqlen_k, num_q_heads, num_kv_heads, head_dim, softmax_scale, causal, stream,
+                            who);
 }

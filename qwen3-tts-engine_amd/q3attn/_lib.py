@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (must precede the library load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -108,6 +108,17 @@ SIGNATURES = {
         _c_vp, _c_i64, _c_i64, _c_i64,                         # q, q strides (seq, tok, head)
         _c_vp, _c_i64, _c_i64, _c_i64,                         # k, k strides (seq, tok, head)
         _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (seq, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # out, o strides (seq, tok, head)
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, seqlen_k, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
+    ]),
+    "q3a_prefill_dense_append": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # q, q strides (seq, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # k, k strides (seq, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (seq, tok, head)
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k_cache, v_cache, cache strides (page, tok, head)
+        _c_int, _c_int, _c_vp, _c_i64, _c_int,                 # num_pages, page_size, block_table, bt stride, max pages
+        _c_int,                                                # first_row
         _c_vp, _c_i64, _c_i64, _c_i64,                         # out, o strides (seq, tok, head)
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, seqlen_k, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream

@@ -169,6 +169,53 @@ def _prefill_dense_fake(q, k, v, softmax_scale, causal):
     return q.new_empty(q.shape)
 
 
+@torch.library.custom_op("q3attn::prefill_dense_append", mutates_args=("k_cache", "v_cache"))
+def prefill_dense_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                         v_cache: torch.Tensor, block_table: torch.Tensor, softmax_scale: float, causal: bool = True,
+                         first_row: int = 0) -> torch.Tensor:
+    """The fast-admission layer step in one launch: rows first_row .. n-1 of every sequence's K and V (dense
+    [S, n, Hkv, D]) go into the paged pool [num_pages, page, Hkv, D] at positions first_row .. n-1 of the sequence,
+    through block_table [S, max_pages] (engine/arrivals.py:144-145 scatters all n rows with index_copy_ at
+    seat * seat_len + position), and the result is flash_attn_func(q, k, v, softmax_scale, causal) on the dense
+    k/v (engine/arrivals.py:148), bit for bit.  first_row = 0 is the engine's call; n - R writes only the new rows
+    (a prefix already in the pool)."""
+    who = "q3attn.prefill_dense_append"
+    _req(q.is_cuda, f"{who}: tensors must be on a GPU (there is no CPU path)")
+    for name, t in (("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table)):
+        _req(t.device == q.device, f"{who}: {name} is on {t.device}, q on {q.device}")
+    _req(all(t.dtype == torch.bfloat16 for t in (q, k, v, k_cache, v_cache)),
+         f"{who}: q, k, v and the caches must be bfloat16")
+    _req(q.dim() == 4 and k.dim() == 4 and k.shape == v.shape and q.shape[0] == k.shape[0] and q.shape[3] == k.shape[3],
+         f"{who}: q [S,R,H,D], k/v [S,n,Hkv,D]")
+    _req(q.stride(3) == 1 and k.stride(3) == 1 and v.stride(3) == 1, f"{who}: head_dim must be contiguous")
+    _req(k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride()
+         and k_cache.stride(-1) == 1 and k_cache.shape[2:] == k.shape[2:],
+         f"{who}: k_cache and v_cache must be [num_pages, page, kv_heads, head_dim] with equal strides")
+    S, R, Hq, D = q.shape
+    n, Hkv = k.shape[1], k.shape[2]
+    _req(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == S
+         and block_table.stride(1) == 1, f"{who}: block_table must be int32 [S, max_pages] with contiguous rows")
+    _req(0 <= first_row <= max(0, n - R), f"{who}: first_row {first_row} must lie in [0, max(0, n - R)]")
+    out = torch.empty((S, R, Hq, D), dtype=q.dtype, device=q.device)
+    if S == 0 or R == 0:
+        return out
+    num_pages, page = k_cache.shape[0], k_cache.shape[1]
+    rc = lib().q3a_prefill_dense_append(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        num_pages, page, block_table.data_ptr(), block_table.stride(0), block_table.shape[1], int(first_row),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), S, R, n, Hq, Hkv, D,
+        float(softmax_scale), 1 if causal else 0, torch.cuda.current_stream(q.device).cuda_stream)
+    check(rc, "q3a_prefill_dense_append")
+    return out
+
+
+@prefill_dense_append.register_fake
+def _prefill_dense_append_fake(q, k, v, k_cache, v_cache, block_table, softmax_scale, causal=True, first_row=0):
+    return q.new_empty(q.shape)
+
+
 def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
                     alibi_slopes=None, deterministic=False, return_attn_probs=False):
     """Drop-in for ``flash_attn.flash_attn_func`` as the fast-admission path calls it (engine/arrivals.py:148):

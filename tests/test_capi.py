@@ -320,6 +320,37 @@ def test_prefill_append_empty_is_a_noop():
     assert _prefill_append(n=0) == 0 and _prefill_append(max_q=0) == 0
 
 
+def _prefill_dense_append(**kw):
+    """The admission shape (engine/arrivals.py:144-148): S = 8, R = 42 over n = 77 keys, fake aligned pointers."""
+    a = dict(q=16, q_ss=42 * 2048, q_st=2048, q_sh=128, k=16, k_ss=77 * 1024, k_st=1024, k_sh=128,
+             v=16, v_ss=77 * 1024, v_st=1024, v_sh=128, kc=16, vc=16, c_sp=16384, c_st=1024, c_sh=128,
+             num_pages=64, page=16, bt=16, bt_sb=8, max_pages=8, first=0, out=16, o_ss=42 * 2048, o_st=2048,
+             o_sh=128, S=8, R=42, n=77, Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
+    a.update(kw)
+    return _lib.lib().q3a_prefill_dense_append(
+        a["q"], a["q_ss"], a["q_st"], a["q_sh"], a["k"], a["k_ss"], a["k_st"], a["k_sh"], a["v"], a["v_ss"],
+        a["v_st"], a["v_sh"], a["kc"], a["vc"], a["c_sp"], a["c_st"], a["c_sh"], a["num_pages"], a["page"], a["bt"],
+        a["bt_sb"], a["max_pages"], a["first"], a["out"], a["o_ss"], a["o_st"], a["o_sh"], a["S"], a["R"], a["n"],
+        a["Hq"], a["Hkv"], a["D"], a["scale"], a["causal"], None)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(kc=None), "null pointer"), (dict(bt=None), "null pointer"), (dict(k=None), "null pointer"),
+    (dict(page=48), "power of two"), (dict(num_pages=0), "num_pages"), (dict(max_pages=0), "num_pages"),
+    (dict(vc=8), "aligned"), (dict(c_st=64), "cache strides"), (dict(c_sp=1024), "cache strides"),
+    (dict(first=-1), "first_row"), (dict(first=36), "first_row"), (dict(n=40, first=1), "first_row"),
+    (dict(D=64), "head_dim"), (dict(k_ss=-8), "sequence strides"), (dict(S=-1), "negative"),
+])
+def test_prefill_dense_append_rejects_bad_arguments(kw, frag):
+    assert _prefill_dense_append(**kw) < 0
+    assert frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_prefill_dense_append_empty_is_a_noop():
+    """Nothing to compute or write: no device pointer is touched (these are fake addresses)."""
+    assert _prefill_dense_append(S=0) == 0 and _prefill_dense_append(R=0, first=0) == 0
+
+
 def test_prefill_empty_is_a_noop():
     assert _prefill(n=0) == 0 and _prefill(max_q=0) == 0
 
