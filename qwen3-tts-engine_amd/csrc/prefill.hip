@@ -523,6 +523,7 @@ constexpr int kResMaxTiles = 4;
 constexpr int kResQ = 16;
 constexpr int kResMaxGroups = 16;  // waves per workgroup
 
+template <bool kAppend>
 __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(const PrefillArgs a, int ntiles) {
   __shared__ __align__(16) uint8_t sK[kResMaxTiles * kTileB];
   __shared__ __align__(16) uint8_t sV[kResMaxTiles * kTileB];
@@ -543,9 +544,12 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
   const int64_t qbase = (int64_t)s * a.q_ss, obase = (int64_t)s * a.o_ss;
 
   // Append form: rows p_first .. Lk - 1 of this KV head go into the pool from the LDS copy, K by the workgroup of
-  // query head 0 and V by that of query head 1 (first query block only).  Lane i holds table entry i (Lk <= 128
-  // keys span at most 8 pages of >= 16); it is loaded beside the copies, so it adds no round trip.
-  const bool app = a.pk != nullptr && (blockIdx.z >> 1) == 0;
+  // query head 0 and V by that of query head 1 (first query block only).  When the query groups fit in one
+  // workgroup the host adds one wave that holds no query token: it helps with the copies and then makes all the
+  // pool stores while the other waves compute; otherwise every wave of the block takes a share.  Lane i holds table
+  // entry i (Lk <= 128 keys span at most 8 pages of >= 16); it is loaded beside the copies, so it adds no round trip.
+  const bool app = kAppend && (blockIdx.z >> 1) == 0;
+  const bool store_wave = kAppend && nwaves > (Lq + kResQ - 1) / kResQ;  // the last wave is the extra one
   int pwo = -1;
   if (app && lane < min(kResMaxTiles * kKT / 16, a.p_max_pages)) pwo = a.pbt[(int64_t)s * a.pbt_sb + lane];
 
@@ -583,18 +587,21 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
   wait_vmem();
   __syncthreads();
   if (app) {
-    // LDS slot c of key row r holds global chunk c ^ (r & 15) (the copy's swizzle).  The loop bound is uniform
-    // across the workgroup so that every lane takes part in the table shuffle.
+    // Rows go out in aligned groups of 4 (lane: row 4 gi + lane / 16, chunk lane % 16), group gi to wave gi mod
+    // nwaves.  A group never straddles a page (pages hold >= 16 rows), so its page id is wave-uniform: one
+    // v_readlane, no cross-lane shuffle in the chain.  LDS slot c of key row r holds global chunk c ^ (r & 15).
     const uint8_t* src = hh == 0 ? sK : sV;
     uint16_t* const dst = hh == 0 ? a.pk : a.pv;
-    const int nch = (Lk - a.p_first) * 16;
-    for (int c0 = 0; c0 < nch; c0 += (int)blockDim.x) {
-      const int idx = c0 + tid;
-      const int r = a.p_first + (idx >> 4);
-      const int ch = idx & 15;
-      const int pi = r >> a.p_shift;
-      const int page = __shfl(pwo, min(pi, 63));
-      if (idx < nch && pi < a.p_max_pages && (unsigned)page < (unsigned)a.p_pages)
+    const int ch = lane & 15;
+    const int ng = (Lk + 3) >> 2;
+    const int w0 = store_wave ? wave - (nwaves - 1) : wave;   // < 0: a compute wave with the extra one present
+    const int ws = store_wave ? 1 : nwaves;
+#pragma unroll 4
+    for (int gi = w0 < 0 ? ng : (a.p_first >> 2) + w0; gi < ng; gi += ws) {
+      const int r = 4 * gi + (lane >> 4);
+      const int pi = (4 * gi) >> a.p_shift;
+      const int page = readlane(pwo, min(pi, 63));
+      if (r >= a.p_first && r < Lk && pi < a.p_max_pages && (unsigned)page < (unsigned)a.p_pages)
         st16(dst + (int64_t)page * a.p_sp + (int64_t)(r & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)g * a.p_sh +
                  8 * ch,
              ld16(src + r * kRowB + ((ch ^ (r & 15)) << 4)));
@@ -946,8 +953,15 @@ static int prefill_dense_impl(PrefillArgs& a, const void* q, int64_t q_stride_s,
     if ((int64_t)num_seqs * num_kv_heads > 0x7fffffff || 2 * nblk > 65535)
       return fail(Q3A_EINVAL, "%s: grid too large (%d seqs x %d KV heads x %d query blocks)", who, num_seqs,
                   num_kv_heads, nblk);
-    hipLaunchKernelGGL(prefill_resident_kernel, dim3(num_seqs * num_kv_heads, 1, 2 * nblk), dim3(64 * waves), 0,
-                       static_cast<hipStream_t>(stream), a, ntiles);
+    // The append form is its own instantiation: its store loop changes the plain kernel's schedule (5.36 -> 5.87 us
+    // on the admission shape when shared).  With fewer than 16 query groups it runs one extra wave for the stores.
+    if (a.pk != nullptr)
+      hipLaunchKernelGGL(prefill_resident_kernel<true>, dim3(num_seqs * num_kv_heads, 1, 2 * nblk),
+                         dim3(64 * (waves + (ngroups < kResMaxGroups ? 1 : 0))), 0, static_cast<hipStream_t>(stream),
+                         a, ntiles);
+    else
+      hipLaunchKernelGGL(prefill_resident_kernel<false>, dim3(num_seqs * num_kv_heads, 1, 2 * nblk), dim3(64 * waves),
+                         0, static_cast<hipStream_t>(stream), a, ntiles);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
     return Q3A_OK;
