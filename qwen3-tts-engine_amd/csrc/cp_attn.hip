@@ -116,8 +116,11 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
       if (s == last) vr[s] = vn;
     const __amdgpu_buffer_rsrc_t wk = make_rsrc(kb + (int64_t)last * a.k_ss, kD * 2);
     const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.v_ss, kD * 2);
-    buffer_store16_s(knc, wk, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange, 0u);
-    __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, 0);
+    // Non-temporal slot and output stores (the lines stream out instead of staying dirty in the L2): 6.83 -> 6.79 us
+    // per call in the 512-row frame.
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, knc), wk,
+                                           (int)(lane < 16 ? (uint32_t)lane * 16 : kOutOfRange), 0, kCacheNT);
+    __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, kCacheNT);
   }
 
   auto dot16 = [](const uint4& q0, const uint4& k0, const uint4& q1, const uint4& k1) {
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   uint16_t* ob = a.out + (int64_t)b * a.o_sb + (int64_t)(kG * g) * kD;
 #pragma unroll
   for (int h = 0; h < kG; ++h)
-    *reinterpret_cast<uint32_t*>(ob + h * kD + 2 * lane) = pack_bf16x2(o[h][0], o[h][1]);
+    __builtin_nontemporal_store(pack_bf16x2(o[h][0], o[h][1]), reinterpret_cast<uint32_t*>(ob + h * kD + 2 * lane));
 }
 
 }  // namespace

@@ -485,10 +485,12 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int b, int g,
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  uint2 o;
+  // Non-temporal: with the slot stores below, 200.5 -> 198.9 us per append call at 576 rows (the plain form
+  // unchanged within noise).
+  u32x2 o;
   o.x = pack_bf16x2(A.x * inv, A.y * inv);
   o.y = pack_bf16x2(A.z * inv, A.w * inv);
-  *reinterpret_cast<uint2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0) = o;
+  __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0));
 }
 
 __device__ __forceinline__ void write_zero_row(const DecodeArgs& a, int b, int g, int lane) {
@@ -776,8 +778,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const Dec
       if ((unsigned)page < (unsigned)a.num_pages) {
         const int pidx = c / a.page_size;
         const int64_t dst = (int64_t)page * a.kv_sp + (int64_t)(c - pidx * a.page_size) * a.kv_st + (int64_t)g * a.kv_sh;
-        reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.kc) + dst)[lane] = kw;
-        reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.vc) + dst)[lane] = vw;
+        __builtin_nontemporal_store(kw, reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.kc) + dst) + lane);
+        __builtin_nontemporal_store(vw, reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.vc) + dst) + lane);
       }
     }
   };

@@ -590,6 +590,7 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
     // Rows go out in aligned groups of 4 (lane: row 4 gi + lane / 16, chunk lane % 16), group gi to wave gi mod
     // nwaves.  A group never straddles a page (pages hold >= 16 rows), so its page id is wave-uniform: one
     // v_readlane, no cross-lane shuffle in the chain.  LDS slot c of key row r holds global chunk c ^ (r & 15).
+    // Non-temporal stores: 6.93 -> 6.53 us per call on the admission shape (8 x 42 over 77 keys).
     const uint8_t* src = hh == 0 ? sK : sV;
     uint16_t* const dst = hh == 0 ? a.pk : a.pv;
     const int ch = lane & 15;
@@ -602,9 +603,9 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
       const int pi = (4 * gi) >> a.p_shift;
       const int page = readlane(pwo, min(pi, 63));
       if (r >= a.p_first && r < Lk && pi < a.p_max_pages && (unsigned)page < (unsigned)a.p_pages)
-        st16(dst + (int64_t)page * a.p_sp + (int64_t)(r & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)g * a.p_sh +
-                 8 * ch,
-             ld16(src + r * kRowB + ((ch ^ (r & 15)) << 4)));
+        st16_nt(dst + (int64_t)page * a.p_sp + (int64_t)(r & ((1 << a.p_shift) - 1)) * a.p_st +
+                    (int64_t)g * a.p_sh + 8 * ch,
+                ld16(src + r * kRowB + ((ch ^ (r & 15)) << 4)));
     }
   }
   if (tg * kResQ >= Lq) return;                 // a wave with no query token (after the barrier: it copied)

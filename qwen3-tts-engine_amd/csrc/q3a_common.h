@@ -63,6 +63,7 @@ __device__ __forceinline__ uint4 buffer_load16_s(__amdgpu_buffer_rsrc_t r, uint3
 }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // 16-byte loads/stores through a vector type.  A plain `uint4` assignment from memory is a struct copy
 // (a memcpy in the IR) that can leave the destination array in private (scratch) memory; these stay in
@@ -71,6 +72,10 @@ __device__ __forceinline__ uint4 ld16(const void* p) {
   return __builtin_bit_cast(uint4, *reinterpret_cast<const u32x4*>(p));
 }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<u32x4*>(p) = __builtin_bit_cast(u32x4, v); }
+// The same store with the non-temporal hint: the line streams out instead of staying dirty in the L2.
+__device__ __forceinline__ void st16_nt(void* p, uint4 v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+}
 __device__ __forceinline__ void buffer_store16_s(uint4 v, __amdgpu_buffer_rsrc_t r, uint32_t byte_off,
                                                  uint32_t s_off) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)byte_off, (int)s_off, 0);
