@@ -478,7 +478,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
   // The 4 lanes of a token hold partial sums over disjoint keys.  The output goes out through LDS as whole 256 B
   // head rows (16 B per lane): written straight from the accumulator layout each lane would store 8 B pieces, 32 B
-  // of a token row per 4 lanes, which the L2 has to merge.  Each wave stages its 16 tokens x 2 heads (8 KiB) in one
+  // of a token row per 4 lanes, which the L2 has to merge.  The stores carry the non-temporal hint: the output is
+  // never read here, and kept in the L2 it evicted the K/V pages a sequence's query tiles share (32 x U[150, 400]
+  // tokens: 33.6 -> 30.4 us per call).  Each wave stages its 16 tokens x 2 heads (8 KiB) in one
   // of the tile arrays, free once every wave has passed the loop's last barrier (the pool stores above still read
   // them, hence the barrier in that form).  16 B chunks are XOR-swizzled by token, so neither side conflicts.
   if (pool_from_lds) __syncthreads();
@@ -504,7 +506,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int token = qt * kQT + wave * 16 + t;
     if (token < Lq) {
       const uint4 x = ld16(so + hh * 16 * kRowB + t * kRowB + ((c ^ t) << 4));
-      st16(a.out + obase + (int64_t)token * a.o_st + (kG * g + hh) * a.o_sh + 8 * c, x);
+      st16_nt(a.out + obase + (int64_t)token * a.o_st + (kG * g + hh) * a.o_sh + 8 * c, x);
     }
   }
 }
