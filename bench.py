@@ -686,6 +686,7 @@ def bench_admit_append(args, dev, wls):
     import torch
 
     import q3attn
+    from q3attn.workloads import rope_tables as W_rope_tables
 
     S, n = wls[0].k.shape[0], wls[0].k.shape[1]
     P, page, num_pages = -(-n // 16), 16, 256
@@ -712,14 +713,66 @@ def bench_admit_append(args, dev, wls):
         return [q3attn.prefill_dense_append(wl.q, wl.k, wl.v, kc, vc, bt, wl.scale, True, 0)
                 for wl, kc, vc, bt, _ in steps]
 
+    # The whole attention block of the admission layer (engine/arrivals.py:112-118, 144-148): q/k RMSNorm + RoPE as the
+    # eager bf16 torch ops the uncompiled layer runs, torch.cat of the voice prefix K/V (gathered per admitted slot),
+    # the two scatters and the attention, against prefill_dense_append_rope.  Synthetic qkv projections and weights.
+    P = n - wls[0].q.shape[1]
+    R = wls[0].q.shape[1]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 77)
+    cos_t, sin_t = W_rope_tables(n, dev)
+    cos_r = cos_t[P:].to(torch.bfloat16)[None, :, None]
+    sin_r = sin_t[P:].to(torch.bfloat16)[None, :, None]
+    voices = 4
+    blocks = []
+    for l, (wl, kc, vc, bt, flat) in enumerate(steps):
+        qkv = torch.randn((S, R, 4096), generator=gen, device=dev).to(torch.bfloat16)
+        pk = wl.k[:voices, :P].contiguous() if S >= voices else wl.k[:, :P].contiguous()
+        pv = wl.v[:voices, :P].contiguous() if S >= voices else wl.v[:, :P].contiguous()
+        qn = (1.0 + 0.1 * torch.randn(128, generator=gen, device=dev)).to(torch.bfloat16)
+        kn = (1.0 + 0.1 * torch.randn(128, generator=gen, device=dev)).to(torch.bfloat16)
+        slot = torch.arange(S, device=dev, dtype=torch.int64) % pk.shape[0]
+        blocks.append((qkv, pk, pv, qn, kn, slot, kc, vc, bt, flat))
+
+    def rms_t(x, w, eps=1e-6):
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+        return w * xf.to(x.dtype)
+
+    def rope_t(x, c, s_):
+        return x * c + torch.cat((-x[..., 64:], x[..., :64]), dim=-1) * s_
+
+    def engine_block():
+        out = []
+        for qkv, pk, pv, qn, kn, slot, kc, vc, bt, flat in blocks:
+            q = rope_t(rms_t(qkv[..., :2048].view(S, R, 16, 128), qn), cos_r, sin_r)
+            kk = rope_t(rms_t(qkv[..., 2048:3072].view(S, R, 8, 128), kn), cos_r, sin_r)
+            K = torch.cat((pk[slot], kk), 1)
+            V = torch.cat((pv[slot], qkv[..., 3072:].view(S, R, 8, 128)), 1)
+            kc.view(-1, 8, 128).index_copy_(0, flat, K.reshape(-1, 8, 128))
+            vc.view(-1, 8, 128).index_copy_(0, flat, V.reshape(-1, 8, 128))
+            out.append(q3attn.flash_attn_func(q, K, V, softmax_scale=wls[0].scale, causal=True))
+        return out
+
+    def fused_block():
+        return [q3attn.prefill_dense_append_rope(qkv[..., :2048].view(S, R, 16, 128),
+                                                 qkv[..., 2048:3072].view(S, R, 8, 128),
+                                                 qkv[..., 3072:].view(S, R, 8, 128), pk, pv, qn, kn,
+                                                 cos_r, sin_r, kc, vc, bt, wls[0].scale, slot)
+                for qkv, pk, pv, qn, kn, slot, kc, vc, bt, _ in blocks]
+
     res = {}
     for name, fn in (("flash_attn_func", dense), ("index_copy_then_prefill", scatter_then_prefill),
-                     ("prefill_dense_append", fused)):
+                     ("prefill_dense_append", fused), ("torch_producers_cat_index_copy_then_prefill", engine_block),
+                     ("prefill_dense_append_rope", fused_block)):
         _, fr, _ = time_graph(dev, fn, args.steps, args.warmup, getattr(args, "min_warm_s", 0.0))
         res[name + "_us_per_layer_call"] = round(statistics.mean(fr) * 1e3 / LAYERS, 2)
     log(f"[bench] admission step: prefill_dense_append {res['prefill_dense_append_us_per_layer_call']:.2f} us/layer "
         f"call; index_copy_ x2 + prefill {res['index_copy_then_prefill_us_per_layer_call']:.2f}; prefill alone "
         f"{res['flash_attn_func_us_per_layer_call']:.2f}")
+    log(f"[bench] admission block with the q/k producers: prefill_dense_append_rope "
+        f"{res['prefill_dense_append_rope_us_per_layer_call']:.2f} us/layer call; eager torch producers + cat + "
+        f"index_copy_ x2 + prefill {res['torch_producers_cat_index_copy_then_prefill_us_per_layer_call']:.2f}")
     return res
 
 

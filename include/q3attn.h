@@ -27,8 +27,8 @@ extern "C" {
 
 /* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
  * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope.
- * 5: q3a_prefill_dense_append. */
-#define Q3A_ABI_VERSION 5
+ * 5: q3a_prefill_dense_append.  6: q3a_prefill_dense_append_rope. */
+#define Q3A_ABI_VERSION 6
 int q3a_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -283,6 +283,42 @@ int q3a_prefill_dense_append(const void* q, int64_t q_stride_s, int64_t q_stride
                              int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, int num_seqs, int seqlen_q,
                              int seqlen_k, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale,
                              int causal, void* stream);
+
+/*
+ * The fast-admission layer's attention block in two launches on the caller's stream (engine/arrivals.py:112-118 and
+ * 144-148): the producers q = rope(rms(q_raw, q_norm_w)), k = rope(rms(k_raw, k_norm_w)) (engine/ops.py:51-60,
+ * evaluated with the rounding of eager bf16 ops: every op rounds to bf16), K = cat(prefix_k, k), V = cat(prefix_v, v)
+ * (engine/arrivals.py:118), the two index_copy_ scatters of K and V into the pool (:144-145) and the attention
+ * flash_attn_func(q, K, V, causal) (:148).  The first launch writes q, K and V into the workspace; the second is
+ * q3a_prefill_dense_append on them (rows first_row .. n-1 into the pool, n = prefix_len + seqlen_q).
+ *
+ *   q          [S, R, Hq, D] bf16 raw projections (strides q_stride_s/t/h; a view of the qkv output is fine)
+ *   k, v       [S, R, Hkv, D] bf16 raw new keys and the new values (their own strides)
+ *   prefix_k/v [num_prefixes, P, Hkv, D] bf16, already normalised and rotated (the registered voice's K/V);
+ *              sequence s takes prefix prefix_index[s] (int64), or prefix s when prefix_index is NULL.  An index
+ *              outside [0, num_prefixes) reads zeros.
+ *   q_norm_w, k_norm_w  [D] bf16;  cos, sin  [R, D] bf16 rows of the new tokens' positions (row stride
+ *              rope_stride_t; the same for every sequence, as engine/arrivals.py:109 slices them)
+ *   pool, table, first_row (0 <= first_row <= P), out: as q3a_prefill_dense_append
+ *   workspace  q3a_prefill_dense_append_rope_workspace_bytes(S, R, P, Hq, Hkv, D) bytes, 16-byte aligned
+ * Requirements: D == 128, Hq == 2 * Hkv, Hkv a multiple of 4, 16-byte aligned tensors, strides non-negative multiples
+ * of 8 elements.  With num_seqs == 0 or seqlen_q == 0 nothing is computed or written.
+ */
+size_t q3a_prefill_dense_append_rope_workspace_bytes(int num_seqs, int seqlen_q, int prefix_len, int num_q_heads,
+                                                     int num_kv_heads, int head_dim);
+int q3a_prefill_dense_append_rope(
+    const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
+    const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
+    const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
+    const void* prefix_k, int64_t pk_stride_s, int64_t pk_stride_t, int64_t pk_stride_h,
+    const void* prefix_v, int64_t pv_stride_s, int64_t pv_stride_t, int64_t pv_stride_h,
+    const int64_t* prefix_index, int64_t num_prefixes,
+    const void* q_norm_w, const void* k_norm_w, const void* cos, const void* sin, int64_t rope_stride_t, float eps,
+    void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head,
+    int num_pages, int page_size, const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq,
+    int first_row, void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, void* workspace,
+    size_t workspace_bytes, int num_seqs, int seqlen_q, int prefix_len, int num_q_heads, int num_kv_heads,
+    int head_dim, float softmax_scale, int causal, void* stream);
 
 #ifdef __cplusplus
 }

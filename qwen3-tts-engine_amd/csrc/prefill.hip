@@ -599,7 +599,6 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
     const int ng = (Lk + 3) >> 2;
     const int w0 = store_wave ? wave - (nwaves - 1) : wave;   // < 0: a compute wave with the extra one present
     const int ws = store_wave ? 1 : nwaves;
-#pragma unroll 4
     for (int gi = w0 < 0 ? ng : (a.p_first >> 2) + w0; gi < ng; gi += ws) {
       const int r = 4 * gi + (lane >> 4);
       const int pi = (4 * gi) >> a.p_shift;
@@ -704,6 +703,85 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
       w.y = pack_bf16x2(acc[db][2] * inv, acc[db][3] * inv);
       *reinterpret_cast<uint2*>(o + db * 16) = w;
     }
+  }
+}
+
+// ------------------------------------------------------------------------------ admission producers
+// The fast-admission layer's attention inputs (engine/arrivals.py:112-118): q = rope(rms(q_raw, qn)), the new keys
+// rope(rms(k_raw, kn)) after the K/V prefix, and the new values after the V prefix, i.e. K = cat(prefix K, new keys)
+// and V = cat(prefix V, v) of engine/arrivals.py:118, written dense for the attention that follows.  One 128-dim row
+// per 16 lanes (16 B each, the qk_norm_rope16 layout); the row jobs are numbered q rows, new K rows, new V rows,
+// prefix K rows, prefix V rows, each block a multiple of 4 rows, so a wave's four rows are all of one kind.
+struct AdmitPrepArgs {
+  const uint16_t* q;
+  int64_t q_ss, q_st, q_sh;
+  const uint16_t* k;
+  int64_t k_ss, k_st, k_sh;
+  const uint16_t* v;
+  int64_t v_ss, v_st, v_sh;
+  const uint16_t* pk;
+  int64_t pk_ss, pk_st, pk_sh;
+  const uint16_t* pv;
+  int64_t pv_ss, pv_st, pv_sh;
+  const int64_t* pidx;  // nullptr: sequence s takes prefix s; else prefix pidx[s] (outside [0, npre): zeros)
+  int64_t npre;
+  const uint16_t* qn;
+  const uint16_t* kn;
+  const uint16_t* cs;   // cos/sin rows of the new tokens' positions, row t for token t
+  const uint16_t* sn;
+  int64_t cs_st;
+  float eps;
+  uint16_t* qo;  // [S, R, Hq, D]
+  uint16_t* ko;  // [S, n, Hkv, D]
+  uint16_t* vo;  // [S, n, Hkv, D]
+  int R, P, Hq, Hkv;
+  int64_t jq, jk, jv, jp, jall;  // job block ends: q | new K | new V | prefix K | prefix V
+};
+
+__global__ __launch_bounds__(256) void admit_prep_kernel(const AdmitPrepArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t j0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;  // the wave's first row job
+  if (j0 >= a.jall) return;                                               // wave-uniform
+  const int64_t j = j0 + (lane >> 4);
+  const int c8 = 8 * (lane & 15);  // this lane's 8 dims
+  const int n = a.P + a.R;
+  if (j0 < a.jk) {
+    // normalise + rotate: q rows, then the new K rows
+    const bool isq = j0 < a.jq;
+    const int H = isq ? a.Hq : a.Hkv;
+    const int64_t jj = isq ? j : j - a.jq;
+    const int h = (int)(jj % H);
+    const int t = (int)((jj / H) % a.R);
+    const int64_t sq = jj / ((int64_t)H * a.R);
+    const uint4 x = isq ? ld16(a.q + sq * a.q_ss + (int64_t)t * a.q_st + (int64_t)h * a.q_sh + c8)
+                        : ld16(a.k + sq * a.k_ss + (int64_t)t * a.k_st + (int64_t)h * a.k_sh + c8);
+    const uint4 w = ld16((isq ? a.qn : a.kn) + c8);
+    const uint4 c = ld16(a.cs + (int64_t)t * a.cs_st + c8);
+    const uint4 sn = ld16(a.sn + (int64_t)t * a.cs_st + c8);
+    const uint4 y = qk_norm_rope16_eager(x, w, c, sn, a.eps);
+    if (isq)
+      st16(a.qo + ((sq * a.R + t) * a.Hq + h) * kD + c8, y);
+    else
+      st16(a.ko + ((sq * n + a.P + t) * a.Hkv + h) * kD + c8, y);
+  } else if (j0 < a.jv) {
+    const int64_t jj = j - a.jk;  // new V rows
+    const int h = (int)(jj % a.Hkv);
+    const int t = (int)((jj / a.Hkv) % a.R);
+    const int64_t sq = jj / ((int64_t)a.Hkv * a.R);
+    st16(a.vo + ((sq * n + a.P + t) * a.Hkv + h) * kD + c8,
+         ld16(a.v + sq * a.v_ss + (int64_t)t * a.v_st + (int64_t)h * a.v_sh + c8));
+  } else {
+    const bool isk = j0 < a.jp;   // prefix K rows, then prefix V rows
+    const int64_t jj = isk ? j - a.jv : j - a.jp;
+    const int h = (int)(jj % a.Hkv);
+    const int r = (int)((jj / a.Hkv) % a.P);
+    const int64_t sq = jj / ((int64_t)a.Hkv * a.P);
+    const int64_t src = a.pidx != nullptr ? a.pidx[sq] : sq;
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if ((uint64_t)src < (uint64_t)a.npre)
+      x = isk ? ld16(a.pk + src * a.pk_ss + (int64_t)r * a.pk_st + (int64_t)h * a.pk_sh + c8)
+              : ld16(a.pv + src * a.pv_ss + (int64_t)r * a.pv_st + (int64_t)h * a.pv_sh + c8);
+    st16((isk ? a.ko : a.vo) + ((sq * n + r) * a.Hkv + h) * kD + c8, x);
   }
 }
 
@@ -1015,4 +1093,115 @@ extern "C" int q3a_prefill_dense_append(const void* q, int64_t q_stride_s, int64
                             v_stride_s, v_stride_t, v_stride_h, out, o_stride_s, o_stride_t, o_stride_h, num_seqs,
                             seqlen_q, seqlen_k, num_q_heads, num_kv_heads, head_dim, softmax_scale, causal, stream,
                             who);
+}
+
+// Workspace of q3a_prefill_dense_append_rope: the normalised q [S, R, Hq, D] and the dense K, V [S, P + R, Hkv, D],
+// each part 256-byte aligned.
+static size_t admit_ws_part(int64_t elems) { return (size_t)((elems * 2 + 255) / 256 * 256); }
+
+extern "C" size_t q3a_prefill_dense_append_rope_workspace_bytes(int num_seqs, int seqlen_q, int prefix_len,
+                                                                int num_q_heads, int num_kv_heads, int head_dim) {
+  if (num_seqs <= 0 || seqlen_q <= 0 || prefix_len < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+    return 0;
+  const int64_t n = (int64_t)prefix_len + seqlen_q;
+  return admit_ws_part((int64_t)num_seqs * seqlen_q * num_q_heads * head_dim) +
+         2 * admit_ws_part((int64_t)num_seqs * n * num_kv_heads * head_dim);
+}
+
+extern "C" int q3a_prefill_dense_append_rope(
+    const void* q, int64_t q_stride_s, int64_t q_stride_t, int64_t q_stride_h,
+    const void* k, int64_t k_stride_s, int64_t k_stride_t, int64_t k_stride_h,
+    const void* v, int64_t v_stride_s, int64_t v_stride_t, int64_t v_stride_h,
+    const void* prefix_k, int64_t pk_stride_s, int64_t pk_stride_t, int64_t pk_stride_h,
+    const void* prefix_v, int64_t pv_stride_s, int64_t pv_stride_t, int64_t pv_stride_h,
+    const int64_t* prefix_index, int64_t num_prefixes,
+    const void* q_norm_w, const void* k_norm_w, const void* cos, const void* sin, int64_t rope_stride_t, float eps,
+    void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head,
+    int num_pages, int page_size, const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq,
+    int first_row, void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, void* workspace,
+    size_t workspace_bytes, int num_seqs, int seqlen_q, int prefix_len, int num_q_heads, int num_kv_heads,
+    int head_dim, float softmax_scale, int causal, void* stream) {
+  const char* who = "prefill_dense_append_rope";
+  if (num_seqs < 0 || seqlen_q < 0 || prefix_len < 0)
+    return fail(Q3A_EINVAL, "%s: negative num_seqs/seqlen_q/prefix_len", who);
+  if (first_row < 0 || first_row > prefix_len)
+    return fail(Q3A_EINVAL, "%s: first_row %d must lie in [0, prefix_len = %d]", who, first_row, prefix_len);
+  if (num_seqs == 0 || seqlen_q == 0) return Q3A_OK;
+  if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
+  if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
+    return fail(Q3A_EINVAL, "%s: num_q_heads %d must be %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
+  if (!q || !k || !v || !q_norm_w || !k_norm_w || !cos || !sin || !out || !workspace ||
+      (prefix_len > 0 && (!prefix_k || !prefix_v)))
+    return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)prefix_k | (uintptr_t)prefix_v |
+                          (uintptr_t)q_norm_w | (uintptr_t)k_norm_w | (uintptr_t)cos | (uintptr_t)sin |
+                          (uintptr_t)workspace;
+  if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: tensors and the workspace must be 16-byte aligned", who);
+  if ((q_stride_s | q_stride_t | q_stride_h | k_stride_s | k_stride_t | k_stride_h | v_stride_s | v_stride_t |
+       v_stride_h | pk_stride_s | pk_stride_t | pk_stride_h | pv_stride_s | pv_stride_t | pv_stride_h | rope_stride_t) %
+          8 != 0 ||
+      q_stride_s < 0 || q_stride_t < 0 || q_stride_h < 0 || k_stride_s < 0 || k_stride_t < 0 || k_stride_h < 0 ||
+      v_stride_s < 0 || v_stride_t < 0 || v_stride_h < 0 || pk_stride_s < 0 || pk_stride_t < 0 || pk_stride_h < 0 ||
+      pv_stride_s < 0 || pv_stride_t < 0 || pv_stride_h < 0 || rope_stride_t < 0)
+    return fail(Q3A_EINVAL, "%s: strides must be non-negative multiples of 8 elements", who);
+  if (prefix_len > 0 && num_prefixes < 1) return fail(Q3A_EINVAL, "%s: num_prefixes must be >= 1", who);
+  const size_t need = q3a_prefill_dense_append_rope_workspace_bytes(num_seqs, seqlen_q, prefix_len, num_q_heads,
+                                                                    num_kv_heads, head_dim);
+  if (workspace_bytes < need)
+    return fail(Q3A_EINVAL, "%s: workspace of %zu bytes, need %zu", who, workspace_bytes, need);
+  int rc = check_pool(k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size,
+                      block_table, max_pages_per_seq, head_dim, who);
+  if (rc != Q3A_OK) return rc;
+
+  const int n = prefix_len + seqlen_q;
+  const int64_t S = num_seqs;
+  AdmitPrepArgs p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_ss = q_stride_s; p.q_st = q_stride_t; p.q_sh = q_stride_h;
+  p.k = static_cast<const uint16_t*>(k);
+  p.k_ss = k_stride_s; p.k_st = k_stride_t; p.k_sh = k_stride_h;
+  p.v = static_cast<const uint16_t*>(v);
+  p.v_ss = v_stride_s; p.v_st = v_stride_t; p.v_sh = v_stride_h;
+  p.pk = static_cast<const uint16_t*>(prefix_k);
+  p.pk_ss = pk_stride_s; p.pk_st = pk_stride_t; p.pk_sh = pk_stride_h;
+  p.pv = static_cast<const uint16_t*>(prefix_v);
+  p.pv_ss = pv_stride_s; p.pv_st = pv_stride_t; p.pv_sh = pv_stride_h;
+  p.pidx = prefix_index;
+  p.npre = prefix_index != nullptr ? num_prefixes : S;
+  p.qn = static_cast<const uint16_t*>(q_norm_w);
+  p.kn = static_cast<const uint16_t*>(k_norm_w);
+  p.cs = static_cast<const uint16_t*>(cos);
+  p.sn = static_cast<const uint16_t*>(sin);
+  p.cs_st = rope_stride_t;
+  p.eps = eps;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  p.qo = reinterpret_cast<uint16_t*>(ws);
+  p.ko = reinterpret_cast<uint16_t*>(ws + admit_ws_part(S * seqlen_q * num_q_heads * kD));
+  p.vo = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(p.ko) + admit_ws_part(S * n * num_kv_heads * kD));
+  p.R = seqlen_q;
+  p.P = prefix_len;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.jq = S * seqlen_q * num_q_heads;
+  p.jk = p.jq + S * seqlen_q * num_kv_heads;
+  p.jv = p.jk + S * seqlen_q * num_kv_heads;
+  p.jp = p.jv + S * prefix_len * num_kv_heads;
+  p.jall = p.jp + S * prefix_len * num_kv_heads;
+  // Every job block is a multiple of Hkv rows; with Hkv a multiple of 4 each wave's four rows are of one kind.
+  if (num_kv_heads % 4 != 0) return fail(Q3A_EINVAL, "%s: num_kv_heads %d must be a multiple of 4", who, num_kv_heads);
+  const int64_t waves = p.jall / 4;
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks > 0x7fffffff) return fail(Q3A_EINVAL, "%s: grid too large", who);
+  hipLaunchKernelGGL(admit_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: producer launch failed: %s", who, hipGetErrorString(e));
+
+  PrefillArgs a{};
+  set_pool(a, k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
+           bt_stride_b, max_pages_per_seq, first_row);
+  return prefill_dense_impl(a, p.qo, (int64_t)seqlen_q * num_q_heads * kD, (int64_t)num_q_heads * kD, kD, p.ko,
+                            (int64_t)n * num_kv_heads * kD, (int64_t)num_kv_heads * kD, kD, p.vo,
+                            (int64_t)n * num_kv_heads * kD, (int64_t)num_kv_heads * kD, kD, out, o_stride_s, o_stride_t,
+                            o_stride_h, num_seqs, seqlen_q, n, num_q_heads, num_kv_heads, head_dim, softmax_scale,
+                            causal, stream, who);
 }

@@ -205,6 +205,40 @@ __device__ __forceinline__ uint4 qk_norm_rope16(uint4 x, uint4 w, uint4 c, uint4
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// The same producers as eager bf16 torch ops evaluate them (engine/ops.py:51-60 outside torch.compile; the
+// admission layer runs this way by default, engine/arrivals.py:57-61): every op rounds to bf16,
+//   y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))),  o = bf16(bf16(y * cos) + bf16(rot(y) * sin)).
+// Layout and reduction tree as qk_norm_rope16.
+__device__ __forceinline__ uint4 qk_norm_rope16_eager(uint4 x, uint4 w, uint4 c, uint4 s, float eps) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ws[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t cs[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v0 = bf16_lo(xs[i]), v1 = bf16_hi(xs[i]);
+    p[i] = v0 * v0 + v1 * v1;
+  }
+  const float r = rms_rsqrt(row16_sum((p[0] + p[1]) + (p[2] + p[3])), eps);
+  const bool lo = (threadIdx.x & 8) == 0;  // dims 0..63: rot = -y[d + 64]
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float out[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float xv = e ? bf16_hi(xs[i]) : bf16_lo(xs[i]);
+      const float wv = e ? bf16_hi(ws[i]) : bf16_lo(ws[i]);
+      const float y = round_bf16(wv * round_bf16(xv * r));
+      const float yp = dpp_f32<kDppRor8>(y);
+      const float cv = e ? bf16_hi(cs[i]) : bf16_lo(cs[i]);
+      const float sv = e ? bf16_hi(ss[i]) : bf16_lo(ss[i]);
+      out[e] = round_bf16(y * cv) + round_bf16((lo ? -yp : yp) * sv);
+    }
+    o[i] = pack_bf16x2(out[0], out[1]);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // qk_norm_rope16 with the weight and cos/sin chunks read from LDS a word at a time (the lane's 16 B chunk at w, c,
 // s), for kernels whose tile pipeline leaves few registers free: same arithmetic, same bits.
 __device__ __forceinline__ uint4 qk_norm_rope16_lds(uint4 x, const uint8_t* w, const uint8_t* c, const uint8_t* s,

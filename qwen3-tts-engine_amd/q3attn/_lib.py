@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (must precede the library load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -110,6 +110,23 @@ SIGNATURES = {
         _c_vp, _c_i64, _c_i64, _c_i64,                         # v, v strides (seq, tok, head)
         _c_vp, _c_i64, _c_i64, _c_i64,                         # out, o strides (seq, tok, head)
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, seqlen_k, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
+    ]),
+    "q3a_prefill_dense_append_rope_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "q3a_prefill_dense_append_rope": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # q (raw), strides (seq, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # k (raw new keys), strides
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # v (new values), strides
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # prefix_k, strides (prefix, tok, head)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # prefix_v, strides
+        _c_vp, _c_i64,                                         # prefix_index (int64 or NULL), num_prefixes
+        _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_float,          # q/k norm weights, cos, sin, rope row stride, eps
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k_cache, v_cache, cache strides (page, tok, head)
+        _c_int, _c_int, _c_vp, _c_i64, _c_int,                 # num_pages, page_size, block_table, bt stride, max pages
+        _c_int,                                                # first_row
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # out, o strides (seq, tok, head)
+        _c_vp, _c_size,                                        # workspace, workspace bytes
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, prefix_len, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
     ]),
     "q3a_prefill_dense_append": (_c_int, [

@@ -216,6 +216,82 @@ def _prefill_dense_append_fake(q, k, v, k_cache, v_cache, block_table, softmax_s
     return q.new_empty(q.shape)
 
 
+@torch.library.custom_op("q3attn::prefill_dense_append_rope", mutates_args=("k_cache", "v_cache"))
+def prefill_dense_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, prefix_k: torch.Tensor,
+                              prefix_v: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                              cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                              block_table: torch.Tensor, softmax_scale: float,
+                              prefix_index: Optional[torch.Tensor] = None, causal: bool = True, eps: float = 1e-6,
+                              first_row: int = 0) -> torch.Tensor:
+    """The fast-admission layer's attention block (engine/arrivals.py:112-118, 144-148) in two launches: q and the
+    new k arrive raw (views of the qkv projection [S, R, ...]) and are RMS-normalised and rotated with the new tokens'
+    cos/sin rows ([R, D], or any view with R*D elements and a contiguous last dim such as [1, R, 1, D]), with the
+    rounding of eager bf16 torch ops (engine/ops.py:51-60); K = cat(prefix_k, k) and V = cat(prefix_v, v) with
+    prefix_k/prefix_v [num_prefixes, P, Hkv, D] taken at prefix_index[s] (int64 [S], as engine/arrivals.py:143 gathers
+    self.pK[l][slot]) or at s; rows first_row .. P+R-1 of K and V go into the pool through block_table [S, max_pages]
+    and the result is flash_attn_func(q, K, V, softmax_scale, causal) [S, R, Hq, D]."""
+    who = "q3attn.prefill_dense_append_rope"
+    _req(q.is_cuda, f"{who}: tensors must be on a GPU (there is no CPU path)")
+    dev = q.device
+    for name, t in (("k", k), ("v", v), ("prefix_k", prefix_k), ("prefix_v", prefix_v), ("q_norm_w", q_norm_w),
+                    ("k_norm_w", k_norm_w), ("cos", cos), ("sin", sin), ("k_cache", k_cache), ("v_cache", v_cache),
+                    ("block_table", block_table)):
+        _req(t.device == dev, f"{who}: {name} is on {t.device}, q on {dev}")
+    _req(all(t.dtype == torch.bfloat16 for t in (q, k, v, prefix_k, prefix_v, q_norm_w, k_norm_w, cos, sin, k_cache,
+                                                  v_cache)), f"{who}: all tensors but the table and index must be bfloat16")
+    _req(q.dim() == 4 and k.dim() == 4 and k.shape == v.shape and q.shape[:2] == k.shape[:2]
+         and q.shape[3] == k.shape[3], f"{who}: q [S,R,Hq,D], k/v [S,R,Hkv,D]")
+    S, R, Hq, D = q.shape
+    Hkv = k.shape[2]
+    _req(prefix_k.dim() == 4 and prefix_k.shape == prefix_v.shape and prefix_k.shape[2:] == k.shape[2:],
+         f"{who}: prefix_k/prefix_v must be [num_prefixes, P, Hkv, D]")
+    P = prefix_k.shape[1]
+    _req(all(t.stride(-1) == 1 for t in (q, k, v, prefix_k, prefix_v)), f"{who}: head_dim must be contiguous")
+    for name, w in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w)):
+        _req(tuple(w.shape) == (D,) and w.is_contiguous(), f"{who}: {name} must be a contiguous [{D}] tensor")
+    c2, s2 = cos.reshape(-1, D), sin.reshape(-1, D)
+    _req(c2.shape[0] == R and s2.shape[0] == R and c2.stride(1) == 1 and c2.stride(0) == s2.stride(0),
+         f"{who}: cos/sin must hold R = {R} rows of {D} with a contiguous last dim and a shared row stride")
+    if prefix_index is not None:
+        _req(prefix_index.device == dev and prefix_index.dtype == torch.int64 and prefix_index.shape == (S,)
+             and prefix_index.is_contiguous(), f"{who}: prefix_index must be a contiguous int64 [S] tensor")
+    else:
+        _req(prefix_k.shape[0] == S, f"{who}: without prefix_index, prefix_k needs one prefix per sequence")
+    _req(k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride()
+         and k_cache.stride(-1) == 1 and k_cache.shape[2:] == k.shape[2:],
+         f"{who}: k_cache and v_cache must be [num_pages, page, kv_heads, head_dim] with equal strides")
+    _req(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == S
+         and block_table.stride(1) == 1, f"{who}: block_table must be int32 [S, max_pages] with contiguous rows")
+    _req(0 <= first_row <= P, f"{who}: first_row {first_row} must lie in [0, prefix length {P}]")
+    out = torch.empty((S, R, Hq, D), dtype=q.dtype, device=dev)
+    if S == 0 or R == 0:
+        return out
+    L = lib()
+    ws_bytes = L.q3a_prefill_dense_append_rope_workspace_bytes(S, R, P, Hq, Hkv, D)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    num_pages, page = k_cache.shape[0], k_cache.shape[1]
+    rc = L.q3a_prefill_dense_append_rope(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        prefix_k.data_ptr(), prefix_k.stride(0), prefix_k.stride(1), prefix_k.stride(2),
+        prefix_v.data_ptr(), prefix_v.stride(0), prefix_v.stride(1), prefix_v.stride(2),
+        prefix_index.data_ptr() if prefix_index is not None else None, prefix_k.shape[0],
+        q_norm_w.data_ptr(), k_norm_w.data_ptr(), c2.data_ptr(), s2.data_ptr(), c2.stride(0), float(eps),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        num_pages, page, block_table.data_ptr(), block_table.stride(0), block_table.shape[1], int(first_row),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), ws.data_ptr(), ws_bytes,
+        S, R, P, Hq, Hkv, D, float(softmax_scale), 1 if causal else 0, torch.cuda.current_stream(dev).cuda_stream)
+    check(rc, "q3a_prefill_dense_append_rope")
+    return out
+
+
+@prefill_dense_append_rope.register_fake
+def _prefill_dense_append_rope_fake(q, k, v, prefix_k, prefix_v, q_norm_w, k_norm_w, cos, sin, k_cache, v_cache,
+                                    block_table, softmax_scale, prefix_index=None, causal=True, eps=1e-6,
+                                    first_row=0):
+    return q.new_empty(q.shape)
+
+
 def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
                     alibi_slopes=None, deterministic=False, return_attn_probs=False):
     """Drop-in for ``flash_attn.flash_attn_func`` as the fast-admission path calls it (engine/arrivals.py:148):

@@ -346,6 +346,46 @@ def test_prefill_dense_append_rejects_bad_arguments(kw, frag):
     assert frag in _lib.lib().q3a_last_error().decode()
 
 
+def _dense_rope(**kw):
+    """The admission shape (S = 8, R = 42 new tokens after a 35-token prefix), fake aligned pointers; q/k/v as views
+    of a [S, R, 4096] qkv projection."""
+    a = dict(q=16, q_ss=42 * 4096, q_st=4096, q_sh=128, k=16, k_ss=42 * 4096, k_st=4096, k_sh=128,
+             v=16, v_ss=42 * 4096, v_st=4096, v_sh=128, pk=16, pk_ss=35 * 1024, pk_st=1024, pk_sh=128,
+             pv=16, pv_ss=35 * 1024, pv_st=1024, pv_sh=128, pidx=None, npre=8, qn=16, kn=16, cos=16, sin=16,
+             rope_st=128, eps=1e-6, kc=16, vc=16, c_sp=16384, c_st=1024, c_sh=128, num_pages=64, page=16, bt=16,
+             bt_sb=8, max_pages=8, first=0, out=16, o_ss=42 * 2048, o_st=2048, o_sh=128, ws=16, ws_bytes=1 << 30,
+             S=8, R=42, P=35, Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
+    a.update(kw)
+    return _lib.lib().q3a_prefill_dense_append_rope(
+        a["q"], a["q_ss"], a["q_st"], a["q_sh"], a["k"], a["k_ss"], a["k_st"], a["k_sh"], a["v"], a["v_ss"], a["v_st"],
+        a["v_sh"], a["pk"], a["pk_ss"], a["pk_st"], a["pk_sh"], a["pv"], a["pv_ss"], a["pv_st"], a["pv_sh"], a["pidx"],
+        a["npre"], a["qn"], a["kn"], a["cos"], a["sin"], a["rope_st"], a["eps"], a["kc"], a["vc"], a["c_sp"],
+        a["c_st"], a["c_sh"], a["num_pages"], a["page"], a["bt"], a["bt_sb"], a["max_pages"], a["first"], a["out"],
+        a["o_ss"], a["o_st"], a["o_sh"], a["ws"], a["ws_bytes"], a["S"], a["R"], a["P"], a["Hq"], a["Hkv"], a["D"],
+        a["scale"], a["causal"], None)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(qn=None), "null pointer"), (dict(pk=None), "null pointer"), (dict(ws=None), "null pointer"),
+    (dict(kc=None), "null pointer"), (dict(cos=8), "aligned"), (dict(ws=8), "aligned"), (dict(q_st=4100), "strides"),
+    (dict(rope_st=-128), "strides"), (dict(first=36), "first_row"), (dict(first=-1), "first_row"),
+    (dict(ws_bytes=1024), "workspace"), (dict(D=64), "head_dim"), (dict(Hq=12), "num_q_heads"),
+    (dict(Hq=12, Hkv=6), "multiple of 4"), (dict(npre=0), "num_prefixes"), (dict(page=48), "power of two"),
+    (dict(P=-1), "negative"),
+])
+def test_prefill_dense_append_rope_rejects_bad_arguments(kw, frag):
+    assert _dense_rope(**kw) < 0
+    assert frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_prefill_dense_append_rope_workspace_and_noop():
+    L = _lib.lib()
+    # q [8, 42, 16, 128] + K and V [8, 77, 8, 128] in bf16, each part rounded up to 256 B
+    assert L.q3a_prefill_dense_append_rope_workspace_bytes(8, 42, 35, 16, 8, 128) == 8 * 42 * 16 * 256 + 2 * 8 * 77 * 8 * 256
+    assert L.q3a_prefill_dense_append_rope_workspace_bytes(0, 42, 35, 16, 8, 128) == 0
+    assert _dense_rope(S=0) == 0 and _dense_rope(R=0) == 0
+
+
 def test_prefill_dense_append_empty_is_a_noop():
     """Nothing to compute or write: no device pointer is touched (these are fake addresses)."""
     assert _prefill_dense_append(S=0) == 0 and _prefill_dense_append(R=0, first=0) == 0

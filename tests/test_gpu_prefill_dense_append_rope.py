@@ -1,0 +1,201 @@
+"""GPU parity of the fast-admission layer's attention block in one call (q3a_prefill_dense_append_rope).
+
+engine/arrivals.py:112-118 normalises and rotates q and the new keys (engine/ops.py:51-60, eager bf16 ops by default:
+the admission layer is not compiled, engine/arrivals.py:57-61), concatenates the registered voice's prefix K/V
+before the new rows, scatters every K/V row into the seat's cache (:144-145) and attends (:148).  Against that:
+  * the output is within the bar of the oracle attention (engine/arrivals.py:125-131) over the oracle's producers,
+    which restate engine/ops.py:51-60 with the eager rounding points (every op rounds to bf16);
+  * the pool holds the prefix rows and the new V rows bit for bit, and the new K rows as the oracle's producers
+    give them up to the last bf16 bit of a rare row (the mean of squares is summed in another order);
+  * positions outside first_row .. n-1 of the NaN-filled pool stay NaN;
+  * against the same producers as eager torch ops on the GPU followed by prefill_dense_append, outputs and pools
+    agree to the same last-bit allowance.
+Shapes with n <= 128 keys take the short-key attention kernel, longer ones the tiled kernel."""
+import numpy as np
+import pytest
+import torch
+
+import q3attn
+from helpers import to_np
+from oracle import attention as ora
+from q3attn import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def _eager_norm_rope_np(x, w, cos, sin, eps=1e-6):
+    """engine/ops.py:51-60 as eager bf16 ops: y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), then
+    bf16(bf16(y * cos) + bf16(rot(y) * sin)) with rot(y) = cat(-y[64:], y[:64])."""
+    y = ora.bf16_round(w * ora.rms(x, None, eps, to_bf16=True))
+    rot = np.concatenate([-y[..., D // 2:], y[..., : D // 2]], axis=-1)
+    return ora.bf16_round(ora.bf16_round(y * cos) + ora.bf16_round(rot * sin))
+
+
+def _eager_norm_rope_torch(x, w, cos, sin, eps=1e-6):
+    """The same producers as the engine runs them: torch bf16 ops (engine/ops.py:51-60)."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    y = w * xf.to(x.dtype)
+    return y * cos + torch.cat((-y[..., D // 2:], y[..., : D // 2]), dim=-1) * sin
+
+
+def _inputs(dev, S, R, P, n_prefixes, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    qkv = torch.randn((S, R, 4096), generator=g, device=dev).to(torch.bfloat16)
+    pre = W.make_admit(dev, n_prefixes, 1, P, seed=seed + 1) if P > 0 else None
+    pk = pre.k if pre is not None else torch.zeros(n_prefixes, 0, 8, D, dtype=torch.bfloat16, device=dev)
+    pv = pre.v if pre is not None else torch.zeros_like(pk)
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    cos, sin = W.rope_tables(P + R, dev)
+    return qkv, pk, pv, qn, kn, cos[P:].to(torch.bfloat16).contiguous(), sin[P:].to(torch.bfloat16).contiguous()
+
+
+def _views(qkv):
+    S, R = qkv.shape[:2]
+    return (qkv[..., :2048].view(S, R, 16, D), qkv[..., 2048:3072].view(S, R, 8, D), qkv[..., 3072:].view(S, R, 8, D))
+
+
+def _table(S, P, num_pages, seed):
+    return np.random.default_rng(seed).permutation(num_pages)[: S * P].reshape(S, P).astype(np.int32)
+
+
+def _pool_rows(cache, bt, n, page):
+    """[S, n, Hkv, D] rows 0..n-1 of every sequence read back through its table."""
+    S = bt.shape[0]
+    j = np.arange(n)
+    return cache[bt[:, j // page], j % page]
+
+
+def _assert_last_bit(a, b, what, frac=2e-3):
+    """Equal except for rare elements a bf16 step or two apart: the mean of squares summed in another order can move
+    one normalised value by one bf16 step, and the rope's sum can then land a step or two away (more where its two
+    products cancel, so the bound is relative to the normalised rows' unit scale as well)."""
+    diff = np.abs(a.astype(np.float32) - b.astype(np.float32))
+    bad = diff > 0
+    tol = np.maximum(np.abs(b).astype(np.float32), 0.5) * 2.0 ** -6
+    assert (diff <= tol).all(), f"{what}: a difference beyond two bf16 steps ({diff.max():.3e})"
+    assert bad.mean() <= frac, f"{what}: {bad.mean():.2e} of the elements differ"
+    print(f"[parity] {what}: {int(bad.sum())} of {bad.size} elements one bf16 step apart", flush=True)
+
+
+@pytest.mark.parametrize("S,R,P,page,first,indexed", [
+    (8, 42, 35, 16, 0, True),       # the admission shape: 8 seats, 42 new tokens after a 35-token voice prefix
+    (8, 42, 35, 16, 35, True),      # prefix already in the pool: the new rows only
+    (4, 42, 35, 256, 0, False),     # the reference's 256-token pages, one prefix per sequence
+    (3, 20, 0, 16, 0, False),       # no prefix
+    (2, 100, 200, 16, 0, True),     # 300 keys: the tiled attention kernel
+    (2, 40, 660, 32, 600, True),    # tiled, part of a long prefix
+])
+def test_dense_append_rope_matches_oracle(cuda_device, S, R, P, page, first, indexed):
+    dev = cuda_device
+    n = P + R
+    nvoices = 3 if indexed else S
+    qkv, pk, pv, qn, kn, cos, sin = _inputs(dev, S, R, P, nvoices, seed=40 + n)
+    q, k, v = _views(qkv)
+    pidx = torch.tensor([(2 * s + 1) % nvoices for s in range(S)], dtype=torch.int64, device=dev) if indexed else None
+    Pn = -(-n // page)
+    num_pages = max(2 * S * Pn, 64)
+    bt = _table(S, Pn, num_pages, seed=41)
+    kc = torch.full((num_pages, page, 8, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, float("nan"))
+    scale = D ** -0.5
+    print(f"[case] prefill_dense_append_rope S={S} R={R} P={P} page={page} first={first} indexed={indexed}",
+          flush=True)
+    out = q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, kc, vc,
+                                           torch.from_numpy(bt).to(dev), scale, pidx, True, 1e-6, first)
+    torch.cuda.synchronize()
+    # the oracle's producers and attention
+    sel = pidx.cpu().numpy() if indexed else np.arange(S)
+    cn, sn = to_np(cos)[None, :, None], to_np(sin)[None, :, None]
+    q_o = _eager_norm_rope_np(to_np(q), to_np(qn), cn, sn)
+    k_o = _eager_norm_rope_np(to_np(k), to_np(kn), cn, sn)
+    K = np.concatenate([to_np(pk)[sel], k_o], axis=1)
+    V = np.concatenate([to_np(pv)[sel], to_np(v)], axis=1)
+    ok, st = ora.compare(to_np(out), ora.prefill_prefix(q_o, K, V, scale))
+    print(f"[parity] prefill_dense_append_rope S={S} R={R} P={P} vs oracle {st}", flush=True)
+    assert ok, st
+    # the pool: rows first..n-1 as the producers give them, every other slot still NaN
+    kp, vp = _pool_rows(to_np(kc), bt, n, page), _pool_rows(to_np(vc), bt, n, page)
+    assert np.isnan(kp[:, :first]).all() and np.isnan(vp[:, :first]).all()
+    assert np.array_equal(kp[:, first:P], K[:, first:P]) and np.array_equal(vp[:, first:], V[:, first:])
+    _assert_last_bit(kp[:, max(first, P):], k_o, "pool new K rows vs oracle producers")
+    written = np.zeros(kc.shape[:2], dtype=bool)
+    j = np.arange(first, n)
+    written[bt[:, j // page], j % page] = True
+    assert torch.isnan(kc[torch.from_numpy(~written).to(dev)]).all()
+    assert torch.isnan(vc[torch.from_numpy(~written).to(dev)]).all()
+
+
+@pytest.mark.parametrize("P", [35, 200])
+def test_dense_append_rope_matches_torch_producers(cuda_device, P):
+    """The engine's own sequence on the GPU: eager torch producers, torch.cat, then prefill_dense_append (the fused
+    scatters + attention); the one-call form agrees up to rare last-bit differences of the normalised rows."""
+    dev = cuda_device
+    S, R = 8, 42
+    n = P + R
+    qkv, pk, pv, qn, kn, cos, sin = _inputs(dev, S, R, P, S, seed=43)
+    q, k, v = _views(qkv)
+    Pn = -(-n // 16)
+    bt = torch.from_numpy(_table(S, Pn, 256, seed=44)).to(dev)
+    pools = [torch.zeros(256, 16, 8, D, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    scale = D ** -0.5
+    out = q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, pools[0], pools[1], bt, scale)
+    c4, s4 = cos[None, :, None], sin[None, :, None]
+    qe = _eager_norm_rope_torch(q, qn, c4, s4)
+    K = torch.cat((pk, _eager_norm_rope_torch(k, kn, c4, s4)), 1)
+    V = torch.cat((pv, v), 1)
+    ref = q3attn.prefill_dense_append(qe, K, V, pools[2], pools[3], bt, scale, True, 0)
+    torch.cuda.synchronize()
+    _assert_last_bit(to_np(pools[0]), to_np(pools[2]), f"pool K, P={P}")
+    assert torch.equal(pools[1], pools[3])
+    ok, st = ora.compare(to_np(out), to_np(ref), max_abs=1e-2, mean_abs=2e-4)
+    print(f"[parity] rope form vs torch producers + dense append, P={P}: {st}", flush=True)
+    assert ok, st
+
+
+def test_dense_append_rope_invalid_prefix_index_reads_zeros(cuda_device):
+    """A prefix index outside [0, num_prefixes) contributes zero rows (no fault), like an empty voice."""
+    dev = cuda_device
+    S, R, P = 2, 42, 35
+    qkv, pk, pv, qn, kn, cos, sin = _inputs(dev, S, R, P, 2, seed=45)
+    q, k, v = _views(qkv)
+    pidx = torch.tensor([1, 7], dtype=torch.int64, device=dev)
+    bt = torch.from_numpy(_table(S, 5, 64, seed=46)).to(dev)
+    kc = torch.full((64, 16, 8, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, float("nan"))
+    q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, kc, vc, bt, D ** -0.5, pidx)
+    torch.cuda.synchronize()
+    kp = _pool_rows(to_np(kc), bt.cpu().numpy(), P + R, 16)
+    assert np.array_equal(kp[0, :P], to_np(pk)[1]) and not np.abs(kp[1, :P]).any()
+
+
+def test_dense_append_rope_in_graph_replays(cuda_device):
+    dev = cuda_device
+    S, R, P = 8, 42, 35
+    qkv, pk, pv, qn, kn, cos, sin = _inputs(dev, S, R, P, 4, seed=47)
+    q, k, v = _views(qkv)
+    pidx = torch.tensor([s % 4 for s in range(S)], dtype=torch.int64, device=dev)
+    bt = torch.from_numpy(_table(S, 5, 128, seed=48)).to(dev)
+    kc = torch.zeros(128, 16, 8, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    eager = q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, kc, vc, bt, D ** -0.5, pidx)
+    torch.cuda.synchronize()
+    k_ref, v_ref = kc.clone(), vc.clone()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        static = q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, kc, vc, bt, D ** -0.5, pidx)
+    for _ in range(3):
+        kc.fill_(float("nan"))
+        vc.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static, eager)
+        assert torch.equal(torch.nan_to_num(kc), torch.nan_to_num(k_ref))
+        assert torch.equal(torch.nan_to_num(vc), torch.nan_to_num(v_ref))
