@@ -615,14 +615,62 @@ def bench_prefill_append(args, dev, wls):
         return [q3attn.prefill_append(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len, wl.k_cache,
                                       wl.v_cache, wl.block_table, wl.scale, True) for wl, _ in steps]
 
+    # The prompt step with its q/k producers (engine/talker.py:157-169): rope(rms(...)) of q and k as the eager bf16
+    # torch ops prefill_hidden runs, the scatters and the attention, against prefill_append_rope.  Synthetic qkv
+    # projections and norm weights per layer; cos/sin gathered per token as engine/talker.py:154 does.
+    from q3attn.workloads import rope_tables
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 78)
+    wl0 = steps[0][0]
+    T = int(wl0.lens.sum())
+    pos = torch.cat([torch.arange(int(L), device=dev) for L in wl0.lens])
+    cos, sin = rope_tables(int(wl0.lens.max()), dev)
+    cos_t, sin_t = cos.to(torch.bfloat16)[pos][:, None, :], sin.to(torch.bfloat16)[pos][:, None, :]
+    blocks = []
+    for wl, slot in steps:
+        qkv = torch.randn((T, 4096), generator=gen, device=dev).to(torch.bfloat16)
+        qn = (1.0 + 0.1 * torch.randn(128, generator=gen, device=dev)).to(torch.bfloat16)
+        kn = (1.0 + 0.1 * torch.randn(128, generator=gen, device=dev)).to(torch.bfloat16)
+        blocks.append((wl, slot, qkv, qn, kn))
+
+    def rms_t(x, w, eps=1e-6):
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+        return w * xf.to(x.dtype)
+
+    def rope_t(x, c, s_):
+        return x * c + torch.cat((-x[..., 64:], x[..., :64]), dim=-1) * s_
+
+    def engine_step():
+        out = []
+        for wl, slot, qkv, qn, kn in blocks:
+            q = rope_t(rms_t(qkv[:, :2048].view(T, 16, 128), qn), cos_t, sin_t)
+            k = rope_t(rms_t(qkv[:, 2048:3072].view(T, 8, 128), kn), cos_t, sin_t)
+            v = qkv[:, 3072:].view(T, 8, 128)
+            wl.k_cache.view(-1, 8, 128).index_copy_(0, slot, k)
+            wl.v_cache.view(-1, 8, 128).index_copy_(0, slot, v)
+            out.append(q3attn.flash_attn_varlen_func(q, k, v, wl.cu_seqlens, wl.cu_seqlens, wl.max_len, wl.max_len,
+                                                     softmax_scale=wl.scale, causal=True))
+        return out
+
+    def fused_rope():
+        return [q3attn.prefill_append_rope(qkv[:, :2048].view(T, 16, 128), qkv[:, 2048:3072].view(T, 8, 128),
+                                           qkv[:, 3072:].view(T, 8, 128), qn, kn, cos_t, sin_t, wl.cu_seqlens,
+                                           wl.max_len, wl.k_cache, wl.v_cache, wl.block_table, wl.scale)
+                for wl, _, qkv, qn, kn in blocks]
+
     res = {}
     for name, fn in (("packed_prefill", packed), ("index_copy_then_prefill", scatter_then_prefill),
-                     ("prefill_append", fused)):
+                     ("prefill_append", fused), ("torch_producers_index_copy_then_prefill", engine_step),
+                     ("prefill_append_rope", fused_rope)):
         _, fr, _ = time_graph(dev, fn, args.steps, args.warmup, getattr(args, "min_warm_s", 0.0))
         res[name + "_us_per_layer_call"] = round(statistics.mean(fr) * 1e3 / LAYERS, 2)
     log(f"[bench] prompt step: prefill_append {res['prefill_append_us_per_layer_call']:.1f} us/layer call; "
         f"index_copy_ x2 + prefill {res['index_copy_then_prefill_us_per_layer_call']:.1f}; packed prefill alone "
         f"{res['packed_prefill_us_per_layer_call']:.1f}")
+    log(f"[bench] prompt step with the q/k producers: prefill_append_rope "
+        f"{res['prefill_append_rope_us_per_layer_call']:.1f} us/layer call; eager torch producers + index_copy_ x2 + "
+        f"prefill {res['torch_producers_index_copy_then_prefill_us_per_layer_call']:.1f}")
     return res
 
 

@@ -27,7 +27,7 @@ extern "C" {
 
 /* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
  * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope.
- * 5: q3a_prefill_dense_append.  6: q3a_prefill_dense_append_rope. */
+ * 5: q3a_prefill_dense_append.  6: q3a_prefill_dense_append_rope, q3a_prefill_append_rope. */
 #define Q3A_ABI_VERSION 6
 int q3a_abi_version(void);
 
@@ -319,6 +319,30 @@ int q3a_prefill_dense_append_rope(
     int first_row, void* out, int64_t o_stride_s, int64_t o_stride_t, int64_t o_stride_h, void* workspace,
     size_t workspace_bytes, int num_seqs, int seqlen_q, int prefix_len, int num_q_heads, int num_kv_heads,
     int head_dim, float softmax_scale, int causal, void* stream);
+
+/*
+ * The talker's prompt step with its q/k producers, in two launches (engine/talker.py:157-169): q = rope(rms(q_raw,
+ * q_norm_w)) and k = rope(rms(k_raw, k_norm_w)) of every prompt token with the token's own cos/sin row (engine/ops.py:
+ * 51-60 as eager bf16 ops: prefill_hidden is not compiled), the index_copy_ pair into the pool (:161-162) and
+ * flash_attn_varlen_func(q, k, v, cu, cu, ...) (:169).  The first launch writes the normalised q and k into the
+ * workspace, the second is q3a_prefill_append on them and on v where it is (cu_seqlens for both q and k).
+ *
+ *   q          [T, Hq, D] bf16 raw projections of the T = total_tokens packed prompt tokens (q_stride_t/h)
+ *   k, v       [T, Hkv, D] bf16 raw keys and the values (their own strides)
+ *   cos, sin   [T, D] bf16: token t's rows at its position in its sequence (row stride rope_stride_t)
+ *   cu_seqlens [num_seqs + 1] int32;  pool, table, out: as q3a_prefill_append
+ *   workspace  q3a_prefill_append_rope_workspace_bytes(T, Hq, Hkv, D) bytes, 16-byte aligned
+ * Requirements as q3a_prefill_dense_append_rope.
+ */
+size_t q3a_prefill_append_rope_workspace_bytes(int total_tokens, int num_q_heads, int num_kv_heads, int head_dim);
+int q3a_prefill_append_rope(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k, int64_t k_stride_t, int64_t k_stride_h,
+    const void* v, int64_t v_stride_t, int64_t v_stride_h, const void* q_norm_w, const void* k_norm_w,
+    const void* cos, const void* sin, int64_t rope_stride_t, float eps, const int32_t* cu_seqlens, void* k_cache,
+    void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head, int num_pages,
+    int page_size, const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq, void* out,
+    int64_t o_stride_t, int64_t o_stride_h, void* workspace, size_t workspace_bytes, int num_seqs, int total_tokens,
+    int max_seqlen, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1095,6 +1095,20 @@ extern "C" int q3a_prefill_dense_append(const void* q, int64_t q_stride_s, int64
                             who);
 }
 
+// The producer launch shared by the rope entry points (the job block ends in p must be set).
+static int launch_prep(const AdmitPrepArgs& p, void* stream, const char* who) {
+  // Every job block is a multiple of Hkv rows; with Hkv a multiple of 4 each wave's four rows are of one kind.
+  if (p.Hkv % 4 != 0) return fail(Q3A_EINVAL, "%s: num_kv_heads %d must be a multiple of 4", who, p.Hkv);
+  const int64_t waves = p.jall / 4;
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks > 0x7fffffff) return fail(Q3A_EINVAL, "%s: grid too large", who);
+  if (blocks == 0) return Q3A_OK;
+  hipLaunchKernelGGL(admit_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: producer launch failed: %s", who, hipGetErrorString(e));
+  return Q3A_OK;
+}
+
 // Workspace of q3a_prefill_dense_append_rope: the normalised q [S, R, Hq, D] and the dense K, V [S, P + R, Hkv, D],
 // each part 256-byte aligned.
 static size_t admit_ws_part(int64_t elems) { return (size_t)((elems * 2 + 255) / 256 * 256); }
@@ -1187,14 +1201,8 @@ extern "C" int q3a_prefill_dense_append_rope(
   p.jv = p.jk + S * seqlen_q * num_kv_heads;
   p.jp = p.jv + S * prefix_len * num_kv_heads;
   p.jall = p.jp + S * prefix_len * num_kv_heads;
-  // Every job block is a multiple of Hkv rows; with Hkv a multiple of 4 each wave's four rows are of one kind.
-  if (num_kv_heads % 4 != 0) return fail(Q3A_EINVAL, "%s: num_kv_heads %d must be a multiple of 4", who, num_kv_heads);
-  const int64_t waves = p.jall / 4;
-  const int64_t blocks = (waves + 3) / 4;
-  if (blocks > 0x7fffffff) return fail(Q3A_EINVAL, "%s: grid too large", who);
-  hipLaunchKernelGGL(admit_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: producer launch failed: %s", who, hipGetErrorString(e));
+  rc = launch_prep(p, stream, who);
+  if (rc != Q3A_OK) return rc;
 
   PrefillArgs a{};
   set_pool(a, k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
@@ -1204,4 +1212,81 @@ extern "C" int q3a_prefill_dense_append_rope(
                             (int64_t)n * num_kv_heads * kD, (int64_t)num_kv_heads * kD, kD, out, o_stride_s, o_stride_t,
                             o_stride_h, num_seqs, seqlen_q, n, num_q_heads, num_kv_heads, head_dim, softmax_scale,
                             causal, stream, who);
+}
+
+// Workspace of q3a_prefill_append_rope: the normalised q [T, Hq, D] and k [T, Hkv, D] (v is read where it is).
+extern "C" size_t q3a_prefill_append_rope_workspace_bytes(int total_tokens, int num_q_heads, int num_kv_heads,
+                                                          int head_dim) {
+  if (total_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+  return admit_ws_part((int64_t)total_tokens * num_q_heads * head_dim) +
+         admit_ws_part((int64_t)total_tokens * num_kv_heads * head_dim);
+}
+
+extern "C" int q3a_prefill_append_rope(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k, int64_t k_stride_t, int64_t k_stride_h,
+    const void* v, int64_t v_stride_t, int64_t v_stride_h, const void* q_norm_w, const void* k_norm_w,
+    const void* cos, const void* sin, int64_t rope_stride_t, float eps, const int32_t* cu_seqlens, void* k_cache,
+    void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok, int64_t kv_stride_head, int num_pages,
+    int page_size, const int32_t* block_table, int64_t bt_stride_b, int max_pages_per_seq, void* out,
+    int64_t o_stride_t, int64_t o_stride_h, void* workspace, size_t workspace_bytes, int num_seqs, int total_tokens,
+    int max_seqlen, int num_q_heads, int num_kv_heads, int head_dim, float softmax_scale, int causal, void* stream) {
+  const char* who = "prefill_append_rope";
+  if (num_seqs < 0 || total_tokens < 0 || max_seqlen < 0)
+    return fail(Q3A_EINVAL, "%s: negative num_seqs/total_tokens/max_seqlen", who);
+  if (num_seqs == 0 || total_tokens == 0 || max_seqlen == 0) return Q3A_OK;
+  if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
+  if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
+    return fail(Q3A_EINVAL, "%s: num_q_heads %d must be %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
+  if (!q || !k || !v || !q_norm_w || !k_norm_w || !cos || !sin || !cu_seqlens || !out || !workspace)
+    return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)q_norm_w | (uintptr_t)k_norm_w |
+                          (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)workspace;
+  if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: tensors and the workspace must be 16-byte aligned", who);
+  if ((q_stride_t | q_stride_h | k_stride_t | k_stride_h | v_stride_t | v_stride_h | rope_stride_t) % 8 != 0 ||
+      q_stride_t < 0 || q_stride_h < 0 || k_stride_t < 0 || k_stride_h < 0 || v_stride_t < 0 || v_stride_h < 0 ||
+      rope_stride_t < 0)
+    return fail(Q3A_EINVAL, "%s: strides must be non-negative multiples of 8 elements", who);
+  const size_t need = q3a_prefill_append_rope_workspace_bytes(total_tokens, num_q_heads, num_kv_heads, head_dim);
+  if (workspace_bytes < need)
+    return fail(Q3A_EINVAL, "%s: workspace of %zu bytes, need %zu", who, workspace_bytes, need);
+  int rc = check_pool(k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size,
+                      block_table, max_pages_per_seq, head_dim, who);
+  if (rc != Q3A_OK) return rc;
+
+  // The producers over all T tokens as one sequence with no prefix: token t takes rope row t; no V rows (the
+  // attention reads v where it is).
+  const int64_t T = total_tokens;
+  AdmitPrepArgs p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_st = q_stride_t; p.q_sh = q_stride_h;
+  p.k = static_cast<const uint16_t*>(k);
+  p.k_st = k_stride_t; p.k_sh = k_stride_h;
+  p.v = static_cast<const uint16_t*>(v);
+  p.v_st = v_stride_t; p.v_sh = v_stride_h;
+  p.qn = static_cast<const uint16_t*>(q_norm_w);
+  p.kn = static_cast<const uint16_t*>(k_norm_w);
+  p.cs = static_cast<const uint16_t*>(cos);
+  p.sn = static_cast<const uint16_t*>(sin);
+  p.cs_st = rope_stride_t;
+  p.eps = eps;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  p.qo = reinterpret_cast<uint16_t*>(ws);
+  p.ko = reinterpret_cast<uint16_t*>(ws + admit_ws_part(T * num_q_heads * kD));
+  p.vo = nullptr;
+  p.R = total_tokens;
+  p.P = 0;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.jq = T * num_q_heads;
+  p.jk = p.jq + T * num_kv_heads;
+  p.jv = p.jk;
+  p.jp = p.jv;
+  p.jall = p.jv;
+  rc = launch_prep(p, stream, who);
+  if (rc != Q3A_OK) return rc;
+  return q3a_prefill_append(p.qo, (int64_t)num_q_heads * kD, kD, cu_seqlens, p.ko, (int64_t)num_kv_heads * kD, kD,
+                            v, v_stride_t, v_stride_h, cu_seqlens, k_cache, v_cache, kv_stride_page,
+                            kv_stride_tok, kv_stride_head, num_pages, page_size, block_table, bt_stride_b,
+                            max_pages_per_seq, out, o_stride_t, o_stride_h, num_seqs, max_seqlen, num_q_heads,
+                            num_kv_heads, head_dim, softmax_scale, causal, stream);
 }

@@ -8,6 +8,7 @@ Entry points (each a drop-in for the reference call it names):
                                                        slot write fused: engine/code_predictor.py:58)
   * ``flash_attn_varlen_func`` / ``flash_attn_func``  -- prefill (engine/talker.py:169, engine/arrivals.py:148)
   * ``prefill_append``                               -- prompt K/V into the pool + prefill (engine/talker.py:161-169)
+  * ``prefill_append_rope``                          -- + the prompt's q/k norm and RoPE (engine/talker.py:157-169)
   * ``prefill_dense_append``                         -- admission K/V into the pool + prefill (engine/arrivals.py:144-148)
   * ``prefill_dense_append_rope``                    -- + the admission q/k norm, RoPE and K/V concat (engine/arrivals.py:112-118)
   * ``PagePool``                                     -- 16-token pages per seat from a free list, device block table
@@ -19,4 +20,4 @@ from .cp_attn import cp_attn, cp_attn_append, cp_attn_append_op, cp_attn_op  # n
 from .ops import flash_attn_with_kvcache, paged_decode, paged_decode_append, paged_decode_append_rope  # noqa: F401
 from .pages import PagePool, PoolExhausted  # noqa: F401
 from .prefill import (flash_attn_func, flash_attn_varlen_func, prefill, prefill_append, prefill_dense,  # noqa: F401
-                      prefill_dense_append, prefill_dense_append_rope)
+                      prefill_append_rope, prefill_dense_append, prefill_dense_append_rope)

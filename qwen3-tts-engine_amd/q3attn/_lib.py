@@ -129,6 +129,19 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, prefix_len, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
     ]),
+    "q3a_prefill_append_rope_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "q3a_prefill_append_rope": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,          # q (raw), strides (tok, head), k (raw), strides
+        _c_vp, _c_i64, _c_i64,                                 # v, strides
+        _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_float,          # q/k norm weights, cos, sin, rope row stride, eps
+        _c_vp,                                                 # cu_seqlens
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,                  # k_cache, v_cache, cache strides (page, tok, head)
+        _c_int, _c_int, _c_vp, _c_i64, _c_int,                 # num_pages, page_size, block_table, bt stride, max pages
+        _c_vp, _c_i64, _c_i64,                                 # out, o_stride_t, o_stride_h
+        _c_vp, _c_size,                                        # workspace, workspace bytes
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, total_tokens, max_seqlen, Hq, Hkv, D
+        _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
+    ]),
     "q3a_prefill_dense_append": (_c_int, [
         _c_vp, _c_i64, _c_i64, _c_i64,                         # q, q strides (seq, tok, head)
         _c_vp, _c_i64, _c_i64, _c_i64,                         # k, k strides (seq, tok, head)

@@ -216,6 +216,67 @@ def _prefill_dense_append_fake(q, k, v, k_cache, v_cache, block_table, softmax_s
     return q.new_empty(q.shape)
 
 
+@torch.library.custom_op("q3attn::prefill_append_rope", mutates_args=("k_cache", "v_cache"))
+def prefill_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
+                        k_norm_w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, cu_seqlens: torch.Tensor,
+                        max_seqlen: int, k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
+                        softmax_scale: float, causal: bool = True, eps: float = 1e-6) -> torch.Tensor:
+    """The talker's prompt step with its producers (engine/talker.py:157-169) in two launches: q [T, Hq, D] and k
+    [T, Hkv, D] arrive raw (views of the qkv projection), are RMS-normalised and rotated with each token's cos/sin row
+    ([T, D], or [T, 1, D] as the engine gathers them) with the rounding of eager bf16 ops (engine/ops.py:51-60), k and
+    v go into the pool at each token's position through block_table [n, max_pages], and the result is
+    flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, ...) over the normalised q and k [T, Hq, D]."""
+    who = "q3attn.prefill_append_rope"
+    _req(q.is_cuda, f"{who}: tensors must be on a GPU (there is no CPU path)")
+    dev = q.device
+    for name, t in (("k", k), ("v", v), ("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w), ("cos", cos), ("sin", sin),
+                    ("cu_seqlens", cu_seqlens), ("k_cache", k_cache), ("v_cache", v_cache),
+                    ("block_table", block_table)):
+        _req(t.device == dev, f"{who}: {name} is on {t.device}, q on {dev}")
+    _req(all(t.dtype == torch.bfloat16 for t in (q, k, v, q_norm_w, k_norm_w, cos, sin, k_cache, v_cache)),
+         f"{who}: q, k, v, the weights, cos/sin and the caches must be bfloat16")
+    _req(q.dim() == 3 and k.dim() == 3 and k.shape == v.shape and q.shape[0] == k.shape[0] and q.shape[2] == k.shape[2],
+         f"{who}: q [T, Hq, D], k/v [T, Hkv, D]")
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    _req(all(t.stride(-1) == 1 for t in (q, k, v)), f"{who}: head_dim must be contiguous")
+    for name, w in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w)):
+        _req(tuple(w.shape) == (D,) and w.is_contiguous(), f"{who}: {name} must be a contiguous [{D}] tensor")
+    c2, s2 = cos.reshape(-1, D), sin.reshape(-1, D)
+    _req(c2.shape[0] == T and s2.shape[0] == T and c2.stride(1) == 1 and c2.stride(0) == s2.stride(0),
+         f"{who}: cos/sin must hold T = {T} rows of {D} with a contiguous last dim and a shared row stride")
+    _req(cu_seqlens.dtype == torch.int32 and cu_seqlens.dim() == 1 and cu_seqlens.is_contiguous(),
+         f"{who}: cu_seqlens must be contiguous int32 [n+1]")
+    n = cu_seqlens.shape[0] - 1
+    _req(k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride()
+         and k_cache.stride(-1) == 1 and k_cache.shape[2:] == k.shape[1:],
+         f"{who}: k_cache and v_cache must be [num_pages, page, kv_heads, head_dim] with equal strides")
+    _req(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == max(n, 0)
+         and block_table.stride(1) == 1, f"{who}: block_table must be int32 [n, max_pages] with contiguous rows")
+    out = torch.empty((T, Hq, D), dtype=q.dtype, device=dev)
+    if n <= 0 or T == 0:
+        return out.zero_() if T else out
+    L = lib()
+    ws_bytes = L.q3a_prefill_append_rope_workspace_bytes(T, Hq, Hkv, D)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    num_pages, page = k_cache.shape[0], k_cache.shape[1]
+    rc = L.q3a_prefill_append_rope(
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+        v.stride(1), q_norm_w.data_ptr(), k_norm_w.data_ptr(), c2.data_ptr(), s2.data_ptr(), c2.stride(0), float(eps),
+        cu_seqlens.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+        k_cache.stride(2), num_pages, page, block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws_bytes, n, T, int(max_seqlen), Hq, Hkv, D,
+        float(softmax_scale), 1 if causal else 0, torch.cuda.current_stream(dev).cuda_stream)
+    check(rc, "q3a_prefill_append_rope")
+    return out
+
+
+@prefill_append_rope.register_fake
+def _prefill_append_rope_fake(q, k, v, q_norm_w, k_norm_w, cos, sin, cu_seqlens, max_seqlen, k_cache, v_cache,
+                              block_table, softmax_scale, causal=True, eps=1e-6):
+    return torch.empty_like(q, memory_format=torch.contiguous_format)
+
+
 @torch.library.custom_op("q3attn::prefill_dense_append_rope", mutates_args=("k_cache", "v_cache"))
 def prefill_dense_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, prefix_k: torch.Tensor,
                               prefix_v: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,

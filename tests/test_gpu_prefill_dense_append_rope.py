@@ -1,4 +1,5 @@
-"""GPU parity of the fast-admission layer's attention block in one call (q3a_prefill_dense_append_rope).
+"""GPU parity of the attention blocks with their q/k producers in one call: the fast-admission layer
+(q3a_prefill_dense_append_rope) and, at the end of the file, the talker's prompt step (q3a_prefill_append_rope).
 
 engine/arrivals.py:112-118 normalises and rotates q and the new keys (engine/ops.py:51-60, eager bf16 ops by default:
 the admission layer is not compiled, engine/arrivals.py:57-61), concatenates the registered voice's prefix K/V
@@ -190,6 +191,110 @@ def test_dense_append_rope_in_graph_replays(cuda_device):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         static = q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, kc, vc, bt, D ** -0.5, pidx)
+    for _ in range(3):
+        kc.fill_(float("nan"))
+        vc.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static, eager)
+        assert torch.equal(torch.nan_to_num(kc), torch.nan_to_num(k_ref))
+        assert torch.equal(torch.nan_to_num(vc), torch.nan_to_num(v_ref))
+
+
+# ------------------------------------------------------------------ the talker's prompt step (engine/talker.py:157-169)
+def _prompt_inputs(dev, lens, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    T = int(lens.sum())
+    qkv = torch.randn((T, 4096), generator=g, device=dev).to(torch.bfloat16)
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    pos = torch.cat([torch.arange(int(L), device=dev) for L in lens])
+    cos, sin = W.rope_tables(int(lens.max()), dev)
+    # gathered per token as engine/talker.py:154 does: [T, 1, D]
+    cos_t, sin_t = cos.to(torch.bfloat16)[pos][:, None, :], sin.to(torch.bfloat16)[pos][:, None, :]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=dev)
+    q, k, v = qkv[:, :2048].view(T, 16, D), qkv[:, 2048:3072].view(T, 8, D), qkv[:, 3072:].view(T, 8, D)
+    return q, k, v, qn, kn, cos_t, sin_t, cu
+
+
+@pytest.mark.parametrize("lens", [[1, 7, 16, 33, 150, 400], "prefill32", [300, 5]])
+def test_prompt_step_rope_matches_oracle(cuda_device, lens):
+    dev = cuda_device
+    lens = W.prefill_lengths("prefill32") if lens == "prefill32" else np.array(lens)
+    q, k, v, qn, kn, cos_t, sin_t, cu = _prompt_inputs(dev, lens, seed=50 + len(lens))
+    n, page = len(lens), 16
+    Pn = int(-(-lens.max() // page))
+    num_pages = max(2 * n * Pn, 64)
+    bt = _table(n, Pn, num_pages, seed=51)
+    kc = torch.full((num_pages, page, 8, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, float("nan"))
+    scale = D ** -0.5
+    print(f"[case] prefill_append_rope {n} sequences, {int(lens.sum())} tokens", flush=True)
+    out = q3attn.prefill_append_rope(q, k, v, qn, kn, cos_t, sin_t, cu, int(lens.max()), kc, vc,
+                                     torch.from_numpy(bt).to(dev), scale)
+    torch.cuda.synchronize()
+    cn, sn = to_np(cos_t), to_np(sin_t)
+    q_o = _eager_norm_rope_np(to_np(q), to_np(qn), cn, sn)
+    k_o = _eager_norm_rope_np(to_np(k), to_np(kn), cn, sn)
+    cu_np = cu.cpu().numpy()
+    ok, st = ora.compare(to_np(out), ora.prefill_varlen(q_o, k_o, to_np(v), cu_np, scale))
+    print(f"[parity] prefill_append_rope {n} sequences vs oracle {st}", flush=True)
+    assert ok, st
+    # every token's K (normalised) and V rows at its position; no other slot written
+    kcn, vcn = to_np(kc), to_np(vc)
+    rows = np.concatenate([np.arange(L) for L in lens])
+    seq = np.repeat(np.arange(n), lens)
+    pages, offs = bt[seq, rows // page], rows % page
+    assert np.array_equal(vcn[pages, offs], to_np(v))
+    _assert_last_bit(kcn[pages, offs], k_o, f"prompt pool K rows, {n} sequences")
+    written = np.zeros(kc.shape[:2], dtype=bool)
+    written[pages, offs] = True
+    assert np.isnan(kcn[~written]).all() and np.isnan(vcn[~written]).all()
+
+
+def test_prompt_step_rope_matches_torch_producers(cuda_device):
+    """The talker's own sequence on the GPU (engine/talker.py:157-169): eager torch producers, then prefill_append
+    (the fused scatters + attention)."""
+    dev = cuda_device
+    lens = W.prefill_lengths("prefill32")
+    q, k, v, qn, kn, cos_t, sin_t, cu = _prompt_inputs(dev, lens, seed=52)
+    n = len(lens)
+    Pn = int(-(-lens.max() // 16))
+    bt = torch.from_numpy(_table(n, Pn, 2 * n * Pn, seed=53)).to(dev)
+    pools = [torch.zeros(2 * n * Pn, 16, 8, D, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    scale = D ** -0.5
+    L = int(lens.max())
+    out = q3attn.prefill_append_rope(q, k, v, qn, kn, cos_t, sin_t, cu, L, pools[0], pools[1], bt, scale)
+    qe = _eager_norm_rope_torch(q, qn, cos_t, sin_t)
+    ke = _eager_norm_rope_torch(k, kn, cos_t, sin_t)
+    ref = q3attn.prefill_append(qe, ke, v, cu, cu, L, pools[2], pools[3], bt, scale, True)
+    torch.cuda.synchronize()
+    _assert_last_bit(to_np(pools[0]), to_np(pools[2]), "prompt pool K vs torch producers")
+    assert torch.equal(pools[1], pools[3])
+    ok, st = ora.compare(to_np(out), to_np(ref), max_abs=1e-2, mean_abs=2e-4)
+    print(f"[parity] prompt rope form vs torch producers + prefill_append: {st}", flush=True)
+    assert ok, st
+
+
+def test_prompt_step_rope_in_graph_replays(cuda_device):
+    dev = cuda_device
+    lens = np.array([150, 33, 260, 1, 97])
+    q, k, v, qn, kn, cos_t, sin_t, cu = _prompt_inputs(dev, lens, seed=54)
+    Pn = int(-(-lens.max() // 16))
+    bt = torch.from_numpy(_table(len(lens), Pn, 128, seed=55)).to(dev)
+    kc = torch.zeros(128, 16, 8, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    L = int(lens.max())
+    eager = q3attn.prefill_append_rope(q, k, v, qn, kn, cos_t, sin_t, cu, L, kc, vc, bt, D ** -0.5)
+    torch.cuda.synchronize()
+    k_ref, v_ref = kc.clone(), vc.clone()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        static = q3attn.prefill_append_rope(q, k, v, qn, kn, cos_t, sin_t, cu, L, kc, vc, bt, D ** -0.5)
     for _ in range(3):
         kc.fill_(float("nan"))
         vc.fill_(float("nan"))
