@@ -386,6 +386,38 @@ def test_prefill_dense_append_rope_workspace_and_noop():
     assert _dense_rope(S=0) == 0 and _dense_rope(R=0) == 0
 
 
+def _prompt_rope(**kw):
+    """The prompt-step shape (32 sequences, 8,800 tokens), q/k/v as views of a [T, 4096] qkv projection."""
+    a = dict(q=16, q_st=4096, q_sh=128, k=16, k_st=4096, k_sh=128, v=16, v_st=4096, v_sh=128, qn=16, kn=16, cos=16,
+             sin=16, rope_st=128, eps=1e-6, cu=16, kc=16, vc=16, c_sp=16384, c_st=1024, c_sh=128, num_pages=1024,
+             page=16, bt=16, bt_sb=32, max_pages=32, out=16, o_st=2048, o_sh=128, ws=16, ws_bytes=1 << 30, n=32,
+             T=8800, L=400, Hq=16, Hkv=8, D=128, scale=0.088, causal=1)
+    a.update(kw)
+    return _lib.lib().q3a_prefill_append_rope(
+        a["q"], a["q_st"], a["q_sh"], a["k"], a["k_st"], a["k_sh"], a["v"], a["v_st"], a["v_sh"], a["qn"], a["kn"],
+        a["cos"], a["sin"], a["rope_st"], a["eps"], a["cu"], a["kc"], a["vc"], a["c_sp"], a["c_st"], a["c_sh"],
+        a["num_pages"], a["page"], a["bt"], a["bt_sb"], a["max_pages"], a["out"], a["o_st"], a["o_sh"], a["ws"],
+        a["ws_bytes"], a["n"], a["T"], a["L"], a["Hq"], a["Hkv"], a["D"], a["scale"], a["causal"], None)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(kn=None), "null pointer"), (dict(cu=None), "null pointer"), (dict(ws=None), "null pointer"),
+    (dict(bt=None), "null pointer"), (dict(sin=24), "aligned"), (dict(k_st=4100), "strides"),
+    (dict(ws_bytes=4096), "workspace"), (dict(D=256), "head_dim"), (dict(Hq=8), "num_q_heads"),
+    (dict(Hq=12, Hkv=6), "multiple of 4"), (dict(page=24), "power of two"), (dict(T=-5), "negative"),
+])
+def test_prefill_append_rope_rejects_bad_arguments(kw, frag):
+    assert _prompt_rope(**kw) < 0
+    assert frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_prefill_append_rope_workspace_and_noop():
+    L = _lib.lib()
+    assert L.q3a_prefill_append_rope_workspace_bytes(8800, 16, 8, 128) == 8800 * 16 * 256 + 8800 * 8 * 256
+    assert L.q3a_prefill_append_rope_workspace_bytes(0, 16, 8, 128) == 0
+    assert _prompt_rope(n=0) == 0 and _prompt_rope(T=0) == 0 and _prompt_rope(L=0) == 0
+
+
 def test_prefill_dense_append_empty_is_a_noop():
     """Nothing to compute or write: no device pointer is touched (these are fake addresses)."""
     assert _prefill_dense_append(S=0) == 0 and _prefill_dense_append(R=0, first=0) == 0
