@@ -488,6 +488,7 @@ def bench_cp(args, dev):
     log(f"[bench] cp: {len(order)} calls per frame, fused {frame_us:.1f} us/frame = {call_us:.2f} us/call "
         f"(cache-flushed frame {cold_us:.1f} us); index_copy_ x2 + attention {split_us:.1f} us/frame; launch floor "
         f"{floor_us:.2f} us/call; {achieved:.0f} GB/s algorithmic")
+    norm_rope = bench_cp_rope(args, dev, layers, order, B, L, scale)
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.torch_cpu import cp_attn_rows
@@ -522,7 +523,72 @@ def bench_cp(args, dev):
                 "roofline": {"bound": "latency", "achieved": round(call_us, 3), "peak": round(floor_us, 3),
                              "unit": "us/call", "frac": round(floor_us / call_us, 4), "traffic": None},
                 "cpu_baseline": cpu})
+    if norm_rope is not None:
+        rec["norm_rope_form"] = norm_rope
     return rec
+
+
+def bench_cp_rope(args, dev, layers, order, B, L, scale):
+    """Extra information beside the code-predictor line: the frame with the step's q/k producers
+    (engine/code_predictor.py:38-43) folded into the attention call, cp_attn_append_rope on the raw projections,
+    against the producers as separate ops before cp_attn_append: compiled by torch.compile as the engine compiles
+    _pre (skipped in the short extra runs, whose time budget does not cover a compile) and as eager torch ops.
+    Synthetic qkv projections and norm weights; slot p's cos/sin rows."""
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 98)
+    bf = torch.bfloat16
+    qkv = {(p, l): torch.randn(B, 4096, generator=gen, device=dev).to(bf) for (p, l) in order}
+    qn = [(1.0 + 0.1 * torch.randn(128, generator=gen, device=dev)).to(bf) for _ in range(L)]
+    kn = [(1.0 + 0.1 * torch.randn(128, generator=gen, device=dev)).to(bf) for _ in range(L)]
+    cos, sin = W.rope_tables(16, dev)
+    cos, sin = cos.to(bf), sin.to(bf)
+
+    def producers(x, qw, kw, c, s_):
+        def rms(t, w):
+            tf = t.float()
+            tf = tf * torch.rsqrt(tf.pow(2).mean(-1, keepdim=True) + 1e-6)
+            return w * tf.to(t.dtype)
+
+        def rope(t):
+            return t * c + torch.cat((-t[..., 64:], t[..., :64]), dim=-1) * s_
+        return rope(rms(x[:, :2048].view(B, 16, 128), qw)), rope(rms(x[:, 2048:3072].view(B, 8, 128), kw))
+
+    def fused():
+        return [q3attn.cp_attn_append_rope(qkv[p, l][:, :2048].view(B, 16, 128), qkv[p, l][:, 2048:3072].view(B, 8, 128),
+                                           qkv[p, l][:, 3072:].view(B, 8, 128), layers[l][1], layers[l][2], p, scale,
+                                           qn[l], kn[l], cos[p], sin[p]) for (p, l) in order]
+
+    def separate(fn):
+        def frame():
+            out = []
+            for (p, l) in order:
+                q, k = fn(qkv[p, l], qn[l], kn[l], cos[p], sin[p])
+                out.append(q3attn.cp_attn_append(q, k, qkv[p, l][:, 3072:].view(B, 8, 128), layers[l][1],
+                                                 layers[l][2], p, scale))
+            return out
+        return frame
+
+    warm_s = getattr(args, "min_warm_s", 0.0)
+    res = {}
+    forms = [("fused", fused), ("eager_producers_then_append", separate(producers))]
+    if not getattr(args, "no_compile", False):
+        forms.append(("compiled_producers_then_append", separate(torch.compile(producers, dynamic=False))))
+    for name, fn in forms:
+        try:
+            _, fr, _ = time_graph(dev, fn, args.steps, args.warmup, warm_s)
+            res[name + "_us_per_step"] = round(statistics.mean(fr) * 1e3, 2)
+        except Exception as e:  # noqa: BLE001 - a compile failure is reported, never fatal
+            res[name + "_us_per_step"] = None
+            res[name + "_error"] = f"{type(e).__name__}: {e}"[:200]
+    log(f"[bench] cp norm/rope form: fused {res['fused_us_per_step']} us/frame; eager producers + append "
+        f"{res['eager_producers_then_append_us_per_step']}; compiled producers + append "
+        f"{res.get('compiled_producers_then_append_us_per_step')}")
+    return res
 
 
 def bench_prefill(args, dev):
@@ -836,6 +902,7 @@ def other_workloads(args, dev):
 
     lite = copy.copy(args)
     lite.steps, lite.warmup, lite.no_cpu_baseline, lite.no_append = 20, 3, True, True
+    lite.no_compile = True                # a torch.compile of the CP producers does not fit these short runs
     lite.min_warm_s = 1.0                 # the GPU sat idle during the CPU baseline before: let clocks ramp
     dec = copy.copy(lite)
     dec.no_cpu_baseline = args.no_cpu_baseline
@@ -850,7 +917,7 @@ def other_workloads(args, dev):
             r = fn()
             keep = {k: r[k] for k in ("us_per_layer_call", "us_per_call", "hbm_gbps", "pct_hbm_peak", "tflops",
                                       "three_launch_us_per_step", "cold_us_per_call", "launch_floor_us_per_call",
-                                      "prompt_step", "admission_step") if k in r}
+                                      "prompt_step", "admission_step", "norm_rope_form") if k in r}
             keep["us_per_step"] = r["value"]
             keep["roofline_frac"] = r["roofline"]["frac"]
             keep["roofline_unit"] = r["roofline"]["unit"]

@@ -27,7 +27,8 @@ extern "C" {
 
 /* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
  * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope.
- * 5: q3a_prefill_dense_append.  6: q3a_prefill_dense_append_rope, q3a_prefill_append_rope. */
+ * 5: q3a_prefill_dense_append.  6: q3a_prefill_dense_append_rope, q3a_prefill_append_rope,
+ * q3a_cp_attn_append_rope. */
 #define Q3A_ABI_VERSION 6
 int q3a_abi_version(void);
 
@@ -187,6 +188,21 @@ int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void* k_new, int
                        int64_t k_stride_s, void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
                        void* out, int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                        int n_live, float softmax_scale, void* stream);
+
+/*
+ * q3a_cp_attn_append with the step's producers (engine/code_predictor.py:38-43): q and k_new arrive raw (views of
+ * the qkv projection: q [B, Hq, D] with head stride D, k_new as in q3a_cp_attn_append) and are RMS-normalised with
+ * q_norm_w / k_norm_w [D] and rotated with slot (n_live - 1)'s cos/sin rows [D] (engine/ops.py:51-60 as the compiled
+ * _pre evaluates them: y = bf16(x * rsqrt(mean(x^2) + eps)) * w, then bf16(y * cos + rot(y) * sin) rounded once).
+ * The normalised k_new is what slot n_live - 1 receives; the rest as q3a_cp_attn_append.  The weights and the
+ * cos/sin rows must be 16-byte aligned.
+ */
+int q3a_cp_attn_append_rope(const void* q, int64_t q_stride_b, const void* k_new, int64_t kn_stride_b,
+                            const void* v_new, int64_t vn_stride_b, const void* q_norm_w, const void* k_norm_w,
+                            const void* cos, const void* sin, float eps, void* k, int64_t k_stride_b,
+                            int64_t k_stride_h, int64_t k_stride_s, void* v, int64_t v_stride_b, int64_t v_stride_h,
+                            int64_t v_stride_s, void* out, int64_t o_stride_b, int batch, int num_q_heads,
+                            int num_kv_heads, int head_dim, int n_live, float softmax_scale, void* stream);
 
 /*
  * Talker prefill attention (packed variable-length, MFMA).

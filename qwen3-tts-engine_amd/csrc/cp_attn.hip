@@ -43,6 +43,13 @@ struct CpArgs {
   int64_t o_sb;
   int pairs, hkv, n_live;
   float scale_log2;
+  // Norm/rope form: q and the new k arrive raw and are RMS-normalised (q_norm_w / k_norm_w) and rotated with the
+  // step's cos/sin row in the kernel.
+  const uint16_t* qn;
+  const uint16_t* kn;
+  const uint16_t* cs;
+  const uint16_t* sn;
+  float eps;
 };
 
 // The 16 bytes lane `src` holds (ds_bpermute: the LDS crossbar, no LDS storage).  All lanes must be active.
@@ -54,8 +61,9 @@ __device__ __forceinline__ uint4 bpermute16(const uint4& v, int src) {
 
 // kNV: slots whose V rows are loaded and walked by P.V, n_live rounded up to a multiple of 4 (one instantiation
 // each, so every load stays unconditional and the slot loop fully unrolled).
-template <bool kAppend, int kNV>
+template <bool kAppend, int kNV, bool kRope = false>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpArgs a) {
+  static_assert(kAppend || !kRope, "the norm/rope form is an append form");
   const int wave = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (wave >= a.pairs) return;
   const int b = __builtin_amdgcn_readfirstlane(wave / a.hkv);
@@ -81,7 +89,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
   uint4 kr[4], qr[kG][2];
   uint32_t vr[kNV], vn = 0u;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(qb, kG * kD * 2);
-  const uint4 qc = buffer_load16(rq, lane < kG * 16 ? (uint32_t)lane * 16 : kOutOfRange);
+  uint4 qc = buffer_load16(rq, lane < kG * 16 ? (uint32_t)lane * 16 : kOutOfRange);
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     kr[j] = buffer_load16(rk, (uint32_t)(s8 + 8 * (j >> 1)) * krow_b + (uint32_t)(8 * c + 64 * (j & 1)) * 2);
@@ -89,20 +97,41 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
       kAppend ? make_rsrc(a.k_new + (int64_t)b * a.kn_sb + (int64_t)g * kD, kD * 2) : rk;
   const __amdgpu_buffer_rsrc_t rvn =
       kAppend ? make_rsrc(a.v_new + (int64_t)b * a.vn_sb + (int64_t)g * kD, kD * 2) : rv;
+  // The new k row sits on lanes kKL .. kKL + 15 (16 B each); the norm/rope form puts it beside q's lanes 0..31, so
+  // one qk_norm_rope16 pass transforms both.
+  constexpr int kKL = kRope ? 32 : 0;
   uint4 knc = make_uint4(0u, 0u, 0u, 0u);
-  if constexpr (kAppend) knc = buffer_load16(rkn, lane < 16 ? (uint32_t)lane * 16 : kOutOfRange);
+  if constexpr (kAppend)
+    knc = buffer_load16(rkn, (unsigned)(lane - kKL) < 16u ? (uint32_t)(lane - kKL) * 16 : kOutOfRange);
 #pragma unroll
   for (int s = 0; s < kNV; ++s)
     vr[s] = __builtin_amdgcn_raw_buffer_load_b32(rv, lane * 4, (int)((uint32_t)s * vrow_b), 0);
   if constexpr (kAppend) vn = __builtin_amdgcn_raw_buffer_load_b32(rvn, lane * 4, 0, 0);
+  // Norm/rope form: lane l's 16 B chunk (dims 8 (l % 16)..+8) of the weights and of the step's cos/sin row, loaded
+  // beside the row loads (no extra round trip).
+  uint4 wn, rc, rs;
+  if constexpr (kRope) {
+    const int c16 = 8 * (lane & 15);
+    wn = ld16((lane < 32 ? a.qn : a.kn) + c16);
+    rc = ld16(a.cs + c16);
+    rs = ld16(a.sn + c16);
+  }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kRope) {
+    // q of heads 2g, 2g+1 on lanes 0..31 and the new k row on lanes 32..47, each row on 16 lanes in the layout
+    // qk_norm_rope16 takes: one pass normalises and rotates all three rows (lanes 48..63 transform zeros and are
+    // not read).  The rope is rounded once, as the compiled _pre evaluates it (engine/code_predictor.py:38-43).
+    const uint4 y = qk_norm_rope16(lane < 32 ? qc : knc, wn, rc, rs, a.eps);
+    qc = y;
+    knc = y;
+  }
 #pragma unroll
   for (int h = 0; h < kG; ++h) {
     qr[h][0] = bpermute16(qc, 16 * h + c);
     qr[h][1] = bpermute16(qc, 16 * h + 8 + c);
   }
   if constexpr (kAppend) {
-    const uint4 kn0 = bpermute16(knc, c), kn1 = bpermute16(knc, 8 + c);
+    const uint4 kn0 = bpermute16(knc, kKL + c), kn1 = bpermute16(knc, kKL + 8 + c);
     if (s8 == last) {
       kr[0] = kn0;
       kr[1] = kn1;
@@ -118,8 +147,9 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
     const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.v_ss, kD * 2);
     // Non-temporal slot and output stores (the lines stream out instead of staying dirty in the L2): 6.83 -> 6.79 us
     // per call in the 512-row frame.
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, knc), wk,
-                                           (int)(lane < 16 ? (uint32_t)lane * 16 : kOutOfRange), 0, kCacheNT);
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(u32x4, knc), wk,
+        (int)((unsigned)(lane - kKL) < 16u ? (uint32_t)(lane - kKL) * 16 : kOutOfRange), 0, kCacheNT);
     __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, kCacheNT);
   }
 
@@ -190,7 +220,9 @@ static int cp_launch(const void* q, int64_t q_stride_b, void* k, int64_t k_strid
                      int64_t k_stride_s, void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
                      const void* k_new, const void* v_new, int64_t kn_stride_b, int64_t vn_stride_b, void* out,
                      int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim, int n_live,
-                     float softmax_scale, void* stream, const char* who) {
+                     float softmax_scale, void* stream, const char* who, const void* q_norm_w = nullptr,
+                     const void* k_norm_w = nullptr, const void* cos = nullptr, const void* sin = nullptr,
+                     float eps = 0.f) {
   if (batch < 0) return fail(Q3A_EINVAL, "%s: batch %d < 0", who, batch);
   if (batch == 0) return Q3A_OK;
   if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
@@ -232,11 +264,22 @@ static int cp_launch(const void* q, int64_t q_stride_b, void* k, int64_t k_strid
   a.hkv = num_kv_heads;
   a.n_live = n_live;
   a.scale_log2 = softmax_scale * kLog2e;
+  const bool rope = q_norm_w != nullptr;
+  a.qn = static_cast<const uint16_t*>(q_norm_w);
+  a.kn = static_cast<const uint16_t*>(k_norm_w);
+  a.cs = static_cast<const uint16_t*>(cos);
+  a.sn = static_cast<const uint16_t*>(sin);
+  a.eps = eps;
   const int blocks = (int)((pairs + kWavesPerBlock - 1) / kWavesPerBlock);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(blocks), block(64 * kWavesPerBlock);
   const int nv = (n_live + 3) / 4;
-  if (k_new != nullptr) {
+  if (rope) {
+    if (nv == 1) hipLaunchKernelGGL((cp_attn_kernel<true, 4, true>), grid, block, 0, st, a);
+    else if (nv == 2) hipLaunchKernelGGL((cp_attn_kernel<true, 8, true>), grid, block, 0, st, a);
+    else if (nv == 3) hipLaunchKernelGGL((cp_attn_kernel<true, 12, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((cp_attn_kernel<true, 16, true>), grid, block, 0, st, a);
+  } else if (k_new != nullptr) {
     if (nv == 1) hipLaunchKernelGGL((cp_attn_kernel<true, 4>), grid, block, 0, st, a);
     else if (nv == 2) hipLaunchKernelGGL((cp_attn_kernel<true, 8>), grid, block, 0, st, a);
     else if (nv == 3) hipLaunchKernelGGL((cp_attn_kernel<true, 12>), grid, block, 0, st, a);
@@ -271,4 +314,21 @@ extern "C" int q3a_cp_attn_append(const void* q, int64_t q_stride_b, const void*
   return cp_launch(q, q_stride_b, k, k_stride_b, k_stride_h, k_stride_s, v, v_stride_b, v_stride_h, v_stride_s,
                    k_new, v_new, kn_stride_b, vn_stride_b, out, o_stride_b, batch, num_q_heads, num_kv_heads,
                    head_dim, n_live, softmax_scale, stream, "cp_attn_append");
+}
+
+extern "C" int q3a_cp_attn_append_rope(const void* q, int64_t q_stride_b, const void* k_new, int64_t kn_stride_b,
+                                       const void* v_new, int64_t vn_stride_b, const void* q_norm_w,
+                                       const void* k_norm_w, const void* cos, const void* sin, float eps, void* k,
+                                       int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s, void* v,
+                                       int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s, void* out,
+                                       int64_t o_stride_b, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                       int n_live, float softmax_scale, void* stream) {
+  const char* who = "cp_attn_append_rope";
+  if (!k_new || !v_new) return fail(Q3A_EINVAL, "%s: null k_new/v_new", who);
+  if (!q_norm_w || !k_norm_w || !cos || !sin) return fail(Q3A_EINVAL, "%s: null norm weight or cos/sin row", who);
+  if (((uintptr_t)q_norm_w | (uintptr_t)k_norm_w | (uintptr_t)cos | (uintptr_t)sin) % 16 != 0)
+    return fail(Q3A_EINVAL, "%s: norm weights and cos/sin rows must be 16-byte aligned", who);
+  return cp_launch(q, q_stride_b, k, k_stride_b, k_stride_h, k_stride_s, v, v_stride_b, v_stride_h, v_stride_s,
+                   k_new, v_new, kn_stride_b, vn_stride_b, out, o_stride_b, batch, num_q_heads, num_kv_heads,
+                   head_dim, n_live, softmax_scale, stream, who, q_norm_w, k_norm_w, cos, sin, eps);
 }

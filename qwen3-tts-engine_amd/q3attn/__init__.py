@@ -6,6 +6,7 @@ Entry points (each a drop-in for the reference call it names):
   * ``paged_decode_append_rope``                     -- q/k RMSNorm + RoPE, KV append and decode (engine/talker.py:69-77)
   * ``cp_attn`` / ``cp_attn_append``                 -- code-predictor attention (engine/cp_attn.py:33-39;
                                                        slot write fused: engine/code_predictor.py:58)
+  * ``cp_attn_append_rope``                          -- + the step's q/k norm and RoPE (engine/code_predictor.py:38-43)
   * ``flash_attn_varlen_func`` / ``flash_attn_func``  -- prefill (engine/talker.py:169, engine/arrivals.py:148)
   * ``prefill_append``                               -- prompt K/V into the pool + prefill (engine/talker.py:161-169)
   * ``prefill_append_rope``                          -- + the prompt's q/k norm and RoPE (engine/talker.py:157-169)
@@ -16,7 +17,8 @@ Entry points (each a drop-in for the reference call it names):
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 from ._lib import LIB_PATH, Q3AttnError, lib  # noqa: F401
-from .cp_attn import cp_attn, cp_attn_append, cp_attn_append_op, cp_attn_op  # noqa: F401
+from .cp_attn import (cp_attn, cp_attn_append, cp_attn_append_op, cp_attn_append_rope,  # noqa: F401
+                      cp_attn_append_rope_op, cp_attn_op)
 from .ops import flash_attn_with_kvcache, paged_decode, paged_decode_append, paged_decode_append_rope  # noqa: F401
 from .pages import PagePool, PoolExhausted  # noqa: F401
 from .prefill import (flash_attn_func, flash_attn_varlen_func, prefill, prefill_append, prefill_dense,  # noqa: F401

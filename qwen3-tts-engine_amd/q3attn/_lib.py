@@ -129,6 +129,14 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,        # num_seqs, seqlen_q, prefix_len, Hq, Hkv, D
         _c_float, _c_int, _c_vp,                               # softmax_scale, causal, stream
     ]),
+    "q3a_cp_attn_append_rope": (_c_int, [
+        _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,          # q (raw), row stride, k_new (raw), stride, v_new, stride
+        _c_vp, _c_vp, _c_vp, _c_vp, _c_float,                  # q/k norm weights, cos, sin rows, eps
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # K scratch, strides (row, head, slot)
+        _c_vp, _c_i64, _c_i64, _c_i64,                         # V scratch, strides
+        _c_vp, _c_i64,                                         # out, row stride
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_vp,  # B, Hq, Hkv, D, n_live, scale, stream
+    ]),
     "q3a_prefill_append_rope_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "q3a_prefill_append_rope": (_c_int, [
         _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,          # q (raw), strides (tok, head), k (raw), strides

@@ -8,7 +8,8 @@ to bf16 before P.V, P.V accumulates in float32.  GPU only.
 
 ``cp_attn_append(q, k, v, K, V, p, scale)`` is the slot write of engine/code_predictor.py:58
 (``K.index_copy_(2, p, k.unsqueeze(2))`` and the same for V) fused with that attention over
-n_live = p + 1 slots: one launch instead of three.
+n_live = p + 1 slots: one launch instead of three.  ``cp_attn_append_rope`` takes q and k raw and applies the
+q/k RMSNorm + RoPE of ``_pre`` (engine/code_predictor.py:38-43) in the same launch.
 """
 from __future__ import annotations
 
@@ -102,3 +103,42 @@ def cp_attn_append(q, k, v, K, V, p, scale):
     K[:, :, p] = k, V[:, :, p] = v (k, v [B, 8, 128], v may be a view into the qkv projection), then
     attention over slots 0..p -> o [B, 2048]."""
     return cp_attn_append_op(q, k, v, K, V, int(p), float(scale))
+
+
+@torch.library.custom_op("q3attn::cp_attn_append_rope", mutates_args=("K", "V"))
+def cp_attn_append_rope_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
+                           p: int, scale: float, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
+                           sin: torch.Tensor, eps: float) -> torch.Tensor:
+    q2, B, Hkv, D, Hq = _check_common(q, K, V, int(p) + 1, "cp_attn_append_rope")
+    dev = q.device
+    for name, t in (("k", k), ("v", v), ("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w), ("cos", cos), ("sin", sin)):
+        _req(t.device == dev, f"q3attn.cp_attn_append_rope: {name} must be on q's device")
+    k3 = _new_rows(k, B, Hkv, D, "k")
+    v3 = _new_rows(v, B, Hkv, D, "v")
+    for name, t in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w), ("cos", cos), ("sin", sin)):
+        _req(t.dtype == torch.bfloat16 and t.numel() == D and t.is_contiguous(),
+             f"q3attn.cp_attn_append_rope: {name} must be a contiguous bfloat16 row of {D}")
+    out = torch.empty((B, Hq * D), dtype=q.dtype, device=dev)
+    if B == 0:
+        return out
+    rc = lib().q3a_cp_attn_append_rope(
+        q2.data_ptr(), q2.stride(0), k3.data_ptr(), k3.stride(0), v3.data_ptr(), v3.stride(0),
+        q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), float(eps),
+        K.data_ptr(), K.stride(0), K.stride(1), K.stride(2), V.data_ptr(), V.stride(0), V.stride(1), V.stride(2),
+        out.data_ptr(), out.stride(0), B, Hq, Hkv, D, int(p) + 1, float(scale), torch.cuda.current_stream(dev).cuda_stream)
+    check(rc, "q3a_cp_attn_append_rope")
+    return out
+
+
+@cp_attn_append_rope_op.register_fake
+def _cp_attn_append_rope_fake(q, k, v, K, V, p, scale, q_norm_w, k_norm_w, cos, sin, eps):
+    return q.new_empty((q.shape[0], K.shape[1] * 2 * K.shape[3]))
+
+
+def cp_attn_append_rope(q, k, v, K, V, p, scale, q_norm_w, k_norm_w, cos, sin, eps=1e-6):
+    """One code-predictor step's attention block (engine/code_predictor.py:38-43, 58, 46-47) in one launch: q
+    [B, 16, 128] and k [B, 8, 128] arrive raw (views of the qkv projection), are RMS-normalised with q_norm_w /
+    k_norm_w and rotated with slot p's cos/sin row ([128], W.cp_cos[p]) as the compiled _pre evaluates them (the rope
+    rounded once), k and v go into slot p of K/V [B, 8, 16, 128], and the attention over slots 0..p -> o [B, 2048]."""
+    return cp_attn_append_rope_op(q, k, v, K, V, int(p), float(scale), q_norm_w, k_norm_w, cos.reshape(-1),
+                                  sin.reshape(-1), float(eps))

@@ -153,7 +153,7 @@ def test_dense_append_rope_matches_torch_producers(cuda_device, P):
     torch.cuda.synchronize()
     _assert_last_bit(to_np(pools[0]), to_np(pools[2]), f"pool K, P={P}")
     assert torch.equal(pools[1], pools[3])
-    ok, st = ora.compare(to_np(out), to_np(ref), max_abs=1e-2, mean_abs=2e-4)
+    ok, st = ora.compare(to_np(out), to_np(ref), max_abs=2e-2, mean_abs=2e-4)
     print(f"[parity] rope form vs torch producers + dense append, P={P}: {st}", flush=True)
     assert ok, st
 
@@ -273,7 +273,7 @@ def test_prompt_step_rope_matches_torch_producers(cuda_device):
     torch.cuda.synchronize()
     _assert_last_bit(to_np(pools[0]), to_np(pools[2]), "prompt pool K vs torch producers")
     assert torch.equal(pools[1], pools[3])
-    ok, st = ora.compare(to_np(out), to_np(ref), max_abs=1e-2, mean_abs=2e-4)
+    ok, st = ora.compare(to_np(out), to_np(ref), max_abs=2e-2, mean_abs=2e-4)
     print(f"[parity] prompt rope form vs torch producers + prefill_append: {st}", flush=True)
     assert ok, st
 
