@@ -120,6 +120,23 @@ def test_cp_attn_append_rejects_bad_arguments(kw, frag):
     assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
 
 
+@pytest.mark.parametrize("kw,frag", [
+    (dict(qn=None), "null norm weight"), (dict(sin=None), "null norm weight"), (dict(cos=24), "16-byte aligned"),
+    (dict(kn=None, ), "null norm weight"), (dict(k_new=None), "k_new"), (dict(n_live=0), "n_live"),
+    (dict(Hq=8), "num_q_heads"), (dict(D=64), "head_dim"),
+])
+def test_cp_attn_append_rope_rejects_bad_arguments(kw, frag):
+    a = dict(q=16, q_sb=4096, k_new=16, kn_sb=4096, v_new=16, vn_sb=4096, qn=16, kn=16, cos=16, sin=16, eps=1e-6,
+             k=16, k_sb=16384, k_sh=2048, k_ss=128, v=16, v_sb=16384, v_sh=2048, v_ss=128, out=16, o_sb=2048, B=4,
+             Hq=16, Hkv=8, D=128, n_live=3, scale=0.088)
+    a.update(kw)
+    rc = _lib.lib().q3a_cp_attn_append_rope(a["q"], a["q_sb"], a["k_new"], a["kn_sb"], a["v_new"], a["vn_sb"], a["qn"],
+                                            a["kn"], a["cos"], a["sin"], a["eps"], a["k"], a["k_sb"], a["k_sh"],
+                                            a["k_ss"], a["v"], a["v_sb"], a["v_sh"], a["v_ss"], a["out"], a["o_sb"],
+                                            a["B"], a["Hq"], a["Hkv"], a["D"], a["n_live"], a["scale"], None)
+    assert rc < 0 and frag in _lib.lib().q3a_last_error().decode()
+
+
 def test_python_entry_points_refuse_cpu_tensors():
     q = torch.zeros(2, 1, 16, 128, dtype=torch.bfloat16)
     kc = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16)

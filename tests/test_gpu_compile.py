@@ -296,3 +296,53 @@ def test_compiled_decode_rope_form(cuda_device):
         torch.cuda.synchronize()
         assert torch.equal(static[0], o)
         assert torch.equal(kc, pool)
+
+
+def test_compiled_code_predictor_step_with_fused_producers(cuda_device):
+    """The code-predictor step with _pre's producers folded in (engine/code_predictor.py:38-47, 58): a compiled
+    function takes the raw qkv projection, calls cp_attn_append_rope on its views (q/k norm + RoPE, slot write,
+    attention) and applies the o-projection.  Compiled, the call mutates the scratch slice in place (no
+    functionalised copy), its output matches the eager op's bit for bit and it replays from a graph."""
+    from torch._inductor.utils import run_and_get_code
+
+    dev = cuda_device
+    torch._dynamo.reset()
+    L, max_bs, B = 5, 512, 400
+    Ks = torch.zeros(L, max_bs, NKV, 16, HD, dtype=torch.bfloat16, device=dev)
+    Vs = torch.zeros_like(Ks)
+    g = torch.Generator(device=dev).manual_seed(10)
+    qkv_w = (torch.randn(4096, 1024, generator=g, device=dev) * 1024 ** -0.5).to(torch.bfloat16)
+    o_w = (torch.randn(1024, NQ, generator=g, device=dev) * NQ ** -0.5).to(torch.bfloat16)
+    qn = (1.0 + 0.1 * torch.randn(HD, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(HD, generator=g, device=dev)).to(torch.bfloat16)
+    cos_t, sin_t = rope_bf16(16, dev)
+
+    def step(x, K, V, c, s, p: int):
+        qkv = F.linear(x, qkv_w)
+        o = q3attn.cp_attn_append_rope(qkv[:, :NQ].view(-1, 16, HD), qkv[:, NQ:NQ + 1024].view(-1, NKV, HD),
+                                       qkv[:, NQ + 1024:].view(-1, NKV, HD), K, V, p, SCALE, qn, kn, c, s)
+        return x + F.linear(o, o_w), o
+
+    cstep = torch.compile(step, dynamic=False)
+    for p in (0, 5, 15):
+        x = torch.randn(B, 1024, generator=g, device=dev).to(torch.bfloat16)
+        l = p % L
+        K, V = Ks[l, :B], Vs[l, :B]
+        Ke, Ve = K.clone(), V.clone()
+        y_e, o_e = step(x, Ke, Ve, cos_t[p], sin_t[p], p)          # eager reference on copies of the slices
+        (y, o), codes = run_and_get_code(cstep, x, K, V, cos_t[p], sin_t[p], p)
+        torch.cuda.synchronize()
+        # the qkv projection's own output (B x 4096) is a quarter of the slice; a copy of the slice would be all of it
+        assert not _big_allocations(codes, K.numel() // 2), "cp_attn_append_rope must not copy the scratch"
+        assert torch.equal(o, o_e)                       # the op's output, bit for bit
+        # the compiled o-projection + residual rounds its fused add differently from eager addmm: torch's own numerics
+        assert torch.allclose(y.float(), y_e.float(), atol=3e-2, rtol=1e-2)
+        assert torch.equal(K, Ke) and torch.equal(V, Ve)
+        gr, static = _capture(lambda: cstep(x, K, V, cos_t[p], sin_t[p], p), dev)
+        for _ in range(2):
+            Ks[l, :B, :, p] = float("nan")
+            gr.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static[1], o) and torch.equal(static[0], y)
+            assert torch.equal(K, Ke)
+        print(f"[compile] cp step with fused producers p={p}: equal to eager, no scratch copy", flush=True)
