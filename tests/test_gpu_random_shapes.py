@@ -154,3 +154,73 @@ def test_prefill_random_shapes(cuda_device, seed):
     label = f"hkv={hkv} n={n} max_len={int(lens.max())} causal={causal}"
     print(f"[random] prefill {label} {st}", flush=True)
     assert ok, (label, st)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_dense_append_random_shapes(cuda_device, seed):
+    """The admission forms (q3a_prefill_dense_append and, on every other seed, the producer form
+    q3a_prefill_dense_append_rope) on random S, R, n, first_row, page size and table: output against the oracle,
+    pool rows first_row .. n-1 at their table positions and nothing else written (NaN-poisoned pool)."""
+    dev = cuda_device
+    rng = np.random.default_rng(2000 + seed)
+    rope = seed % 2 == 1
+    S = int(rng.choice([1, 2, 3, 5, 8]))
+    R = int(rng.choice([1, 7, 16, 42, 65, 130]))
+    P = int(rng.choice([0, 1, 35, 64, 90, 200]))
+    n = P + R
+    page = int(rng.choice([16, 32, 64, 256]))
+    first = int(rng.integers(0, P + 1))
+    Pn = -(-n // page)
+    num_pages = 2 * S * Pn + 3
+    bt = rng.permutation(num_pages)[: S * Pn].reshape(S, Pn).astype(np.int32)
+    scale = 128 ** -0.5
+    print(f"[case] dense append seed={seed} rope={rope} S={S} R={R} P={P} page={page} first={first}", flush=True)
+    kc = torch.full((num_pages, page, 8, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, float("nan"))
+    btd = torch.from_numpy(bt).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3000 + seed)
+    if rope:
+        qkv = torch.randn((S, R, 4096), generator=g, device=dev).to(torch.bfloat16)
+        pk = torch.randn((S, P, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+        pv = torch.randn((S, P, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+        qn = (1.0 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+        kn = (1.0 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+        ang = np.arange(P, n)[:, None] * (1e6 ** (-np.arange(0, 128, 2) / 128))[None, :]
+        emb = np.concatenate([ang, ang], -1)
+        cos, sin = _bf16(np.cos(emb), dev), _bf16(np.sin(emb), dev)
+        q, k, v = qkv[..., :2048].view(S, R, 16, 128), qkv[..., 2048:3072].view(S, R, 8, 128), qkv[..., 3072:].view(S, R, 8, 128)
+        out = q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, kc, vc, btd, scale, None, True,
+                                               EPS, first)
+        c, s = to_np(cos)[None, :, None], to_np(sin)[None, :, None]
+
+        def prod(x, w):   # eager rounding points (engine/ops.py:51-60 as bf16 torch ops)
+            y = ora.bf16_round(to_np(w) * ora.rms(to_np(x), None, EPS, to_bf16=True))
+            rot = np.concatenate([-y[..., 64:], y[..., :64]], axis=-1)
+            return ora.bf16_round(ora.bf16_round(y * c) + ora.bf16_round(rot * s))
+        qo = prod(q, qn)
+        K = np.concatenate([to_np(pk), prod(k, kn)], 1)
+        V = np.concatenate([to_np(pv), to_np(v)], 1)
+    else:
+        qo = rng.standard_normal((S, R, 16, 128)).astype(np.float32)
+        K = rng.standard_normal((S, n, 8, 128)).astype(np.float32)
+        V = rng.standard_normal((S, n, 8, 128)).astype(np.float32)
+        qd, Kd, Vd = _bf16(qo, dev), _bf16(K, dev), _bf16(V, dev)
+        qo, K, V = to_np(qd), to_np(Kd), to_np(Vd)
+        out = q3attn.prefill_dense_append(qd, Kd, Vd, kc, vc, btd, scale, True, first)
+    torch.cuda.synchronize()
+    ref = ora.prefill_prefix(qo, K, V, scale)
+    ok, st = ora.compare(to_np(out), ref)
+    print(f"[parity] dense append seed={seed}: {st}", flush=True)
+    assert ok, st
+    kp, vp = to_np(kc), to_np(vc)
+    j = np.arange(first, n)
+    pages, offs = bt[:, j // page], j % page
+    assert np.array_equal(vp[pages, offs], V[:, first:])
+    diff = np.abs(kp[pages, offs] - K[:, first:])
+    assert (diff <= np.maximum(np.abs(K[:, first:]), 0.5) * 2.0 ** -6).all()
+    if not rope:
+        assert not diff.any()
+    written = np.zeros(kc.shape[:2], dtype=bool)
+    written[pages, offs] = True
+    assert np.isnan(kp[~written]).all() and np.isnan(vp[~written]).all()
