@@ -80,6 +80,13 @@ struct PrefillArgs {
   int nseq;
   int nqt;
   int grp_shift;
+  // Norm/rope q (prefill_kernel<*, true>): q arrives raw and is RMS-normalised with qn and rotated with the cos/sin
+  // row of its packed token index (row stride rs_st), with the rounding of eager bf16 ops, as it is loaded.
+  const uint16_t* qn;
+  const uint16_t* rcos;
+  const uint16_t* rsin;
+  int64_t rs_st;
+  float eps;
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -103,7 +110,7 @@ __device__ __forceinline__ uint2 ldtr(const uint8_t* lds) {
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Three waves per SIMD (<= 168 VGPRs): three workgroups per CU hide each other's prologues and barriers.
-template <bool kGrouped>
+template <bool kGrouped, bool kRopeQ = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void prefill_kernel(const PrefillArgs a) {
   // Two stages of K and V tiles; separate arrays so the compiler can tell the stage being filled from the one
   // being read.
@@ -162,8 +169,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   int Lq, Lk;
   int64_t qbase, obase, kbase;  // kbase: the first key row of the operand this wave copies
   int64_t krow0, vrow0;         // the first K and V rows (append form)
+  int q0 = 0;                   // the sequence's first packed token (the norm/rope form's cos/sin row)
   if (a.cu_q != nullptr) {
-    const int q0 = a.cu_q[s];
+    q0 = a.cu_q[s];
     const int k0 = a.cu_k[s];
     Lq = a.cu_q[s + 1] - q0;
     Lk = a.cu_k[s + 1] - k0;
@@ -191,13 +199,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
   // Q^T of both heads as B operands of S^T = K Q^T: 4 chunks of 32 dims each.
   bf16x8_t qb[kG][4];
+  uint4 x[kG][4], w[4], c[4], sn[4];  // norm/rope-q form: raw q, weight, cos, sin
+  if constexpr (!kRopeQ) {
 #pragma unroll
-  for (int hh = 0; hh < kG; ++hh) {
+    for (int hh = 0; hh < kG; ++hh) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        uint4 xq = make_uint4(0u, 0u, 0u, 0u);
+        if (qvalid) xq = ld16(a.q + qbase + (int64_t)tq * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
+        qb[hh][kk] = as_bf16x8(xq);
+      }
+    }
+  } else {
+    // Raw q, normalised and rotated here (engine/ops.py:51-60 as eager bf16 ops: y = bf16(w * bf16(x * r)),
+    // o = bf16(bf16(y * cos) + bf16(rot(y) * sin))).  The lane holds dims 32 kk + 8 g4 .. +8 of its token for
+    // kk = 0..3, so the mean of squares is an in-lane sum and two lane swaps over the token's 4 lanes, and the
+    // rotate-half partner of chunk kk is chunk kk ^ 2 of the same lane.
+    const int64_t crow = (int64_t)(q0 + (qvalid ? tq : 0)) * a.rs_st;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      uint4 x = make_uint4(0u, 0u, 0u, 0u);
-      if (qvalid) x = ld16(a.q + qbase + (int64_t)tq * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
-      qb[hh][kk] = as_bf16x8(x);
+      const int d0 = 32 * kk + 8 * g4;
+      w[kk] = ld16(a.qn + d0);
+      c[kk] = make_uint4(0u, 0u, 0u, 0u);
+      sn[kk] = c[kk];
+      if (qvalid) {
+        c[kk] = ld16(a.rcos + crow + d0);
+        sn[kk] = ld16(a.rsin + crow + d0);
+      }
+#pragma unroll
+      for (int hh = 0; hh < kG; ++hh) {
+        x[hh][kk] = make_uint4(0u, 0u, 0u, 0u);
+        if (qvalid) x[hh][kk] = ld16(a.q + qbase + (int64_t)tq * a.q_st + (kG * g + hh) * a.q_sh + d0);
+      }
     }
   }
 
@@ -214,7 +247,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // With causal masking and a K/V prefix that is a whole number of 32-key tiles (a prompt has none), the query
   // tokens' rows are the last one or two key tiles the workgroup streams; they are stored from LDS after the loop,
   // and the prologue only fetches the table entries of those positions (lane i: page kown0 / page_size + i).
-  const bool pool_from_lds = a.pk != nullptr && !chunked && a.causal && Lk >= Lq && ((Lk - Lq) & (kKT - 1)) == 0;
+  // (The norm/rope-q form is launched only for whole causal prompts, cu_seqlens_k == cu_seqlens_q: always this case.)
+  const bool pool_from_lds =
+      kRopeQ || (a.pk != nullptr && !chunked && a.causal && Lk >= Lq && ((Lk - Lq) & (kKT - 1)) == 0);
   const int kown0 = Lk - Lq + qt * kQT;
   int pwo = -1;
   if (pool_from_lds) {
@@ -248,7 +283,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       }
     }
   };
-  if (a.pk != nullptr && !pool_from_lds) load_rows(chunked ? a.p_first + qt * kQT : kown0);
+  if (!kRopeQ && a.pk != nullptr && !pool_from_lds) load_rows(chunked ? a.p_first + qt * kQT : kown0);
 
   int kend = Lk;
   if (a.causal) {
@@ -429,7 +464,62 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   if (ntiles > 0) issue(0, sK0, sV0);
   wait_vmem();
   __syncthreads();
-  if (a.pk != nullptr && !pool_from_lds) {
+  if constexpr (kRopeQ) {
+    // The norm/rope-q form's arithmetic, on the loads the prologue issued beside tile 0's copies.
+#pragma unroll
+    for (int hh = 0; hh < kG; ++hh) {
+      float ss = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint32_t xs[4] = {x[hh][kk].x, x[hh][kk].y, x[hh][kk].z, x[hh][kk].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss += bf16_lo(xs[i]) * bf16_lo(xs[i]) + bf16_hi(xs[i]) * bf16_hi(xs[i]);
+      }
+      const float r = rms_rsqrt(sum_xor32(sum_xor16(ss)), a.eps);
+      // chunk pairs (kp, kp + 2): dims d and d + 64
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) {
+        const uint32_t xl[4] = {x[hh][kp].x, x[hh][kp].y, x[hh][kp].z, x[hh][kp].w};
+        const uint32_t xh[4] = {x[hh][kp + 2].x, x[hh][kp + 2].y, x[hh][kp + 2].z, x[hh][kp + 2].w};
+        const uint32_t wl[4] = {w[kp].x, w[kp].y, w[kp].z, w[kp].w};
+        const uint32_t wh[4] = {w[kp + 2].x, w[kp + 2].y, w[kp + 2].z, w[kp + 2].w};
+        const uint32_t cl[4] = {c[kp].x, c[kp].y, c[kp].z, c[kp].w};
+        const uint32_t ch[4] = {c[kp + 2].x, c[kp + 2].y, c[kp + 2].z, c[kp + 2].w};
+        const uint32_t sl[4] = {sn[kp].x, sn[kp].y, sn[kp].z, sn[kp].w};
+        const uint32_t sh[4] = {sn[kp + 2].x, sn[kp + 2].y, sn[kp + 2].z, sn[kp + 2].w};
+        uint32_t ol[4], oh[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float el[2], eh[2];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            auto half = [h2](uint32_t v) { return h2 ? bf16_hi(v) : bf16_lo(v); };
+            const float yl = round_bf16(half(wl[i]) * round_bf16(half(xl[i]) * r));
+            const float yh = round_bf16(half(wh[i]) * round_bf16(half(xh[i]) * r));
+            el[h2] = round_bf16(yl * half(cl[i])) + round_bf16(-yh * half(sl[i]));
+            eh[h2] = round_bf16(yh * half(ch[i])) + round_bf16(yl * half(sh[i]));
+          }
+          ol[i] = pack_bf16x2(el[0], el[1]);
+          oh[i] = pack_bf16x2(eh[0], eh[1]);
+        }
+        qb[hh][kp] = as_bf16x8(make_uint4(ol[0], ol[1], ol[2], ol[3]));
+        qb[hh][kp + 2] = as_bf16x8(make_uint4(oh[0], oh[1], oh[2], oh[3]));
+      }
+    }
+    // Pin the rotated q here, ahead of the loop state: left to itself the compiler sinks this arithmetic into the
+    // loop preheader, beside the live accumulators, where it spills.
+#pragma unroll
+    for (int hh = 0; hh < kG; ++hh) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        uint4 u = __builtin_bit_cast(uint4, qb[hh][kk]);
+        asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
+        qb[hh][kk] = as_bf16x8(u);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (!kRopeQ && a.pk != nullptr && !pool_from_lds) {
     store_rows();
     if (chunked) {
       for (int c = qt + nqt_seq; a.p_first + c * kQT < Lk; c += nqt_seq) {
@@ -740,19 +830,23 @@ struct AdmitPrepArgs {
 
 __global__ __launch_bounds__(256) void admit_prep_kernel(const AdmitPrepArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t j0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;  // the wave's first row job
-  if (j0 >= a.jall) return;                                               // wave-uniform
-  const int64_t j = j0 + (lane >> 4);
+  // The wave's first row job, a multiple of 4 (the job count is below 2^31).  It is wave-uniform, so the block and
+  // index decomposition below is done once per wave in 32 bits; the wave's 4 rows differ only in the head (every
+  // block's row count and head count are multiples of 4).
+  const uint32_t j0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4u + (threadIdx.x >> 6)) * 4u);
+  if (j0 >= (uint32_t)a.jall) return;
+  const int hsub = lane >> 4;      // the lane's row of the wave's 4
   const int c8 = 8 * (lane & 15);  // this lane's 8 dims
   const int n = a.P + a.R;
-  if (j0 < a.jk) {
+  const uint32_t jq = (uint32_t)a.jq, jk = (uint32_t)a.jk, jv = (uint32_t)a.jv, jp = (uint32_t)a.jp;
+  if (j0 < jk) {
     // normalise + rotate: q rows, then the new K rows
-    const bool isq = j0 < a.jq;
-    const int H = isq ? a.Hq : a.Hkv;
-    const int64_t jj = isq ? j : j - a.jq;
-    const int h = (int)(jj % H);
-    const int t = (int)((jj / H) % a.R);
-    const int64_t sq = jj / ((int64_t)H * a.R);
+    const bool isq = j0 < jq;
+    const uint32_t H = isq ? a.Hq : a.Hkv;
+    const uint32_t jj = isq ? j0 : j0 - jq, ht = jj / H;
+    const int h = (int)(jj - ht * H) + hsub;
+    const int t = (int)(ht % (uint32_t)a.R);
+    const int64_t sq = ht / (uint32_t)a.R;
     const uint4 x = isq ? ld16(a.q + sq * a.q_ss + (int64_t)t * a.q_st + (int64_t)h * a.q_sh + c8)
                         : ld16(a.k + sq * a.k_ss + (int64_t)t * a.k_st + (int64_t)h * a.k_sh + c8);
     const uint4 w = ld16((isq ? a.qn : a.kn) + c8);
@@ -763,19 +857,19 @@ __global__ __launch_bounds__(256) void admit_prep_kernel(const AdmitPrepArgs a) 
       st16(a.qo + ((sq * a.R + t) * a.Hq + h) * kD + c8, y);
     else
       st16(a.ko + ((sq * n + a.P + t) * a.Hkv + h) * kD + c8, y);
-  } else if (j0 < a.jv) {
-    const int64_t jj = j - a.jk;  // new V rows
-    const int h = (int)(jj % a.Hkv);
-    const int t = (int)((jj / a.Hkv) % a.R);
-    const int64_t sq = jj / ((int64_t)a.Hkv * a.R);
+  } else if (j0 < jv) {
+    const uint32_t jj = j0 - jk, ht = jj / (uint32_t)a.Hkv;  // new V rows
+    const int h = (int)(jj - ht * a.Hkv) + hsub;
+    const int t = (int)(ht % (uint32_t)a.R);
+    const int64_t sq = ht / (uint32_t)a.R;
     st16(a.vo + ((sq * n + a.P + t) * a.Hkv + h) * kD + c8,
          ld16(a.v + sq * a.v_ss + (int64_t)t * a.v_st + (int64_t)h * a.v_sh + c8));
   } else {
-    const bool isk = j0 < a.jp;   // prefix K rows, then prefix V rows
-    const int64_t jj = isk ? j - a.jv : j - a.jp;
-    const int h = (int)(jj % a.Hkv);
-    const int r = (int)((jj / a.Hkv) % a.P);
-    const int64_t sq = jj / ((int64_t)a.Hkv * a.P);
+    const bool isk = j0 < jp;   // prefix K rows, then prefix V rows
+    const uint32_t jj = isk ? j0 - jv : j0 - jp, hr = jj / (uint32_t)a.Hkv;
+    const int h = (int)(jj - hr * a.Hkv) + hsub;
+    const int r = (int)(hr % (uint32_t)a.P);
+    const int64_t sq = hr / (uint32_t)a.P;
     const int64_t src = a.pidx != nullptr ? a.pidx[sq] : sq;
     uint4 x = make_uint4(0u, 0u, 0u, 0u);
     if ((uint64_t)src < (uint64_t)a.npre)
@@ -845,12 +939,15 @@ static int launch(const PrefillArgs& args, int num_seqs, int max_seqlen_q, void*
   const int ngroups = (num_seqs + (1 << a.grp_shift) - 1) >> a.grp_shift;
   const bool grouped = (int64_t)num_seqs * nqt * a.hkv > 3 * resident_slots() && ngroups > 1 &&
                        (int64_t)ngroups * nqt <= 65535;
-  if (grouped)
-    hipLaunchKernelGGL(prefill_kernel<true>, dim3((1u << a.grp_shift) * a.hkv, 1, ngroups * nqt), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
-  else
-    hipLaunchKernelGGL(prefill_kernel<false>, dim3(num_seqs * a.hkv, 1, nqt), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
+  const dim3 ggrid((1u << a.grp_shift) * a.hkv, 1, ngroups * nqt), grid(num_seqs * a.hkv, 1, nqt);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a.qn != nullptr) {
+    if (grouped) hipLaunchKernelGGL((prefill_kernel<true, true>), ggrid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((prefill_kernel<false, true>), grid, dim3(256), 0, st, a);
+  } else {
+    if (grouped) hipLaunchKernelGGL((prefill_kernel<true, false>), ggrid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, dim3(256), 0, st, a);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   return Q3A_OK;
@@ -943,15 +1040,15 @@ extern "C" int q3a_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h
   return launch(a, num_seqs, max_seqlen_q, stream, "prefill");
 }
 
-extern "C" int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
-                                  const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v,
-                                  int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_k,
-                                  void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
-                                  int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
-                                  int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_t,
-                                  int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
-                                  int head_dim, float softmax_scale, int causal, void* stream) {
-  const char* who = "prefill_append";
+// q3a_prefill_append with the caller's extra fields in a (the norm/rope-q form's weight and cos/sin tables).
+static int prefill_append_impl(PrefillArgs& a, const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                               const int32_t* cu_seqlens_q, const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                               const void* v, int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_k,
+                               void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                               int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                               int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_t,
+                               int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
+                               int head_dim, float softmax_scale, int causal, void* stream, const char* who) {
   if (num_seqs < 0 || max_seqlen_q < 0) return fail(Q3A_EINVAL, "%s: negative num_seqs/max_seqlen_q", who);
   if (num_seqs == 0 || max_seqlen_q == 0) return Q3A_OK;
   if (!cu_seqlens_q || !cu_seqlens_k) return fail(Q3A_EINVAL, "%s: null pointer argument", who);
@@ -962,7 +1059,6 @@ extern "C" int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_s
                   max_pages_per_seq, head_dim, who);
   if (rc != Q3A_OK) return rc;
 
-  PrefillArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.q_st = q_stride_t;
   a.q_sh = q_stride_h;
@@ -984,6 +1080,22 @@ extern "C" int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_s
   set_pool(a, k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
            bt_stride_b, max_pages_per_seq, -1);
   return launch(a, num_seqs, max_seqlen_q, stream, who);
+}
+
+extern "C" int q3a_prefill_append(const void* q, int64_t q_stride_t, int64_t q_stride_h, const int32_t* cu_seqlens_q,
+                                  const void* k, int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+                                  int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_k,
+                                  void* k_cache, void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
+                                  int64_t kv_stride_head, int num_pages, int page_size, const int32_t* block_table,
+                                  int64_t bt_stride_b, int max_pages_per_seq, void* out, int64_t o_stride_t,
+                                  int64_t o_stride_h, int num_seqs, int max_seqlen_q, int num_q_heads, int num_kv_heads,
+                                  int head_dim, float softmax_scale, int causal, void* stream) {
+  PrefillArgs a{};
+  return prefill_append_impl(a, q, q_stride_t, q_stride_h, cu_seqlens_q, k, k_stride_tok, k_stride_head, v,
+                             v_stride_tok, v_stride_head, cu_seqlens_k, k_cache, v_cache, kv_stride_page, kv_stride_tok,
+                             kv_stride_head, num_pages, page_size, block_table, bt_stride_b, max_pages_per_seq, out,
+                             o_stride_t, o_stride_h, num_seqs, max_seqlen_q, num_q_heads, num_kv_heads, head_dim,
+                             softmax_scale, causal, stream, "prefill_append");
 }
 
 // The dense form with an optional pool write (a.pk set by the caller).
@@ -1099,9 +1211,9 @@ extern "C" int q3a_prefill_dense_append(const void* q, int64_t q_stride_s, int64
 static int launch_prep(const AdmitPrepArgs& p, void* stream, const char* who) {
   // Every job block is a multiple of Hkv rows; with Hkv a multiple of 4 each wave's four rows are of one kind.
   if (p.Hkv % 4 != 0) return fail(Q3A_EINVAL, "%s: num_kv_heads %d must be a multiple of 4", who, p.Hkv);
+  if (p.jall >= ((int64_t)1 << 31)) return fail(Q3A_EINVAL, "%s: grid too large (%lld row jobs)", who, (long long)p.jall);
   const int64_t waves = p.jall / 4;
   const int64_t blocks = (waves + 3) / 4;
-  if (blocks > 0x7fffffff) return fail(Q3A_EINVAL, "%s: grid too large", who);
   if (blocks == 0) return Q3A_OK;
   hipLaunchKernelGGL(admit_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
   const hipError_t e = hipGetLastError();
@@ -1254,8 +1366,10 @@ extern "C" int q3a_prefill_append_rope(
   if (rc != Q3A_OK) return rc;
 
   // The producers over all T tokens as one sequence with no prefix: token t takes rope row t; no V rows (the
-  // attention reads v where it is).
+  // attention reads v where it is).  Causal: k rows only, the attention kernel normalises and rotates q as it loads
+  // it (its pool rows then always go out from the last tiles it streams); otherwise q rows too.
   const int64_t T = total_tokens;
+  const bool q_in_kernel = causal != 0;
   AdmitPrepArgs p{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_stride_t; p.q_sh = q_stride_h;
@@ -1277,16 +1391,25 @@ extern "C" int q3a_prefill_append_rope(
   p.P = 0;
   p.Hq = num_q_heads;
   p.Hkv = num_kv_heads;
-  p.jq = T * num_q_heads;
+  p.jq = q_in_kernel ? 0 : T * num_q_heads;
   p.jk = p.jq + T * num_kv_heads;
   p.jv = p.jk;
   p.jp = p.jv;
   p.jall = p.jv;
   rc = launch_prep(p, stream, who);
   if (rc != Q3A_OK) return rc;
-  return q3a_prefill_append(p.qo, (int64_t)num_q_heads * kD, kD, cu_seqlens, p.ko, (int64_t)num_kv_heads * kD, kD,
-                            v, v_stride_t, v_stride_h, cu_seqlens, k_cache, v_cache, kv_stride_page,
-                            kv_stride_tok, kv_stride_head, num_pages, page_size, block_table, bt_stride_b,
-                            max_pages_per_seq, out, o_stride_t, o_stride_h, num_seqs, max_seqlen, num_q_heads,
-                            num_kv_heads, head_dim, softmax_scale, causal, stream);
+  PrefillArgs a{};
+  if (q_in_kernel) {
+    a.qn = p.qn;
+    a.rcos = p.cs;
+    a.rsin = p.sn;
+    a.rs_st = rope_stride_t;
+    a.eps = eps;
+  }
+  return prefill_append_impl(a, q_in_kernel ? q : p.qo, q_in_kernel ? q_stride_t : (int64_t)num_q_heads * kD,
+                             q_in_kernel ? q_stride_h : kD, cu_seqlens, p.ko, (int64_t)num_kv_heads * kD, kD, v,
+                             v_stride_t, v_stride_h, cu_seqlens, k_cache, v_cache, kv_stride_page, kv_stride_tok,
+                             kv_stride_head, num_pages, page_size, block_table, bt_stride_b, max_pages_per_seq, out,
+                             o_stride_t, o_stride_h, num_seqs, max_seqlen, num_q_heads, num_kv_heads, head_dim,
+                             softmax_scale, causal, stream, who);
 }

@@ -254,9 +254,11 @@ def test_prompt_step_rope_matches_oracle(cuda_device, lens):
     assert np.isnan(kcn[~written]).all() and np.isnan(vcn[~written]).all()
 
 
-def test_prompt_step_rope_matches_torch_producers(cuda_device):
+@pytest.mark.parametrize("causal", [True, False])
+def test_prompt_step_rope_matches_torch_producers(cuda_device, causal):
     """The talker's own sequence on the GPU (engine/talker.py:157-169): eager torch producers, then prefill_append
-    (the fused scatters + attention)."""
+    (the fused scatters + attention).  Causal, q is normalised inside the attention kernel; otherwise by the
+    producer pass with k."""
     dev = cuda_device
     lens = W.prefill_lengths("prefill32")
     q, k, v, qn, kn, cos_t, sin_t, cu = _prompt_inputs(dev, lens, seed=52)
@@ -266,10 +268,11 @@ def test_prompt_step_rope_matches_torch_producers(cuda_device):
     pools = [torch.zeros(2 * n * Pn, 16, 8, D, dtype=torch.bfloat16, device=dev) for _ in range(4)]
     scale = D ** -0.5
     L = int(lens.max())
-    out = q3attn.prefill_append_rope(q, k, v, qn, kn, cos_t, sin_t, cu, L, pools[0], pools[1], bt, scale)
+    print(f"[case] prefill_append_rope vs torch producers, causal={causal}", flush=True)
+    out = q3attn.prefill_append_rope(q, k, v, qn, kn, cos_t, sin_t, cu, L, pools[0], pools[1], bt, scale, causal)
     qe = _eager_norm_rope_torch(q, qn, cos_t, sin_t)
     ke = _eager_norm_rope_torch(k, kn, cos_t, sin_t)
-    ref = q3attn.prefill_append(qe, ke, v, cu, cu, L, pools[2], pools[3], bt, scale, True)
+    ref = q3attn.prefill_append(qe, ke, v, cu, cu, L, pools[2], pools[3], bt, scale, causal)
     torch.cuda.synchronize()
     _assert_last_bit(to_np(pools[0]), to_np(pools[2]), "prompt pool K vs torch producers")
     assert torch.equal(pools[1], pools[3])
