@@ -340,8 +340,9 @@ int q3a_prefill_dense_append_rope(
  * The talker's prompt step with its q/k producers, in two launches (engine/talker.py:157-169): q = rope(rms(q_raw,
  * q_norm_w)) and k = rope(rms(k_raw, k_norm_w)) of every prompt token with the token's own cos/sin row (engine/ops.py:
  * 51-60 as eager bf16 ops: prefill_hidden is not compiled), the index_copy_ pair into the pool (:161-162) and
- * flash_attn_varlen_func(q, k, v, cu, cu, ...) (:169).  The first launch writes the normalised q and k into the
- * workspace, the second is q3a_prefill_append on them and on v where it is (cu_seqlens for both q and k).
+ * flash_attn_varlen_func(q, k, v, cu, cu, ...) (:169).  The first launch writes the normalised k (and, when not
+ * causal, q) into the workspace; the second is q3a_prefill_append's attention on them and on v where it is
+ * (cu_seqlens for both q and k), normalising and rotating the raw q itself when causal.
  *
  *   q          [T, Hq, D] bf16 raw projections of the T = total_tokens packed prompt tokens (q_stride_t/h)
  *   k, v       [T, Hkv, D] bf16 raw keys and the values (their own strides)

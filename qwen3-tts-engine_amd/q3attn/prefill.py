@@ -225,7 +225,8 @@ def prefill_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_nor
     [T, Hkv, D] arrive raw (views of the qkv projection), are RMS-normalised and rotated with each token's cos/sin row
     ([T, D], or [T, 1, D] as the engine gathers them) with the rounding of eager bf16 ops (engine/ops.py:51-60), k and
     v go into the pool at each token's position through block_table [n, max_pages], and the result is
-    flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, ...) over the normalised q and k [T, Hq, D]."""
+    flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, ...) over the normalised q and k [T, Hq, D].  Causal, the
+    first launch normalises k and the attention kernel q; otherwise the first launch normalises both."""
     who = "q3attn.prefill_append_rope"
     _req(q.is_cuda, f"{who}: tensors must be on a GPU (there is no CPU path)")
     dev = q.device
