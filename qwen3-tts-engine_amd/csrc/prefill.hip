@@ -83,6 +83,13 @@ struct PrefillArgs {
   // Norm/rope q (prefill_kernel<*, true>): q arrives raw and is RMS-normalised with qn and rotated with the cos/sin
   // row of its packed token index (row stride rs_st), with the rounding of eager bf16 ops, as it is loaded.
   const uint16_t* qn;
+  const uint16_t* kn;   // the fused admission form (short key ranges): k's weight, then the prefix bank
+  const uint16_t* pfk;
+  const uint16_t* pfv;
+  int64_t pfk_ss, pfk_st, pfk_sh, pfv_ss, pfv_st, pfv_sh;
+  const int64_t* pidx;  // nullptr: sequence s takes prefix s; else prefix pidx[s] (outside [0, npre): zeros)
+  int64_t npre;
+  int P;                // prefix rows; key row j >= P is new row j - P of k/v
   const uint16_t* rcos;
   const uint16_t* rsin;
   int64_t rs_st;
@@ -615,7 +622,7 @@ constexpr int kResMaxTiles = 4;
 constexpr int kResQ = 16;
 constexpr int kResMaxGroups = 16;  // waves per workgroup
 
-template <bool kAppend>
+template <bool kAppend, bool kRope = false>
 __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(const PrefillArgs a, int ntiles) {
   __shared__ __align__(16) uint8_t sK[kResMaxTiles * kTileB];
   __shared__ __align__(16) uint8_t sV[kResMaxTiles * kTileB];
@@ -648,6 +655,12 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
   // Copies: the 16-key groups of K and V (2 per tile and operand) are dealt round-robin to the waves; four
   // direct-to-LDS loads each, same layout and swizzle as the tiled kernel.
   const int ngroups = 4 * ntiles;
+  const int P = kRope ? a.P : 0;  // fused admission form: key rows below P come from the prefix bank
+  int64_t psrc = -1;              // its prefix row (-1: zeros)
+  if constexpr (kRope) {
+    psrc = a.pidx != nullptr ? a.pidx[s] : s;
+    if ((uint64_t)psrc >= (uint64_t)a.npre) psrc = -1;
+  }
   for (int c = wave; c < ngroups; c += nwaves) {
     const int op = c & 1;                       // 0: K, 1: V
     const int grp = c >> 1;                     // 16-key group 0 .. 2 ntiles - 1
@@ -656,28 +669,122 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
     const int64_t sh = op == 0 ? a.k_sh : a.v_sh;
     const int64_t ss = op == 0 ? a.k_ss : a.v_ss;
     const int jg = 16 * grp;
-    const int nv = min(16, Lk - jg);
-    const bool ok = nv > 0;
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (ok ? (int64_t)s * ss + (int64_t)jg * st : 0) + (int64_t)g * sh,
-                                               ok ? (uint32_t)(((nv - 1) * st + kD) * 2) : 0u);
     uint8_t* dst = (op == 0 ? sK : sV) + grp * 16 * kRowB;
+    if constexpr (!kRope) {
+      const int nv = min(16, Lk - jg);
+      const bool ok = nv > 0;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(
+          base + (ok ? (int64_t)s * ss + (int64_t)jg * st : 0) + (int64_t)g * sh,
+          ok ? (uint32_t)(((nv - 1) * st + kD) * 2) : 0u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = 4 * i + (lane >> 4);
-      dma16(r, dst + 4 * i * kRowB, (uint32_t)((rr * st + 8 * ((lane & 15) ^ rr)) * 2));
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 4 * i + (lane >> 4);
+        dma16(r, dst + 4 * i * kRowB, (uint32_t)((rr * st + 8 * ((lane & 15) ^ rr)) * 2));
+      }
+    } else {
+      // Rows jg .. jg + 15 from two sources: prefix rows [jg, min(jg + 16, P)) of the bank's row psrc, new rows
+      // [max(jg, P), min(jg + 16, Lk)) of k/v (row j - P).  Each lane's copy goes through the descriptor of its
+      // row's source, the other copy masked off, so neither writes the other's rows; rows past a source's range
+      // (or a prefix of index -1) arrive as zeros.
+      const uint16_t* pbase = op == 0 ? a.pfk : a.pfv;
+      const int64_t pst = op == 0 ? a.pfk_st : a.pfv_st;
+      const int64_t psh = op == 0 ? a.pfk_sh : a.pfv_sh;
+      const int64_t pss = op == 0 ? a.pfk_ss : a.pfv_ss;
+      const int np = psrc >= 0 ? min(16, P - jg) : 0;
+      const __amdgpu_buffer_rsrc_t rp = make_rsrc(
+          np > 0 ? pbase + psrc * pss + (int64_t)jg * pst + (int64_t)g * psh : base,
+          np > 0 ? (uint32_t)(((np - 1) * pst + kD) * 2) : 0u);
+      const int j1 = max(jg, P);
+      const int nn = min(jg + 16, Lk) - j1;
+      const __amdgpu_buffer_rsrc_t rn = make_rsrc(
+          nn > 0 ? base + (int64_t)s * ss + (int64_t)(j1 - P) * st + (int64_t)g * sh : base,
+          nn > 0 ? (uint32_t)(((nn - 1) * st + kD) * 2) : 0u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 4 * i + (lane >> 4);
+        const int sw = 8 * ((lane & 15) ^ rr);
+        if (jg + rr < P)
+          dma16(rp, dst + 4 * i * kRowB, (uint32_t)((rr * pst + sw) * 2));
+        else
+          dma16(rn, dst + 4 * i * kRowB, (uint32_t)(((jg + rr - j1) * st + sw) * 2));
+      }
     }
   }
   const int tq = tg * kResQ + col;
   const bool qvalid = tq < Lq;
   bf16x8_t qb[4];
+  uint4 qx[4], qw[4], qc[4], qs[4];  // fused admission form: raw q, weight, cos, sin
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     uint4 x = make_uint4(0u, 0u, 0u, 0u);
     if (qvalid) x = ld16(a.q + qbase + (int64_t)tq * a.q_st + (kG * g + hh) * a.q_sh + 32 * kk + 8 * g4);
     qb[kk] = as_bf16x8(x);
+    if constexpr (kRope) {
+      qx[kk] = x;
+      qw[kk] = ld16(a.qn + 32 * kk + 8 * g4);
+      qc[kk] = make_uint4(0u, 0u, 0u, 0u);
+      qs[kk] = qc[kk];
+      if (qvalid) {
+        qc[kk] = ld16(a.rcos + (int64_t)tq * a.rs_st + 32 * kk + 8 * g4);
+        qs[kk] = ld16(a.rsin + (int64_t)tq * a.rs_st + 32 * kk + 8 * g4);
+      }
+    }
   }
   wait_vmem();
   __syncthreads();
+  if constexpr (kRope) {
+    // The new K rows P .. Lk - 1 normalised and rotated in place (engine/ops.py:51-60 as eager bf16 ops, token
+    // j - P's cos/sin row), 16 lanes per row: lane chunk c of row r sits at LDS slot c ^ (r & 15).  Then q, in
+    // registers: the lane holds dims 32 kk + 8 g4 .. +8 of its token, so the mean of squares is an in-lane sum and
+    // two lane swaps, and the rotate-half partner of chunk kk is chunk kk ^ 2.
+    const int ch = lane & 15;
+    for (int gi = (P >> 2) + wave; 4 * gi < Lk; gi += nwaves) {
+      const int r = 4 * gi + (lane >> 4);   // < 4 ceil(Lk / 4) <= 128 rows of sK
+      const int t = min(max(r - P, 0), Lq - 1);
+      uint8_t* p = sK + r * kRowB + ((ch ^ (r & 15)) << 4);
+      const uint4 y = qk_norm_rope16_eager(ld16(p), ld16(a.kn + 8 * ch), ld16(a.rcos + (int64_t)t * a.rs_st + 8 * ch),
+                                           ld16(a.rsin + (int64_t)t * a.rs_st + 8 * ch), a.eps);
+      if (r >= P && r < Lk) st16(p, y);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint32_t xs[4] = {qx[kk].x, qx[kk].y, qx[kk].z, qx[kk].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss += bf16_lo(xs[i]) * bf16_lo(xs[i]) + bf16_hi(xs[i]) * bf16_hi(xs[i]);
+    }
+    const float rq = rms_rsqrt(sum_xor32(sum_xor16(ss)), a.eps);
+#pragma unroll
+    for (int kp = 0; kp < 2; ++kp) {
+      const uint32_t xl[4] = {qx[kp].x, qx[kp].y, qx[kp].z, qx[kp].w};
+      const uint32_t xh[4] = {qx[kp + 2].x, qx[kp + 2].y, qx[kp + 2].z, qx[kp + 2].w};
+      const uint32_t wl[4] = {qw[kp].x, qw[kp].y, qw[kp].z, qw[kp].w};
+      const uint32_t wh[4] = {qw[kp + 2].x, qw[kp + 2].y, qw[kp + 2].z, qw[kp + 2].w};
+      const uint32_t cl[4] = {qc[kp].x, qc[kp].y, qc[kp].z, qc[kp].w};
+      const uint32_t chh[4] = {qc[kp + 2].x, qc[kp + 2].y, qc[kp + 2].z, qc[kp + 2].w};
+      const uint32_t sl[4] = {qs[kp].x, qs[kp].y, qs[kp].z, qs[kp].w};
+      const uint32_t sh[4] = {qs[kp + 2].x, qs[kp + 2].y, qs[kp + 2].z, qs[kp + 2].w};
+      uint32_t ol[4], oh[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float el[2], eh[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          auto half = [h2](uint32_t v) { return h2 ? bf16_hi(v) : bf16_lo(v); };
+          const float yl = round_bf16(half(wl[i]) * round_bf16(half(xl[i]) * rq));
+          const float yh = round_bf16(half(wh[i]) * round_bf16(half(xh[i]) * rq));
+          el[h2] = round_bf16(yl * half(cl[i])) + round_bf16(-yh * half(sl[i]));
+          eh[h2] = round_bf16(yh * half(chh[i])) + round_bf16(yl * half(sh[i]));
+        }
+        ol[i] = pack_bf16x2(el[0], el[1]);
+        oh[i] = pack_bf16x2(eh[0], eh[1]);
+      }
+      qb[kp] = as_bf16x8(make_uint4(ol[0], ol[1], ol[2], ol[3]));
+      qb[kp + 2] = as_bf16x8(make_uint4(oh[0], oh[1], oh[2], oh[3]));
+    }
+    wait_vmem();
+    __syncthreads();
+  }
   if (app) {
     // Rows go out in aligned groups of 4 (lane: row 4 gi + lane / 16, chunk lane % 16), group gi to wave gi mod
     // nwaves.  A group never straddles a page (pages hold >= 16 rows), so its page id is wave-uniform: one
@@ -1148,7 +1255,11 @@ static int prefill_dense_impl(PrefillArgs& a, const void* q, int64_t q_stride_s,
                   num_kv_heads, nblk);
     // The append form is its own instantiation: its store loop changes the plain kernel's schedule (5.36 -> 5.87 us
     // on the admission shape when shared).  With fewer than 16 query groups it runs one extra wave for the stores.
-    if (a.pk != nullptr)
+    if (a.kn != nullptr)
+      hipLaunchKernelGGL((prefill_resident_kernel<true, true>), dim3(num_seqs * num_kv_heads, 1, 2 * nblk),
+                         dim3(64 * (waves + (ngroups < kResMaxGroups ? 1 : 0))), 0, static_cast<hipStream_t>(stream),
+                         a, ntiles);
+    else if (a.pk != nullptr)
       hipLaunchKernelGGL(prefill_resident_kernel<true>, dim3(num_seqs * num_kv_heads, 1, 2 * nblk),
                          dim3(64 * (waves + (ngroups < kResMaxGroups ? 1 : 0))), 0, static_cast<hipStream_t>(stream),
                          a, ntiles);
@@ -1281,6 +1392,30 @@ extern "C" int q3a_prefill_dense_append_rope(
 
   const int n = prefix_len + seqlen_q;
   const int64_t S = num_seqs;
+  if (n <= kResMaxTiles * kKT) {
+    // Short key range (the admission shape): one launch.  The resident kernel copies the prefix rows from the bank
+    // and the new rows from k/v, normalises and rotates the new K rows in LDS and q in registers, then stores the
+    // pool rows and attends; the workspace is not used.
+    PrefillArgs a{};
+    set_pool(a, k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
+             bt_stride_b, max_pages_per_seq, first_row);
+    a.qn = static_cast<const uint16_t*>(q_norm_w);
+    a.kn = static_cast<const uint16_t*>(k_norm_w);
+    a.rcos = static_cast<const uint16_t*>(cos);
+    a.rsin = static_cast<const uint16_t*>(sin);
+    a.rs_st = rope_stride_t;
+    a.eps = eps;
+    a.pfk = static_cast<const uint16_t*>(prefix_k);
+    a.pfv = static_cast<const uint16_t*>(prefix_v);
+    a.pfk_ss = pk_stride_s; a.pfk_st = pk_stride_t; a.pfk_sh = pk_stride_h;
+    a.pfv_ss = pv_stride_s; a.pfv_st = pv_stride_t; a.pfv_sh = pv_stride_h;
+    a.pidx = prefix_index;
+    a.npre = prefix_index != nullptr ? num_prefixes : S;
+    a.P = prefix_len;
+    return prefill_dense_impl(a, q, q_stride_s, q_stride_t, q_stride_h, k, k_stride_s, k_stride_t, k_stride_h, v,
+                              v_stride_s, v_stride_t, v_stride_h, out, o_stride_s, o_stride_t, o_stride_h, num_seqs,
+                              seqlen_q, n, num_q_heads, num_kv_heads, head_dim, softmax_scale, causal, stream, who);
+  }
   AdmitPrepArgs p{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_ss = q_stride_s; p.q_st = q_stride_t; p.q_sh = q_stride_h;
