@@ -622,8 +622,14 @@ constexpr int kResMaxTiles = 4;
 constexpr int kResQ = 16;
 constexpr int kResMaxGroups = 16;  // waves per workgroup
 
+// The fused admission form (kRope) runs at most kResRopeWaves waves per workgroup (7 query groups + the store wave):
+// with 64 KiB of LDS per workgroup two fit a CU whatever the bound, and the lower bound leaves room in the registers
+// for its prologue loads.
+constexpr int kResRopeWaves = 8;
+
 template <bool kAppend, bool kRope = false>
-__global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(const PrefillArgs a, int ntiles) {
+__global__ __launch_bounds__(64 * (kRope ? kResRopeWaves : kResMaxGroups)) void prefill_resident_kernel(
+    const PrefillArgs a, int ntiles) {
   __shared__ __align__(16) uint8_t sK[kResMaxTiles * kTileB];
   __shared__ __align__(16) uint8_t sV[kResMaxTiles * kTileB];
 
@@ -682,18 +688,10 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
         dma16(r, dst + 4 * i * kRowB, (uint32_t)((rr * st + 8 * ((lane & 15) ^ rr)) * 2));
       }
     } else {
-      // Rows jg .. jg + 15 from two sources: prefix rows [jg, min(jg + 16, P)) of the bank's row psrc, new rows
-      // [max(jg, P), min(jg + 16, Lk)) of k/v (row j - P).  Each lane's copy goes through the descriptor of its
-      // row's source, the other copy masked off, so neither writes the other's rows; rows past a source's range
-      // (or a prefix of index -1) arrive as zeros.
-      const uint16_t* pbase = op == 0 ? a.pfk : a.pfv;
-      const int64_t pst = op == 0 ? a.pfk_st : a.pfv_st;
-      const int64_t psh = op == 0 ? a.pfk_sh : a.pfv_sh;
-      const int64_t pss = op == 0 ? a.pfk_ss : a.pfv_ss;
-      const int np = psrc >= 0 ? min(16, P - jg) : 0;
-      const __amdgpu_buffer_rsrc_t rp = make_rsrc(
-          np > 0 ? pbase + psrc * pss + (int64_t)jg * pst + (int64_t)g * psh : base,
-          np > 0 ? (uint32_t)(((np - 1) * pst + kD) * 2) : 0u);
+      // Rows jg .. jg + 15 from two sources: new rows [max(jg, P), min(jg + 16, Lk)) of k/v (row j - P) here, prefix
+      // rows [jg, min(jg + 16, P)) of the bank's row psrc after the q loads (below), once the bank index has arrived.
+      // Each lane's copy goes through the descriptor of its row's source, the other masked off, so neither writes
+      // the other's rows; rows past a source's range (or a prefix of index -1) arrive as zeros.
       const int j1 = max(jg, P);
       const int nn = min(jg + 16, Lk) - j1;
       const __amdgpu_buffer_rsrc_t rn = make_rsrc(
@@ -702,11 +700,8 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int rr = 4 * i + (lane >> 4);
-        const int sw = 8 * ((lane & 15) ^ rr);
-        if (jg + rr < P)
-          dma16(rp, dst + 4 * i * kRowB, (uint32_t)((rr * pst + sw) * 2));
-        else
-          dma16(rn, dst + 4 * i * kRowB, (uint32_t)(((jg + rr - j1) * st + sw) * 2));
+        if (jg + rr >= P)
+          dma16(rn, dst + 4 * i * kRowB, (uint32_t)(((jg + rr - j1) * st + 8 * ((lane & 15) ^ rr)) * 2));
       }
     }
   }
@@ -730,6 +725,39 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
       }
     }
   }
+  // Fused admission form: the weight and cos/sin chunks of the first kPf K-row groups this wave normalises (group
+  // gi = P / 4 + wave + i nwaves, row 4 gi + lane / 16), loaded beside the copies.
+  constexpr int kPf = kRope ? 3 : 1;
+  uint4 kw, kc[kPf], ks[kPf];
+  if constexpr (kRope) {
+    kw = ld16(a.kn + 8 * (lane & 15));
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) {
+      const int r = 4 * ((P >> 2) + wave + i * nwaves) + (lane >> 4);
+      const int t = min(max(r - P, 0), Lq - 1);
+      kc[i] = ld16(a.rcos + (int64_t)t * a.rs_st + 8 * (lane & 15));
+      ks[i] = ld16(a.rsin + (int64_t)t * a.rs_st + 8 * (lane & 15));
+    }
+    // The prefix rows' copies (16-key groups below P), same assignment of groups to waves as above.
+    for (int c = wave; c < ngroups && 16 * (c >> 1) < P; c += nwaves) {
+      const int op = c & 1;
+      const int jg = 16 * (c >> 1);
+      const uint16_t* pbase = op == 0 ? a.pfk : a.pfv;
+      const int64_t pst = op == 0 ? a.pfk_st : a.pfv_st;
+      const int64_t psh = op == 0 ? a.pfk_sh : a.pfv_sh;
+      const int64_t pss = op == 0 ? a.pfk_ss : a.pfv_ss;
+      const int np = psrc >= 0 ? min(16, P - jg) : 0;
+      const __amdgpu_buffer_rsrc_t rp = make_rsrc(
+          np > 0 ? pbase + psrc * pss + (int64_t)jg * pst + (int64_t)g * psh : a.k,
+          np > 0 ? (uint32_t)(((np - 1) * pst + kD) * 2) : 0u);
+      uint8_t* dst = (op == 0 ? sK : sV) + (c >> 1) * 16 * kRowB;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 4 * i + (lane >> 4);
+        if (jg + rr < P) dma16(rp, dst + 4 * i * kRowB, (uint32_t)((rr * pst + 8 * ((lane & 15) ^ rr)) * 2));
+      }
+    }
+  }
   wait_vmem();
   __syncthreads();
   if constexpr (kRope) {
@@ -738,11 +766,20 @@ __global__ __launch_bounds__(64 * kResMaxGroups) void prefill_resident_kernel(co
     // registers: the lane holds dims 32 kk + 8 g4 .. +8 of its token, so the mean of squares is an in-lane sum and
     // two lane swaps, and the rotate-half partner of chunk kk is chunk kk ^ 2.
     const int ch = lane & 15;
-    for (int gi = (P >> 2) + wave; 4 * gi < Lk; gi += nwaves) {
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) {
+      const int gi = (P >> 2) + wave + i * nwaves;
+      if (4 * gi >= Lk) break;              // wave-uniform
       const int r = 4 * gi + (lane >> 4);   // < 4 ceil(Lk / 4) <= 128 rows of sK
+      uint8_t* p = sK + r * kRowB + ((ch ^ (r & 15)) << 4);
+      const uint4 y = qk_norm_rope16_eager(ld16(p), kw, kc[i], ks[i], a.eps);
+      if (r >= P && r < Lk) st16(p, y);
+    }
+    for (int gi = (P >> 2) + wave + kPf * nwaves; 4 * gi < Lk; gi += nwaves) {
+      const int r = 4 * gi + (lane >> 4);
       const int t = min(max(r - P, 0), Lq - 1);
       uint8_t* p = sK + r * kRowB + ((ch ^ (r & 15)) << 4);
-      const uint4 y = qk_norm_rope16_eager(ld16(p), ld16(a.kn + 8 * ch), ld16(a.rcos + (int64_t)t * a.rs_st + 8 * ch),
+      const uint4 y = qk_norm_rope16_eager(ld16(p), kw, ld16(a.rcos + (int64_t)t * a.rs_st + 8 * ch),
                                            ld16(a.rsin + (int64_t)t * a.rs_st + 8 * ch), a.eps);
       if (r >= P && r < Lk) st16(p, y);
     }
@@ -1392,7 +1429,7 @@ extern "C" int q3a_prefill_dense_append_rope(
 
   const int n = prefix_len + seqlen_q;
   const int64_t S = num_seqs;
-  if (n <= kResMaxTiles * kKT) {
+  if (n <= kResMaxTiles * kKT && (seqlen_q + kResQ - 1) / kResQ + 1 <= kResRopeWaves) {
     // Short key range (the admission shape): one launch.  The resident kernel copies the prefix rows from the bank
     // and the new rows from k/v, normalises and rotates the new K rows in LDS and q in registers, then stores the
     // pool rows and attends; the workspace is not used.
