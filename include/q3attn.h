@@ -301,12 +301,15 @@ int q3a_prefill_dense_append(const void* q, int64_t q_stride_s, int64_t q_stride
                              int causal, void* stream);
 
 /*
- * The fast-admission layer's attention block in two launches on the caller's stream (engine/arrivals.py:112-118 and
+ * The fast-admission layer's attention block on the caller's stream (engine/arrivals.py:112-118 and
  * 144-148): the producers q = rope(rms(q_raw, q_norm_w)), k = rope(rms(k_raw, k_norm_w)) (engine/ops.py:51-60,
  * evaluated with the rounding of eager bf16 ops: every op rounds to bf16), K = cat(prefix_k, k), V = cat(prefix_v, v)
  * (engine/arrivals.py:118), the two index_copy_ scatters of K and V into the pool (:144-145) and the attention
- * flash_attn_func(q, K, V, causal) (:148).  The first launch writes q, K and V into the workspace; the second is
- * q3a_prefill_dense_append on them (rows first_row .. n-1 into the pool, n = prefix_len + seqlen_q).
+ * flash_attn_func(q, K, V, causal) (:148).  With n = prefix_len + seqlen_q <= 128 and seqlen_q <= 112 (the
+ * admission shape) it is one launch: the attention kernel copies the prefix and new K/V rows from where they are,
+ * normalises and rotates the new K rows and q itself, and stores rows first_row .. n-1 into the pool; the workspace
+ * is not used.  Otherwise two: the first writes q, K and V into the workspace, the second is
+ * q3a_prefill_dense_append on them.
  *
  *   q          [S, R, Hq, D] bf16 raw projections (strides q_stride_s/t/h; a view of the qkv output is fine)
  *   k, v       [S, R, Hkv, D] bf16 raw new keys and the new values (their own strides)

@@ -1404,6 +1404,7 @@ extern "C" int q3a_prefill_dense_append_rope(
   if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
   if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
     return fail(Q3A_EINVAL, "%s: num_q_heads %d must be %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
+  if (num_kv_heads % 4 != 0) return fail(Q3A_EINVAL, "%s: num_kv_heads %d must be a multiple of 4", who, num_kv_heads);
   if (!q || !k || !v || !q_norm_w || !k_norm_w || !cos || !sin || !out || !workspace ||
       (prefix_len > 0 && (!prefix_k || !prefix_v)))
     return fail(Q3A_EINVAL, "%s: null pointer argument", who);

@@ -285,7 +285,8 @@ def prefill_dense_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               block_table: torch.Tensor, softmax_scale: float,
                               prefix_index: Optional[torch.Tensor] = None, causal: bool = True, eps: float = 1e-6,
                               first_row: int = 0) -> torch.Tensor:
-    """The fast-admission layer's attention block (engine/arrivals.py:112-118, 144-148) in two launches: q and the
+    """The fast-admission layer's attention block (engine/arrivals.py:112-118, 144-148), one launch when P + R <= 128
+    and R <= 112, else two: q and the
     new k arrive raw (views of the qkv projection [S, R, ...]) and are RMS-normalised and rotated with the new tokens'
     cos/sin rows ([R, D], or any view with R*D elements and a contiguous last dim such as [1, R, 1, D]), with the
     rounding of eager bf16 torch ops (engine/ops.py:51-60); K = cat(prefix_k, k) and V = cat(prefix_v, v) with
