@@ -88,6 +88,8 @@ def _assert_last_bit(a, b, what, frac=2e-3):
     (8, 42, 35, 16, 35, True),      # prefix already in the pool: the new rows only
     (4, 42, 35, 256, 0, False),     # the reference's 256-token pages, one prefix per sequence
     (3, 20, 0, 16, 0, False),       # no prefix
+    (5, 70, 50, 16, 3, True),       # one launch, 5 query groups, part of the prefix into the pool
+    (2, 120, 5, 16, 0, True),       # 125 keys but 8 query groups: the two-launch form on the short-key kernel
     (2, 100, 200, 16, 0, True),     # 300 keys: the tiled attention kernel
     (2, 40, 660, 32, 600, True),    # tiled, part of a long prefix
 ])
