@@ -260,24 +260,28 @@ def decode_kernel_name(wl, split):
     from q3attn import _lib
 
     L = wl.layers[0]
-    ws = _lib.lib().q3a_paged_decode_workspace_bytes(wl.batch, 16, wl.k_cache.shape[2], 128,
-                                                     L.block_table.shape[1], wl.page_size, split)
-    if split:
+    lib = _lib.lib()
+    ws = lambda code: lib.q3a_paged_decode_workspace_bytes(wl.batch, 16, wl.k_cache.shape[2], 128,
+                                                           L.block_table.shape[1], wl.page_size, code)
+    if split > 0:
         return "paged decode call (fixed-split decode kernel + combine kernel)"
-    if ws == 0:
+    if split == -1 or (split == 0 and ws(0) == 0):
         return "paged decode call (row-parallel kernel, one launch)"
+    if split == -2 or (split == 0 and ws(0) == ws(-2)):
+        return "paged decode call (chunked decode kernel + chunk combine kernel)"
     return "paged decode call (stream-K decode kernel + combine kernel)"
 
 
-SMALL_SHAPES = ((1, 64), (1, 256), (1, 1024), (1, 1800), (4, 1024), (8, 512), (16, 1024), (16, 1800), (32, 512),
-                (32, 1024), (32, 1800), (64, 256), (64, 512), (64, 1024))
+SMALL_SHAPES = ((1, 64), (1, 256), (1, 1024), (1, 1800), (2, 1800), (4, 1024), (4, 1800), (8, 512), (8, 1800),
+                (16, 1024), (16, 1800), (32, 512), (32, 1024), (32, 1800), (64, 256), (64, 512), (64, 1024))
+SMALL_PATHS = (("row_parallel", -1), ("chunks", -2), ("stream_k", -3), ("auto", 0))
 
 
 def bench_decode_small(args, dev):
     """Decode at small batches: every row of B rows at the same context length, 28 layer calls per graph replay
-    over one pool with per-layer random tables.  Each shape runs twice on the same pages: with a 2,048-token table
-    (the row-parallel kernel, the library's choice up to 64 rows) and with a 2,064-token table (past that kernel's
-    limit: stream-K decode + combine)."""
+    over one pool with per-layer random 2,048-token tables.  Each shape runs through each kernel (the path codes
+    force one: the row-parallel kernel, the chunked kernel + its combine, stream-K + its combine) and through the
+    library's own choice (`auto`, the headline value)."""
     import numpy as np
     import torch
 
@@ -287,24 +291,24 @@ def bench_decode_small(args, dev):
     shapes = {}
     for B, ctx in SMALL_SHAPES:
         res = {}
-        for path, max_ctx in (("row_parallel", 2048), ("stream_k", 2064)):
-            wl = W.make_decode("small", dev, ctx=np.full(B, ctx), num_pages=max(256, B * 130 * 2), max_ctx=max_ctx,
-                               layers=LAYERS, seed=args.seed + 1)
+        wl = W.make_decode("small", dev, ctx=np.full(B, ctx), num_pages=max(256, B * 130 * 2), max_ctx=2048,
+                           layers=LAYERS, seed=args.seed + 1)
+        for path, code in SMALL_PATHS:
             _, frame_ms, _ = time_graph(dev, lambda: [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens,
-                                                                          L.block_table, wl.scale, 0)
+                                                                          L.block_table, wl.scale, code)
                                                       for L in wl.layers], args.steps, args.warmup)
             res[path] = round(statistics.median(frame_ms) * 1e3 / LAYERS, 2)
-            res[path + "_kernel"] = decode_kernel_name(wl, 0)
-            del wl
-            torch.cuda.empty_cache()
+        res["auto_kernel"] = decode_kernel_name(wl, 0)
+        del wl
+        torch.cuda.empty_cache()
         shapes[f"{B}x{ctx}"] = res
-        log(f"[bench] small batch {B} x {ctx}: row-parallel {res['row_parallel']:.2f} us/call, "
-            f"stream-K {res['stream_k']:.2f} us/call")
-    mean_row = statistics.mean(r["row_parallel"] for r in shapes.values())
-    rec = base_record("paged decode attn µs/call at small batches (mean over shapes), 1×MI355X", round(mean_row, 2),
-                      "us/call", args, mean_row * LAYERS / 1e3, False, {
+        log(f"[bench] small batch {B} x {ctx}: row-parallel {res['row_parallel']:.2f}, chunks {res['chunks']:.2f}, "
+            f"stream-K {res['stream_k']:.2f}, auto {res['auto']:.2f} us/call ({res['auto_kernel']})")
+    mean_auto = statistics.mean(r["auto"] for r in shapes.values())
+    rec = base_record("paged decode attn µs/call at small batches (mean over shapes), 1×MI355X", round(mean_auto, 2),
+                      "us/call", args, mean_auto * LAYERS / 1e3, False, {
                           "workload": "talker paged decode attention at 1-64 rows of 64-1,800 tokens each, GQA 16/8, "
-                                      "head_dim 128, bf16, 16-token pages, 28 layer calls per step",
+                                      "head_dim 128, bf16, 16-token pages, 2,048-token tables, 28 layer calls per step",
                           "shapes": [f"{B}x{c}" for B, c in SMALL_SHAPES], "parallelism": "single GPU"})
     rec["per_shape_us_per_call"] = shapes
     return rec

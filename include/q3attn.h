@@ -28,8 +28,22 @@ extern "C" {
 /* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
  * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope.
  * 5: q3a_prefill_dense_append.  6: q3a_prefill_dense_append_rope, q3a_prefill_append_rope,
- * q3a_cp_attn_append_rope. */
-#define Q3A_ABI_VERSION 6
+ * q3a_cp_attn_append_rope.  7: the decode path codes below (negative split_tokens). */
+#define Q3A_ABI_VERSION 7
+
+/* Decode decomposition codes, passed as split_tokens to the q3a_paged_decode* entry points (0 lets the library
+ * choose, a positive multiple of 16 is a fixed split of that many tokens):
+ *   Q3A_DECODE_ROW      one workgroup per (row, KV head), the row's tiles over its waves, one launch (tables of at
+ *                       most 2,048 tokens)
+ *   Q3A_DECODE_CHUNKS   the same kernel over chunks of 128 or more tokens of each row, so one row's tiles spread
+ *                       over many workgroups, then a combine launch that merges the chunks' fp32 (m, l, o) records
+ *                       (small batches of long rows; tables of at most 131,072 tokens)
+ *   Q3A_DECODE_STREAMK  stream-K: a resident grid over all rows' 16-token tiles, then a combine (batch <= 4096)
+ * A code that does not take the shape returns Q3A_EINVAL.  Every decomposition computes the same attention; they
+ * differ in the order of the fp32 reductions. */
+#define Q3A_DECODE_ROW (-1)
+#define Q3A_DECODE_CHUNKS (-2)
+#define Q3A_DECODE_STREAMK (-3)
 int q3a_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -55,10 +69,13 @@ const char* q3a_last_error(void);
  * Query head h reads KV head h / (Hq/Hkv).  softmax is float32.  Rows with ctx <= 0 produce zeros;
  * ctx is clamped to max_pages_per_seq*page_size; a page index outside [0, num_pages) contributes
  * no tokens.  Requirements: D == 128, Hq == 2*Hkv, 1 <= Hkv <= 16, page_size % 16 == 0,
- * 16-byte aligned rows.  split_tokens == 0 selects the stream-K decomposition (a persistent grid
- * sized to the device, balanced over all rows' 16-token tiles; batch <= 4096, larger batches fall
- * back to q3a_paged_decode_default_split()); split_tokens > 0 (a multiple of 16, <= 1024) selects
- * one workgroup per (row, split of that many tokens).
+ * 16-byte aligned rows.  split_tokens == 0 lets the library choose the decomposition from the batch and
+ * the table capacity max_pages_per_seq*page_size (never from the device-resident lengths): tables of at most
+ * 128 tokens and batches of at most 64 rows with tables of at most 2,048 tokens take Q3A_DECODE_ROW, except
+ * batches of at most 16 rows with tables of 256 tokens or more, which take Q3A_DECODE_CHUNKS; larger batches
+ * take stream-K (a persistent grid sized to the device, balanced over all rows' 16-token tiles; batch <= 4096,
+ * larger batches fall back to q3a_paged_decode_default_split()).  The path codes above force one of them;
+ * split_tokens > 0 (a multiple of 16, <= 1024) selects one workgroup per (row, split of that many tokens).
  */
 int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      const void* k_cache, const void* v_cache, int64_t kv_stride_page,

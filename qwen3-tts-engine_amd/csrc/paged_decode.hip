@@ -905,6 +905,14 @@ constexpr int kRowRec = kG * kD + 2 * kG;  // floats per wave state: acc[kG][kD]
 // followed by the plain form).
 constexpr int row_max_waves(bool multi) { return multi ? kRowMaxWaves / 2 : kRowMaxWaves; }
 
+//
+// Chunked (split-KV) form, for small batches of long rows: the grid gets a third dimension, chunk c of
+// CT = W * row_per consecutive tiles, so one row's tiles spread over up to kChunkMax workgroups per KV head
+// instead of the W waves of one CU.  Wave w takes tiles c*CT + w + i*W.  A row whose tiles fit one chunk is
+// written directly by its chunk-0 workgroup; otherwise every chunk holding tiles of the row writes its merged
+// state (fp32 o = sum p.v, m, l of both query heads) as a record, which paged_decode_chunk_combine_kernel merges.
+constexpr int kChunkMax = 16;  // records per (row, KV head): the combine loads them all at once
+
 template <bool kAppend, bool kMulti, bool kRope = false>
 __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_kernel(const DecodeArgs a) {
   static_assert(kAppend || !kRope, "the norm/rope form is an append form");
@@ -917,9 +925,11 @@ __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_k
   const int lane = threadIdx.x & 63;
   const int grp = lane >> 4;
   const int dl = (lane & 15) * 8;
+  const int CT = W * a.row_per;              // tiles per chunk (the one-launch path: the whole table)
+  const int tb = (int)blockIdx.z * CT;       // first tile of this workgroup's chunk
 
   const int cap = a.max_pages * a.page_size;
-  const int t = kTile * (w + lane * W);      // first token of this lane's tile
+  const int t = kTile * (tb + w + lane * W);  // first token of this lane's tile
   const int pidx = min(t, cap - 1) / a.page_size;
   const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
   uint4 q[kG];
@@ -944,9 +954,14 @@ __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_k
   }
   const int ctx = row_ctx<kAppend>(a, b);
   const int nrow = (ctx + kTile - 1) / kTile;  // tiles of the row
+  const int nch = (nrow + CT - 1) / CT;        // chunks holding tiles of the row
+  // Chunks past the row's end have nothing to do (chunk 0 stays: it writes the zero row of an empty one).  The
+  // condition is uniform over the workgroup.
+  if (blockIdx.z > 0 && (int)blockIdx.z >= nch) return;
+  const int nrc = min(nrow - tb, CT);          // tiles of the row in this chunk
 
   TileList L;
-  L.n = nrow > w ? (nrow - w + W - 1) / W : 0;
+  L.n = nrc > w ? (nrc - w + W - 1) / W : 0;
   L.page = lane < L.n ? page : -1;
   L.off = t - pidx * a.page_size;
   L.nvalid = lane < L.n ? min(kTile, ctx - t) : 0;
@@ -957,7 +972,8 @@ __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_k
 
   // Append form: the row's last tile (this wave's tile jt if it owns it) holds the new token at nvalid - 1; the 16
   // lanes holding it take this step's k/v rows instead of the stale slot, and store them after the loop.
-  const int jt = (kAppend && nrow > 0 && (nrow - 1) % W == w) ? (nrow - 1) / W : -1;
+  const int last = nrow - 1 - tb;  // the row's last tile, counted from this chunk's first
+  const int jt = (kAppend && nrow > 0 && last >= 0 && last < CT && last % W == w) ? last / W : -1;
   auto issue = [&](int j, KVTile& T) {
     issue_tile(a, L, lane_off, grp, j, T);
     __builtin_amdgcn_sched_barrier(0);
@@ -1041,10 +1057,74 @@ __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_k
     o[2] += __uint_as_float(x.z) * wgt;
     o[3] += __uint_as_float(x.w) * wgt;
   }
+  if (nch > 1) {
+    // Chunked form, a row spread over several chunks: this chunk's record, [kG][kD] o then m[kG], l[kG] (fp32).
+    float* r = a.ws + (((int64_t)b * gridDim.z + blockIdx.z) * a.hkv + g) * kRowRec;
+    st16(r + h * kD + d0, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                     __float_as_uint(o[3])));
+    if ((lane & 31) == 0) {
+      r[kG * kD + h] = M;
+      r[kG * kD + kG + h] = Ls;
+    }
+    return;
+  }
   const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
   uint2 ov;
   ov.x = pack_bf16x2(o[0] * inv, o[1] * inv);
   ov.y = pack_bf16x2(o[2] * inv, o[3] * inv);
+  *reinterpret_cast<uint2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0) = ov;
+}
+
+// Chunked form: one wave per (row, KV head) merges the row's chunk records.  Lane l owns query head l/32 and dims
+// 4*(l%32)..+4.  The records of every chunk of the grid are loaded at once, before the row's context is known (the
+// combine is one memory round trip); those of chunks past the row's end are stale and are never used.  Rows held by
+// one chunk were written by the row kernel.
+template <bool kAppend>
+__global__ __launch_bounds__(64) void paged_decode_chunk_combine_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int g = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int h = lane >> 5;
+  const int d0 = (lane & 31) * 4;
+  const int nchg = a.max_splits;  // chunks per row in the grid, <= kChunkMax
+  const float* base = a.ws + ((int64_t)b * nchg * a.hkv + g) * kRowRec;
+  uint4 o[kChunkMax];
+  float mr[kChunkMax], lr[kChunkMax];
+#pragma unroll
+  for (int u = 0; u < kChunkMax; ++u) {
+    o[u] = make_uint4(0u, 0u, 0u, 0u);
+    mr[u] = kMaxSeed;
+    lr[u] = 0.f;
+    if (u < nchg) {
+      const float* r = base + (int64_t)u * a.hkv * kRowRec;
+      o[u] = ld16(r + h * kD + d0);
+      mr[u] = r[kG * kD + h];
+      lr[u] = r[kG * kD + kG + h];
+    }
+  }
+  const int ctx = row_ctx<kAppend>(a, b);
+  const int nch = (ctx + a.split_tokens - 1) / a.split_tokens;
+  if (nch <= 1) return;
+  float M = kMaxSeed;
+#pragma unroll
+  for (int u = 0; u < kChunkMax; ++u)
+    if (u < nch) M = fmaxf(M, mr[u]);
+  float Ls = 0.f, x[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kChunkMax; ++u) {
+    if (u < nch) {
+      const float wgt = fast_exp2(mr[u] - M);
+      Ls += lr[u] * wgt;
+      x[0] += __uint_as_float(o[u].x) * wgt;
+      x[1] += __uint_as_float(o[u].y) * wgt;
+      x[2] += __uint_as_float(o[u].z) * wgt;
+      x[3] += __uint_as_float(o[u].w) * wgt;
+    }
+  }
+  const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+  uint2 ov;
+  ov.x = pack_bf16x2(x[0] * inv, x[1] * inv);
+  ov.y = pack_bf16x2(x[2] * inv, x[3] * inv);
   *reinterpret_cast<uint2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0) = ov;
 }
 
@@ -1096,23 +1176,71 @@ int sk_effective_grid_host(int grid, int64_t nt) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(grid, g));
 }
 
-bool use_sk(int batch, int split_tokens) { return split_tokens == 0 && batch <= kSkMaxRows; }
+// The decompositions of one decode call.  split_tokens == 0 lets choose_path pick; Q3A_DECODE_ROW,
+// Q3A_DECODE_CHUNKS and Q3A_DECODE_STREAMK (negative codes) ask for one; split_tokens > 0 is the fixed split.
+enum class Path { kNone, kRow, kChunks, kStreamK, kFixed };
 
-// The row-parallel path: narrow tables at any batch, and small batches of rows up to 2,048 tokens.
-bool use_row(int batch, int64_t max_ctx, int split_tokens) {
-  if (split_tokens != 0) return false;
+// Chunked form geometry for a table of cap_tiles tiles: W waves of `per` tiles per chunk, nch chunks per row.
+// 128-token chunks (8 waves of one tile) while 16 of them cover the table, then 16 waves of one tile, then 8
+// waves of several tiles (two in flight).  False past 64 tiles per wave.
+bool chunk_geometry(int64_t cap_tiles, int* W, int* per, int* nch) {
+  int w = 8, p = 1;
+  if (cap_tiles > (int64_t)kChunkMax * 8) {
+    if (cap_tiles <= (int64_t)kChunkMax * 16) {
+      w = 16;
+    } else {
+      p = (int)((cap_tiles + kChunkMax * 8 - 1) / (kChunkMax * 8));
+      if (p > 64) return false;
+    }
+  }
+  *W = w;
+  *per = p;
+  *nch = (int)((cap_tiles + (int64_t)w * p - 1) / ((int64_t)w * p));
+  return true;
+}
+
+// Batches up to which long rows take the chunked form, and the table capacity (tiles) from which they do.
+constexpr int kChunkMaxBatch = 16;
+constexpr int kChunkMinTiles = 2 * kMaxRowTiles;
+
+Path choose_path(int batch, int64_t max_ctx, int split_tokens) {
   const int64_t cap_tiles = (max_ctx + kTile - 1) / kTile;
-  return cap_tiles <= kMaxRowTiles || (batch <= kRowMaxBatch && cap_tiles <= kRowMaxWaves * kRowMaxPer);
+  const bool row_ok = cap_tiles <= kRowMaxWaves * kRowMaxPer;
+  int w, p, n;
+  const bool chunk_ok = chunk_geometry(cap_tiles, &w, &p, &n);
+  switch (split_tokens) {
+    case Q3A_DECODE_ROW: return row_ok ? Path::kRow : Path::kNone;
+    case Q3A_DECODE_CHUNKS: return chunk_ok ? Path::kChunks : Path::kNone;
+    case Q3A_DECODE_STREAMK: return batch <= kSkMaxRows ? Path::kStreamK : Path::kNone;
+    case 0: break;
+    default: return split_tokens > 0 ? Path::kFixed : Path::kNone;
+  }
+  // Narrow tables: one launch.  Small batches of long rows: chunks over many CUs.  Up to 64 rows: the row-parallel
+  // kernel.  Beyond: stream-K, and past its row limit the fixed split.
+  if (cap_tiles <= kMaxRowTiles) return Path::kRow;
+  if (batch <= kChunkMaxBatch && cap_tiles >= kChunkMinTiles && chunk_ok) return Path::kChunks;
+  if (batch <= kRowMaxBatch && row_ok) return Path::kRow;
+  if (batch <= kSkMaxRows) return Path::kStreamK;
+  return Path::kFixed;
 }
 
 size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int split_tokens) {
-  if (use_row(batch, (int64_t)max_pages * page_size, split_tokens)) return 0;
-  if (use_sk(batch, split_tokens)) {
-    return align256((size_t)(batch + 1) * sizeof(int)) +
-           (size_t)sk_grid(hkv) * kSkSlots * hkv * kPartFloats * sizeof(float);
+  const int64_t max_ctx = (int64_t)max_pages * page_size;
+  switch (choose_path(batch, max_ctx, split_tokens)) {
+    case Path::kNone:
+    case Path::kRow: return 0;
+    case Path::kChunks: {
+      int w, p, n;
+      chunk_geometry((max_ctx + kTile - 1) / kTile, &w, &p, &n);
+      return n <= 1 ? 0 : (size_t)batch * n * hkv * kRowRec * sizeof(float);
+    }
+    case Path::kStreamK:
+      return align256((size_t)(batch + 1) * sizeof(int)) +
+             (size_t)sk_grid(hkv) * kSkSlots * hkv * kPartFloats * sizeof(float);
+    case Path::kFixed: break;
   }
   if (split_tokens <= 0) split_tokens = default_split(batch, hkv, max_pages, page_size);
-  const int max_splits = ceil_div((int64_t)max_pages * page_size, split_tokens);
+  const int max_splits = ceil_div(max_ctx, split_tokens);
   if (max_splits <= 1) return 0;
   return (size_t)batch * max_splits * hkv * kPartFloats * sizeof(float);
 }
@@ -1180,8 +1308,11 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   if (q_stride_h <= 0 || ((int64_t)(kG - 1) * q_stride_h + head_dim) * 2 >= ((int64_t)1 << 31))
     return fail(Q3A_EINVAL, "%s: q head stride %lld unsupported (need > 0, head pair extent < 2 GiB)", who,
                 (long long)q_stride_h);
-  if (split_tokens < 0 || split_tokens % kTile != 0)
-    return fail(Q3A_EINVAL, "%s: split_tokens %d is not 0 or a positive multiple of %d", who, split_tokens, kTile);
+  const bool path_code =
+      split_tokens == Q3A_DECODE_ROW || split_tokens == Q3A_DECODE_CHUNKS || split_tokens == Q3A_DECODE_STREAMK;
+  if (!path_code && (split_tokens < 0 || split_tokens % kTile != 0))
+    return fail(Q3A_EINVAL, "%s: split_tokens %d is not 0, a path code or a positive multiple of %d", who,
+                split_tokens, kTile);
   if (split_tokens > kMaxSplitTokens)
     return fail(Q3A_EINVAL, "%s: split_tokens %d exceeds %d", who, split_tokens, kMaxSplitTokens);
   const int64_t page_extent =
@@ -1191,27 +1322,38 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
                 (long long)page_extent);
   const int64_t max_ctx = (int64_t)max_pages_per_seq * page_size;
   if (max_ctx > (int64_t)1 << 30) return fail(Q3A_EINVAL, "%s: context capacity too large", who);
+  const int workspace_split = split_tokens;  // the value the caller sized the workspace with
+  const Path path = choose_path(batch, max_ctx, split_tokens);
+  if (path == Path::kNone)
+    return fail(Q3A_EINVAL, "%s: decode path %d does not take this shape (batch %d, table of %lld tokens)", who,
+                split_tokens, batch, (long long)max_ctx);
   // Narrow tables and small batches: one workgroup per (row, KV head) streams the row with up to 16 waves and
   // writes its output, one kernel and no partial records.  Stream-K would cut such rows into short pieces and merge
-  // them in a second kernel, whose launch is most of such a call.
-  const bool row = use_row(batch, max_ctx, split_tokens);
+  // them in a second kernel, whose launch is most of such a call.  Small batches of long rows: the same kernel over
+  // chunks of the row, so the row's tiles spread over many CUs, and a combine.
+  const bool row = path == Path::kRow;
+  const bool chunks = path == Path::kChunks;
   const int cap_tiles = (int)((max_ctx + kTile - 1) / kTile);
-  const int row_waves = std::min(cap_tiles, row_max_waves(cap_tiles > kRowMaxWaves));
+  int row_waves = std::min(cap_tiles, row_max_waves(cap_tiles > kRowMaxWaves)), chunk_per = 1, nchunks = 1;
+  if (chunks) chunk_geometry(cap_tiles, &row_waves, &chunk_per, &nchunks);
   if (row) split_tokens = cap_tiles * kTile;
-  const bool sk = !row && use_sk(batch, split_tokens);
-  if (!sk && split_tokens == 0) split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
-  const int max_splits = sk ? 0 : ceil_div(max_ctx, split_tokens);
-  if (!sk && max_splits > kMaxSplits)
+  if (chunks) split_tokens = row_waves * chunk_per * kTile;
+  const bool sk = path == Path::kStreamK;
+  if (sk) split_tokens = 0;
+  if (path == Path::kFixed && split_tokens == 0)
+    split_tokens = default_split(batch, num_kv_heads, max_pages_per_seq, page_size);
+  const int max_splits = sk ? 0 : (chunks ? nchunks : ceil_div(max_ctx, split_tokens));
+  if (path == Path::kFixed && max_splits > kMaxSplits)
     return fail(Q3A_EINVAL, "%s: %d splits exceed %d (raise split_tokens)", who, max_splits, kMaxSplits);
-  const size_t need = workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, sk ? 0 : split_tokens);
+  const size_t need = workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, workspace_split);
   if (need > 0 && (workspace == nullptr || workspace_bytes_ < need))
     return fail(Q3A_ESPACE, "%s: workspace %zu bytes < %zu needed", who, workspace_bytes_, need);
   if (need > 0 && (uintptr_t)workspace % 16 != 0)
     return fail(Q3A_EINVAL, "%s: workspace must be 16-byte aligned", who);
   if (nr != nullptr) {
     if (!append) return fail(Q3A_EINVAL, "%s: the norm/rope form needs k_new/v_new", who);
-    if (!row && !sk) return fail(Q3A_EINVAL, "%s: the norm/rope form needs split_tokens == 0 and batch <= %d", who,
-                                 kSkMaxRows);
+    if (!row && !sk && !chunks)
+      return fail(Q3A_EINVAL, "%s: the norm/rope form needs split_tokens <= 0 and batch <= %d", who, kSkMaxRows);
     if (sk && num_kv_heads > 8)
       return fail(Q3A_EINVAL, "%s: the norm/rope form supports at most 8 KV heads (got %d)", who, num_kv_heads);
     if (!nr->q_norm_w || !nr->k_norm_w || !nr->cos || !nr->sin)
@@ -1293,9 +1435,9 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   a.grid = 0;
   a.prefix = nullptr;
   a.ws = static_cast<float*>(workspace);
-  if (row) {
-    a.row_per = (cap_tiles + row_waves - 1) / row_waves;
-    const dim3 rgrid(batch, num_kv_heads), rblock(64 * row_waves);
+  if (row || chunks) {
+    a.row_per = chunks ? chunk_per : (cap_tiles + row_waves - 1) / row_waves;
+    const dim3 rgrid(batch, num_kv_heads, chunks ? nchunks : 1), rblock(64 * row_waves);
     if (a.row_per == 1) {
       if (rope)
         hipLaunchKernelGGL((paged_decode_row_kernel<true, false, true>), rgrid, rblock, 0, st, a);
@@ -1313,6 +1455,14 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     }
     e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: row launch failed: %s", who, hipGetErrorString(e));
+    if (chunks && nchunks > 1) {
+      if (append)
+        hipLaunchKernelGGL(paged_decode_chunk_combine_kernel<true>, dim3(batch, num_kv_heads), dim3(64), 0, st, a);
+      else
+        hipLaunchKernelGGL(paged_decode_chunk_combine_kernel<false>, dim3(batch, num_kv_heads), dim3(64), 0, st, a);
+      e = hipGetLastError();
+      if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: chunk combine launch failed: %s", who, hipGetErrorString(e));
+    }
     return Q3A_OK;
   }
   if (append)
@@ -1431,9 +1581,8 @@ extern "C" int q3a_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64
   if (batch == 0) return Q3A_OK;
   if (num_kv_heads < 1 || num_kv_heads > 16)
     return fail(Q3A_EINVAL, "%s: num_kv_heads %d outside [1, 16]", who, num_kv_heads);
-  if (page_size <= 0 || max_pages_per_seq <= 0 || split_tokens < 0)
-    return fail(Q3A_EINVAL, "%s: page_size %d / max_pages_per_seq %d must be > 0, split_tokens >= 0", who, page_size,
-                max_pages_per_seq);
+  if (page_size <= 0 || max_pages_per_seq <= 0)
+    return fail(Q3A_EINVAL, "%s: page_size %d / max_pages_per_seq %d must be > 0", who, page_size, max_pages_per_seq);
   if ((int64_t)max_pages_per_seq * page_size > (int64_t)1 << 30)
     return fail(Q3A_EINVAL, "%s: context capacity too large", who);
   void* ws = scratch_address(who);

@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (must precede the library load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int

@@ -20,6 +20,12 @@ from ._lib import check, lib
 _MAX_SPLIT_TOKENS = 1024
 _MAX_SPLITS = 64
 
+# Decomposition codes, passed as split_tokens (include/q3attn.h): 0 lets the library choose from the batch and the
+# table capacity; these force one kernel (tests and benchmarks run each on the same shapes).
+DECODE_ROW = -1        # one workgroup per (row, KV head), one launch (tables <= 2,048 tokens)
+DECODE_CHUNKS = -2     # chunks of each row over many workgroups, then a combine (small batches of long rows)
+DECODE_STREAMK = -3    # stream-K over all rows' tiles, then a combine (batch <= 4096)
+
 
 def _req(cond: bool, msg: str) -> None:
     if not cond:
@@ -165,11 +171,12 @@ def _rope_rows(x: torch.Tensor, B: int, D: int, dev, name: str) -> torch.Tensor:
 def paged_decode_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
                              k_norm_w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
                              v_cache: torch.Tensor, cache_seqlens: torch.Tensor, block_table: torch.Tensor,
-                             softmax_scale: float, eps: float = 1e-6) -> torch.Tensor:
+                             softmax_scale: float, eps: float = 1e-6, split_tokens: int = 0) -> torch.Tensor:
     """The talker's per-layer attention block in one launch (engine/talker.py:69-77): q and k arrive as the raw
     projections (views of the qkv output), are RMS-normalised with q_norm_w / k_norm_w and rotated with each row's
     cos/sin (engine/ops.py:51-60), k and v are written at position p = cache_seqlens[b] of row b, and the attention of
-    q[b] over tokens 0..p is returned, as paged_decode_append does for already-normalised q and k."""
+    q[b] over tokens 0..p is returned, as paged_decode_append does for already-normalised q and k.  split_tokens: 0
+    (the library's choice) or one of the DECODE_* codes; fixed splits do not take this form."""
     _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table)
     B, Hq, D = q.shape
     num_pages, page, Hkv, _ = k_cache.shape
@@ -189,7 +196,8 @@ def paged_decode_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     if B == 0:
         return out
     L = lib()
-    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, 0)
+    split = int(split_tokens)
+    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     rc = L.q3a_paged_decode_append_rope(
         q.data_ptr(), q.stride(0), q.stride(1),
@@ -200,14 +208,14 @@ def paged_decode_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
         cache_seqlens.data_ptr(), block_table.data_ptr(), block_table.stride(0), max_pages,
         out.data_ptr(), out.stride(0), out.stride(1),
         ws.data_ptr(), ws_bytes,
-        B, Hq, Hkv, D, float(softmax_scale), 0, _stream(dev))
+        B, Hq, Hkv, D, float(softmax_scale), split, _stream(dev))
     check(rc, "q3a_paged_decode_append_rope")
     return out
 
 
 @paged_decode_append_rope.register_fake
 def _paged_decode_append_rope_fake(q, k, v, q_norm_w, k_norm_w, cos, sin, k_cache, v_cache, cache_seqlens,
-                                   block_table, softmax_scale, eps=1e-6):
+                                   block_table, softmax_scale, eps=1e-6, split_tokens=0):
     return q.new_empty(q.shape)
 
 

@@ -58,7 +58,12 @@ def _decode(**kw):
     (dict(q_sh=1 << 30), "q head stride"),
     (dict(q_sh=-128), "q head stride"),
     (dict(ws_bytes=10, max_pages=16, B=65), "workspace"),  # 65 rows of a 256-token table: stream-K, with workspace
+    (dict(ws_bytes=10, max_pages=16, B=4), "workspace"),   # 4 rows of a 256-token table: chunks, with workspace
     (dict(B=-1), "batch"),
+    (dict(split=-4), "split_tokens"),                      # not a path code
+    (dict(split=-1, max_pages=129), "decode path"),        # the row kernel takes tables of at most 2,048 tokens
+    (dict(split=-3, B=4097), "decode path"),               # stream-K takes at most 4,096 rows
+    (dict(split=-2, max_pages=8193), "decode path"),       # chunks: at most 64 tiles per wave
 ])
 def test_paged_decode_rejects_bad_arguments(kw, frag):
     rc = _decode(**kw)
@@ -88,6 +93,27 @@ def test_workspace_and_default_split():
     assert L.q3a_paged_decode_workspace_bytes(64, 16, 8, 128, 129, 16, 0) > 0
     # small batches get smaller splits (more workgroups)
     assert L.q3a_paged_decode_default_split(1, 8, 4, 16) == 16
+
+
+def test_workspace_of_the_decode_paths():
+    """Up to 16 rows of tables of 256 tokens or more take the chunked kernel: one 1,040-byte fp32 record (o[2][128],
+    m[2], l[2]) per (row, chunk, KV head), 16 chunks of 128 tokens up to 2,048-token tables, of 256 tokens up to
+    4,096, then 8 waves of several tiles; a table held by one chunk needs no records.  The path codes force a kernel."""
+    L = _lib.lib()
+    ws = lambda B, pages, split: L.q3a_paged_decode_workspace_bytes(B, 16, 8, 128, pages, 16, split)
+    rec = 1040
+    assert ws(4, 128, 0) == 4 * 16 * 8 * rec                      # auto: chunks, 16 x 128 tokens
+    assert ws(4, 128, -2) == 4 * 16 * 8 * rec
+    assert ws(4, 128, -1) == 0                                    # forced row kernel: one launch
+    assert ws(4, 256, 0) == 4 * 16 * 8 * rec                      # 16 x 256 tokens
+    assert ws(4, 512, 0) == 4 * 16 * 8 * rec                      # 16 x (8 waves x 4 tiles)
+    assert ws(4, 300, -2) == 4 * 13 * 8 * rec                     # 8 waves x 3 tiles: ceil(300 / 24) chunks
+    assert ws(16, 16, 0) == 16 * 2 * 8 * rec                      # 256-token tables: two chunks
+    assert ws(1, 8, -2) == 0                                      # one chunk: no records
+    assert ws(17, 16, 0) == 0                                     # 17 rows: the row-parallel kernel
+    assert ws(4, 15, 0) == 0                                      # 240-token tables: the row-parallel kernel
+    assert ws(4, 128, -3) > 0 and ws(4, 128, -3) != ws(4, 128, 0)  # forced stream-K
+    assert ws(4, 129, -1) == 0                                    # a code that does not take the shape: nothing
 
 
 @pytest.mark.parametrize("kw,frag", [
@@ -190,7 +216,7 @@ def test_paged_decode_append_rejects_bad_arguments(kw, frag):
 
 @pytest.mark.parametrize("kw,frag", [
     (dict(qn=None), "norm weight"), (dict(cs=None), "cos/sin"), (dict(cs=24), "16-byte aligned"),
-    (dict(cs_sb=100), "16-byte aligned"), (dict(eps=-1.0), "eps"), (dict(split=64), "split_tokens == 0"),
+    (dict(cs_sb=100), "16-byte aligned"), (dict(eps=-1.0), "eps"), (dict(split=64), "split_tokens <= 0"),
     (dict(B=65, max_pages=256, Hkv=16, Hq=32), "at most 8 KV heads"), (dict(kn=None), "k_new"),
     (dict(page=24), "page_size"),
 ])

@@ -44,13 +44,17 @@ def test_decode_1x64_single_row(cuda_device):
     assert_parity(out, decode_oracle(wl), "decode1x64")
 
 
-# Tables wider than 2,048 tokens take stream-K at any batch; up to 64 rows of narrower tables take the
-# row-parallel kernel.  The tests below run the small ragged batches through both.
+# With split 0 the library picks the kernel from the batch and the table width: tables wider than 2,048 tokens take
+# stream-K beyond 16 rows, up to 64 rows of narrower tables the row-parallel kernel, and up to 16 rows of tables of
+# 256 tokens or more the chunked kernel.  The path codes force one kernel, so the tests below run the same inputs
+# through each.
 SK_CTX = 2064
-PATHS = [pytest.param(1800, id="row"), pytest.param(SK_CTX, id="sk")]
+ROW, CHUNKS, SK = q3attn.DECODE_ROW, q3attn.DECODE_CHUNKS, q3attn.DECODE_STREAMK
+PATHS = [pytest.param(ROW, id="row"), pytest.param(SK, id="sk"), pytest.param(CHUNKS, id="chunks")]
 
 
-@pytest.mark.parametrize("split,max_ctx", [(0, 1800), (0, SK_CTX), (32, 1800), (64, 1800), (128, 1800), (1024, 1800)])
+@pytest.mark.parametrize("split,max_ctx", [(0, 1800), (0, SK_CTX), (32, 1800), (64, 1800), (128, 1800), (1024, 1800),
+                                           (ROW, 1800), (SK, 1800), (CHUNKS, 1800), (CHUNKS, SK_CTX)])
 def test_ragged_contexts_all_splits(cuda_device, split, max_ctx):
     wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=5)
     out = run(wl, split=split)
@@ -67,30 +71,30 @@ def test_short_contexts(cuda_device, split):
     assert_parity(run(wl, split=split), decode_oracle(wl), f"short split={split}")
 
 
-@pytest.mark.parametrize("max_ctx", [64, SK_CTX])
-def test_ctx1_is_exact_v_row(cuda_device, max_ctx):
+@pytest.mark.parametrize("max_ctx,split", [(64, 0), (1800, ROW), (SK_CTX, SK), (SK_CTX, CHUNKS)])
+def test_ctx1_is_exact_v_row(cuda_device, max_ctx, split):
     wl = W.make_decode("one", cuda_device, ctx=np.array([1, 1, 1]), num_pages=512, max_ctx=max_ctx, seed=9)
-    out = run(wl)
+    out = run(wl, split=split)
     bt = wl.layers[0].block_table[:, 0].long()
     want = wl.v_cache[bt, 0]                                   # [B, Hkv, D]
     assert torch.equal(out, want.repeat_interleave(2, dim=1))
 
 
-@pytest.mark.parametrize("seat_len", [768, 2304])
-def test_reference_layout_page256_identity(cuda_device, seat_len):
-    """The reference's own pool geometry: 256-token pages, identity table, seat_len 768 (engine/talker.py:23-31, 42;
-    2,304 takes the stream-K path)."""
+@pytest.mark.parametrize("seat_len,split", [(768, 0), (768, ROW), (2304, SK), (2304, CHUNKS)])
+def test_reference_layout_page256_identity(cuda_device, seat_len, split):
+    """The reference's own pool geometry: 256-token pages, identity table, seat_len 768 (engine/talker.py:23-31, 42),
+    through the library's choice (the chunked kernel for these 8 rows) and each kernel."""
     ctx = np.array([1, 77, 255, 256, 257, 420, 767, 768])
     wl = W.make_decode("ref", cuda_device, ctx=ctx, num_pages=8 * seat_len // 256, max_ctx=seat_len, page=256,
                        identity=True, seed=2)
-    assert_parity(run(wl), decode_oracle(wl), "page256")
+    assert_parity(run(wl, split=split), decode_oracle(wl), f"page256 split={split}")
 
 
-@pytest.mark.parametrize("max_ctx", PATHS)
-def test_stale_nan_slots_and_garbage_table_entries(cuda_device, max_ctx):
+@pytest.mark.parametrize("path", PATHS)
+def test_stale_nan_slots_and_garbage_table_entries(cuda_device, path):
     """Slots past ctx in a row's last page and table entries past its last page are never read."""
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=6)
-    clean = run(wl)
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=6)
+    clean = run(wl, split=path)
     bt = wl.layers[0].block_table.clone()
     k, v = wl.k_cache.clone(), wl.v_cache.clone()
     page = wl.page_size
@@ -101,32 +105,32 @@ def test_stale_nan_slots_and_garbage_table_entries(cuda_device, max_ctx):
             k[pg, c % page:] = float("nan")
             v[pg, c % page:] = float("nan")
         bt[b, used:] = -7 if b % 2 else 1 << 30
-    dirty = run(wl, k=k, v=v, bt=bt)
+    dirty = run(wl, k=k, v=v, bt=bt, split=path)
     assert torch.equal(clean, dirty)
 
 
-@pytest.mark.parametrize("max_ctx", [64, SK_CTX])
-def test_out_of_range_page_ids_do_not_fault(cuda_device, max_ctx):
+@pytest.mark.parametrize("max_ctx,split", [(64, 0), (SK_CTX, SK), (SK_CTX, CHUNKS), (1800, ROW)])
+def test_out_of_range_page_ids_do_not_fault(cuda_device, max_ctx, split):
     wl = W.make_decode("ragged", cuda_device, ctx=np.array([40, 40]), num_pages=512, max_ctx=max_ctx, seed=3)
     bt = wl.layers[0].block_table.clone()
     bt[0, 1] = -1
     bt[1, 0] = 1 << 30
-    out = run(wl, bt=bt)
+    out = run(wl, bt=bt, split=split)
     assert torch.isfinite(out.float()).all()
 
 
-@pytest.mark.parametrize("max_ctx", PATHS)
-def test_page_table_permutation_invariance(cuda_device, max_ctx):
-    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=max_ctx, seed=8)
-    a = run(wl)
+@pytest.mark.parametrize("path", PATHS)
+def test_page_table_permutation_invariance(cuda_device, path):
+    wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED), num_pages=4096, max_ctx=1800, seed=8)
+    a = run(wl, split=path)
     perm = torch.randperm(4096, generator=torch.Generator().manual_seed(1)).to(cuda_device)
     inv = torch.argsort(perm)
-    b = run(wl, k=wl.k_cache[perm], v=wl.v_cache[perm], bt=inv[wl.layers[0].block_table.long()].int())
+    b = run(wl, k=wl.k_cache[perm], v=wl.v_cache[perm], bt=inv[wl.layers[0].block_table.long()].int(), split=path)
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("max_ctx", [256, SK_CTX])
-def test_strided_cache_and_query(cuda_device, max_ctx):
+@pytest.mark.parametrize("max_ctx,split", [(256, ROW), (SK_CTX, SK), (SK_CTX, CHUNKS)])
+def test_strided_cache_and_query(cuda_device, max_ctx, split):
     wl = W.make_decode("ragged", cuda_device, ctx=np.array(RAGGED[:12]), num_pages=2048, max_ctx=max_ctx, seed=10)
     NP, P, H, D = wl.k_cache.shape
     kb = torch.zeros(NP, P, H, D + 8, dtype=torch.bfloat16, device=cuda_device)
@@ -136,8 +140,8 @@ def test_strided_cache_and_query(cuda_device, max_ctx):
     qkv = torch.zeros(wl.batch, 4096, dtype=torch.bfloat16, device=cuda_device)
     qkv[:, :2048] = wl.layers[0].q.reshape(wl.batch, 2048)
     q = qkv[:, :2048].view(wl.batch, 16, 128)                   # row stride 4096
-    out = run(wl, q=q, k=kb[..., :D], v=vb[..., :D])
-    assert torch.equal(out, run(wl))
+    out = run(wl, q=q, k=kb[..., :D], v=vb[..., :D], split=split)
+    assert torch.equal(out, run(wl, split=split))
 
 
 def test_decode256_full(cuda_device):
@@ -173,7 +177,7 @@ def test_stream_k_tiny_workloads(cuda_device, ctx):
     one-tile workgroups (tables of 2,064 tokens: past the row-parallel path's 2,048)."""
     ctx = np.array(ctx)
     wl = W.make_decode("tiny", cuda_device, ctx=ctx, num_pages=512, max_ctx=2064, seed=int(ctx.sum()) % 97)
-    out = run(wl)
+    out = run(wl, split=SK)
     assert_parity(out, decode_oracle(wl), f"tiny {ctx.tolist()}")
 
 
@@ -189,12 +193,12 @@ def test_row_parallel_small_batches(cuda_device, max_ctx, ctx):
     widened past the path's limit."""
     ctx = np.array(ctx)
     wl = W.make_decode("row_small", cuda_device, ctx=ctx, num_pages=4096, max_ctx=max_ctx, seed=max_ctx + len(ctx))
-    out = run(wl)
+    out = run(wl, split=ROW)
     assert_parity(out, decode_oracle(wl), f"row path {max_ctx} {ctx.tolist()}")
     L = wl.layers[0]
     wide = torch.full((wl.batch, 129), -1, dtype=torch.int32, device=cuda_device)
     wide[:, : L.block_table.shape[1]] = L.block_table
-    ok, st = ora.compare(to_np(run(wl, bt=wide)), to_np(out), max_abs=8e-3, mean_abs=2e-4)
+    ok, st = ora.compare(to_np(run(wl, bt=wide, split=SK)), to_np(out), max_abs=8e-3, mean_abs=2e-4)
     assert ok, st
 
 
