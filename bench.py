@@ -314,6 +314,34 @@ def bench_decode_small(args, dev):
     return rec
 
 
+def bench_decode_small_lite(args, dev):
+    """The driver line's short small-batch entry: 1 x 1,024, 1 x 1,800 and 8 x 1,800 tokens on 2,048-token tables,
+    through the library's choice (the chunked kernel) and the row-parallel kernel, µs per call in a 28-call graph."""
+    import numpy as np
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    shapes = {}
+    for B, ctx in ((1, 1024), (1, 1800), (8, 1800)):
+        wl = W.make_decode("small", dev, ctx=np.full(B, ctx), num_pages=max(256, B * 130 * 2), max_ctx=2048,
+                           layers=LAYERS, seed=args.seed + 1)
+        res = {}
+        for path, code in (("auto", 0), ("row_parallel", -1)):
+            _, frame_ms, _ = time_graph(dev, lambda: [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens,
+                                                                          L.block_table, wl.scale, code)
+                                                      for L in wl.layers], args.steps, args.warmup,
+                                        getattr(args, "min_warm_s", 0.0))
+            res[path] = round(statistics.median(frame_ms) * 1e3 / LAYERS, 2)
+        res["auto_kernel"] = decode_kernel_name(wl, 0)
+        shapes[f"{B}x{ctx}"] = res
+        del wl
+        torch.cuda.empty_cache()
+    mean_auto = statistics.mean(r["auto"] for r in shapes.values())
+    return {"value": round(mean_auto * LAYERS, 2), "per_shape_us_per_call": shapes}
+
+
 def bench_decode_append(args, dev, wl):
     """Extra information beside the headline: the same frame with this step's K/V append included, once as the
     engine does it (two index_copy_ scatters per layer, engine/talker.py:72-73, then the decode call) and once
@@ -908,25 +936,31 @@ def other_workloads(args, dev):
     lite.steps, lite.warmup, lite.no_cpu_baseline, lite.no_append = 20, 3, True, True
     lite.no_compile = True                # a torch.compile of the CP producers does not fit these short runs
     lite.min_warm_s = 1.0                 # the GPU sat idle during the CPU baseline before: let clocks ramp
-    dec = copy.copy(lite)
-    dec.no_cpu_baseline = args.no_cpu_baseline
+    # Every configuration's CPU baseline (the reference's torch CPU form of the same call, timed on the host's
+    # threads) runs unless --no-cpu-baseline: each is a bounded sample of well under a second here.
+    lite.no_cpu_baseline = args.no_cpu_baseline
     pre = copy.copy(lite)
     pre.no_append = False                 # the prompt/admission-step comparisons (fused pool writes) are part of these
     out = {}
-    for name, fn in (("decode256", lambda: bench_decode(dec, dev, "decode256", cpu_budget_s=6.0)),
-                     ("decode1x64", lambda: bench_decode(dec, dev, "decode1x64", cpu_budget_s=2.0)),
+    for name, fn in (("decode256", lambda: bench_decode(lite, dev, "decode256", cpu_budget_s=6.0)),
+                     ("decode1x64", lambda: bench_decode(lite, dev, "decode1x64", cpu_budget_s=2.0)),
+                     ("decode_small", lambda: bench_decode_small_lite(lite, dev)),
                      ("cp512", lambda: bench_cp(lite, dev)),
                      ("prefill32", lambda: bench_prefill(pre, dev)), ("admission_prefill", lambda: bench_admit(pre, dev))):
         try:
             r = fn()
             keep = {k: r[k] for k in ("us_per_layer_call", "us_per_call", "hbm_gbps", "pct_hbm_peak", "tflops",
                                       "three_launch_us_per_step", "cold_us_per_call", "launch_floor_us_per_call",
-                                      "prompt_step", "admission_step", "norm_rope_form") if k in r}
+                                      "prompt_step", "admission_step", "norm_rope_form",
+                                      "per_shape_us_per_call") if k in r}
             keep["us_per_step"] = r["value"]
-            keep["roofline_frac"] = r["roofline"]["frac"]
-            keep["roofline_unit"] = r["roofline"]["unit"]
+            if "roofline" in r:
+                keep["roofline_frac"] = r["roofline"]["frac"]
+                keep["roofline_unit"] = r["roofline"]["unit"]
             if r.get("cpu_baseline"):
-                keep["cpu_baseline"] = {k: r["cpu_baseline"][k] for k in ("us_per_layer_call", "gbps", "cores")}
+                keep["cpu_baseline"] = {k: r["cpu_baseline"][k] for k in ("value", "unit", "us_per_layer_call", "gbps",
+                                                                        "cores", "kind", "sample")
+                                        if k in r["cpu_baseline"]}
             out[name] = keep
         except Exception as e:  # noqa: BLE001 - reported, never fatal for the headline
             out[name] = {"error": f"{type(e).__name__}: {e}"}

@@ -22,9 +22,15 @@ Pinning (what independent check fixes each function; see tests/test_oracle.py):
 * ``cp_attn_triton_path``-- n_live=1 -> V[slot 0]; NaN-poisoned stale slots leave the output
                            unchanged; within tolerance of the float64 closed form.
 * ``prefill_varlen``    -- torch CPU SDPA ``is_causal=True`` per sequence; float64 brute force.
-* ``prefill_prefix``    -- R == n reduces to ``prefill_varlen``; brute force float64.
+* ``prefill_prefix``    -- R == n reduces to ``prefill_varlen``; brute force float64; causal=False
+                           against torch CPU SDPA without a mask.
 * ``rms`` / ``rope``    -- unit-RMS invariant; RoPE at position 0 is the identity; RoPE preserves
                            the norm of each rotated pair; relative-position invariance of q.k.
+* ``norm_rope``         -- eager form: bit for bit against torch's CPU bf16 kernels running
+                           engine/ops.py:51-60 (rows of RMS 1e-4..10, so eps matters); planted
+                           mistakes (weight before the cast, no eps, swapped halves, cos/sin
+                           swapped) fail that check.  Compiled form: within one bf16 unit of the
+                           eager form and of the reference's chain in float64.
 * ``rope_tables``       -- closed-form frequencies (theta**(-2i/D)) checked at chosen indices.
 """
 from __future__ import annotations
@@ -85,6 +91,50 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     h = x.shape[-1] // 2
     rot = np.concatenate([-x[..., h:], x[..., :h]], axis=-1)
     return (x * cos + rot * sin).astype(np.float32)
+
+
+def _rsqrt_mean_sq(xf: np.ndarray, eps: float) -> np.ndarray:
+    """1 / sqrt(mean(x^2) + eps) over the last axis in float32 (``torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) +
+    eps)``, engine/ops.py:53), numpy's summation order."""
+    ms = (xf * xf).mean(-1, keepdims=True, dtype=np.float32)
+    return np.float32(1.0) / np.sqrt(ms + np.float32(eps), dtype=np.float32)
+
+
+def _normalise(xf: np.ndarray, r: np.ndarray) -> np.ndarray:
+    """``(xf * r).to(x.dtype)`` (engine/ops.py:53-54): the product rounded to bf16."""
+    return bf16_round(xf * r)
+
+
+def _rotate_half(y: np.ndarray) -> np.ndarray:
+    """``torch.cat((-y[..., h:], y[..., :h]), dim=-1)`` (engine/ops.py:59)."""
+    h = y.shape[-1] // 2
+    return np.concatenate([-y[..., h:], y[..., :h]], axis=-1)
+
+
+def norm_rope(x: np.ndarray, w: np.ndarray, cos: np.ndarray, sin: np.ndarray, eps: float = 1e-6,
+              eager: bool = True) -> np.ndarray:
+    """The talker's q/k producers on bf16 head rows: ``rope(rms(x, w), cos, sin)`` (engine/ops.py:51-60, called at
+    engine/talker.py:69-70, 158-159 and engine/arrivals.py:112-118).  x, w, cos, sin hold bf16 values; the result is
+    bf16 values in float32.
+
+    rms: r = 1 / sqrt(mean(x^2) + eps) in float32, n = bf16(x * r) (the explicit ``.to(x.dtype)``), y = w * n.
+    rope: y * cos + cat(-y[h:], y[:h]) * sin.
+    * eager=True -- eager torch bf16 ops (``prefill_hidden`` and the admission layer are not compiled,
+      engine/arrivals.py:57-61): every op rounds its result, y = bf16(w * n), o = bf16(bf16(y cos) + bf16(rot(y) sin)).
+      Torch's CPU bf16 kernels give these bits exactly.
+    * eager=False -- the chain with the cast kept and nothing else rounded until the result: y = w * n in float32,
+      o = bf16(y cos + rot(y) sin).  This is the form the HIP kernels of the compiled callers (``Talker._decode``,
+      ``CodePredictor._pre``, engine/talker.py:56-59, engine/code_predictor.py:25-29) compute; what a compiler emits for
+      the same source depends on its backend (which intermediates it materialises or rounds).
+    The mean of squares is summed in numpy's order; another order moves mean(x^2) by an fp32 unit, which can move n,
+    and with it o, by a bf16 unit on rare elements."""
+    xf = np.asarray(x, np.float32)
+    n = _normalise(xf, _rsqrt_mean_sq(xf, eps))
+    if eager:
+        y = bf16_round(np.asarray(w, np.float32) * n)
+        return bf16_round(bf16_round(y * cos) + bf16_round(_rotate_half(y) * sin))
+    y = (np.asarray(w, np.float32) * n).astype(np.float32)
+    return bf16_round((y * cos + _rotate_half(y) * sin).astype(np.float32))
 
 
 # ----------------------------------------------------------------------------- talker decode
@@ -249,17 +299,18 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, acc=np.float32):
     return out
 
 
-def prefill_prefix(q, K, V, scale, acc=np.float32):
+def prefill_prefix(q, K, V, scale, acc=np.float32, causal=True):
     """Prefix + new tokens with bottom-right-aligned causal mask.
 
     Restates ``FastAdmit._attn_ref`` (engine/arrivals.py:125-131): query i (of R new) sees the
-    n - R prefix keys and the new keys <= i; mask = triu(n - R + 1).
+    n - R prefix keys and the new keys <= i; mask = triu(n - R + 1).  causal=False: every query sees
+    all n keys (flash_attn_func's causal=False, which the engine never passes).
     q [S, R, Hq, D]; K, V [S, n, Hkv, D].  Returns [S, R, Hq, D].
     """
     S, R, Hq, D = q.shape
     n, Hkv = K.shape[1], K.shape[2]
     G = Hq // Hkv
-    m = np.triu(np.full((R, n), -np.inf, dtype=acc), n - R + 1)
+    m = np.triu(np.full((R, n), -np.inf, dtype=acc), n - R + 1) if causal else np.zeros((R, n), dtype=acc)
     qh = q.astype(acc).transpose(0, 2, 1, 3).reshape(S, Hkv, G, R, D)
     Kh = K.astype(acc).transpose(0, 2, 1, 3)[:, :, None]
     Vh = V.astype(acc).transpose(0, 2, 1, 3)[:, :, None]

@@ -1,12 +1,27 @@
-"""PyTorch-CPU restatement of the reference's fp32 attention paths, used as the CPU baseline.
+"""PyTorch restatement of the reference's fp32 attention paths (the CPU baseline) and of its q/k producers.
 
 TEST INFRASTRUCTURE ONLY: imported by ``bench.py``'s ``cpu_baseline`` leg and by ``tests/``.  It
 times the reference's own CPU-capable formulation (torch fp32 matmul -> softmax -> matmul, one row
-at a time), never the product.
+at a time), never the product.  ``rms`` and ``rope`` are the reference's producers as torch ops on
+any device (the synthetic models and the tests run them on the GPU as the engine does); on the CPU
+they are pinned bit for bit to ``oracle.attention.norm_rope`` (tests/test_producers.py).
 """
 from __future__ import annotations
 
 import torch
+
+
+def rms(x, w, eps=1e-6):
+    """Qwen3 qk/hidden RMSNorm as engine/ops.py:51-55 writes it: normalise in float32, cast back to x's dtype, scale."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * xf.to(x.dtype)
+
+
+def rope(x, cos, sin):
+    """Rotate-half RoPE as engine/ops.py:58-60 writes it."""
+    h = x.shape[-1] // 2
+    return x * cos + torch.cat((-x[..., h:], x[..., :h]), dim=-1) * sin
 
 
 def paged_decode_rows(q, k_cache, v_cache, seqlens, block_table, scale):

@@ -1420,6 +1420,12 @@ extern "C" int q3a_prefill_dense_append_rope(
       pv_stride_s < 0 || pv_stride_t < 0 || pv_stride_h < 0 || rope_stride_t < 0)
     return fail(Q3A_EINVAL, "%s: strides must be non-negative multiples of 8 elements", who);
   if (prefix_len > 0 && num_prefixes < 1) return fail(Q3A_EINVAL, "%s: num_prefixes must be >= 1", who);
+  // The short-key kernel addresses a 16-row group of the prefix bank through one buffer descriptor with a 32-bit
+  // extent ((15 * token stride + head_dim) * 2 bytes), the bound k and v get in check_common.
+  const int64_t lim = (int64_t)1 << 26;
+  if (prefix_len > 0 && (pk_stride_t < head_dim || pk_stride_t > lim || pv_stride_t < head_dim || pv_stride_t > lim))
+    return fail(Q3A_EINVAL, "%s: prefix token strides %lld/%lld must be in [head_dim, 2^26]", who,
+                (long long)pk_stride_t, (long long)pv_stride_t);
   const size_t need = q3a_prefill_dense_append_rope_workspace_bytes(num_seqs, seqlen_q, prefix_len, num_q_heads,
                                                                     num_kv_heads, head_dim);
   if (workspace_bytes < need)

@@ -1,8 +1,9 @@
 """Seeded synthetic talker for the code-0 criterion (test infrastructure).
 
 It restates the talker's per-frame decode (engine/talker.py:63-80: qkv projection, qk-RMSNorm, RoPE, K/V
-append into the paged pool, attention, o-projection, MLP, final norm), the codebook-0 logits
-(engine/talker.py:90-94, without the per-stream penalty state) and the top-k sampler (engine/ops.py:68-76)
+append into the paged pool, attention, o-projection, MLP, final norm), the processed codebook-0 scores with their
+per-seat state (``Cb0State``: engine/talker.py:90-94 and 99-101 -- repetition penalty over the seat's own generated
+ids, special ids suppressed except EOS, EOS blocked for the first frames) and the top-k sampler (engine/ops.py:68-76)
 with random weights of the 0.6B geometry (hidden 1024, 28 layers, 16/8 heads of 128, ffn 3072, 3072 codes).
 The attention call is injected so the identical stack runs once with the HIP kernel and once with the
 oracle.  The page table is a seeded random permutation of 16-token pages; the append slot goes through it.
@@ -13,20 +14,9 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
+from oracle.torch_cpu import rms, rope  # noqa: F401  (engine/ops.py:51-60; re-exported for the GPU tests)
+
 H, NH, NKV, HD, FFN, VOCAB, PAGE = 1024, 16, 8, 128, 3072, 3072, 16
-
-
-def rms(x, w, eps=1e-6):
-    """engine/ops.py:51-55."""
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return w * xf.to(x.dtype)
-
-
-def rope(x, cos, sin):
-    """engine/ops.py:58-60."""
-    h = x.shape[-1] // 2
-    return x * cos + torch.cat((-x[..., h:], x[..., :h]), dim=-1) * sin
 
 
 def sample_topk(logits, temperature, k, gen):
@@ -35,6 +25,33 @@ def sample_topk(logits, temperature, k, gen):
     p = torch.softmax(vals / temperature, dim=-1)
     j = torch.multinomial(p, 1, generator=gen)
     return idx.gather(1, j).squeeze(1)
+
+
+class Cb0State:
+    """Per-seat sampling state of the talker's codebook-0 head (engine/talker.py:36-45) and the processing of its
+    scores (``_cb0_logits``, engine/talker.py:90-94): ids a seat has generated are penalised (negative scores times
+    ``rep``, positive ones divided by it), the last 1,024 ids (specials) are suppressed except EOS, and EOS is blocked
+    until the seat has generated ``min_new`` codes.  ``update`` records a frame's codes (engine/talker.py:99-101).
+    Defaults are the engine's (temperature 0.9, top-k 50, rep 1.05, min_new 2, engine/talker.py:22); EOS is one id
+    of the special range, as the codec's is."""
+
+    def __init__(self, seats, device, rep=1.05, min_new=2, eos=VOCAB - 1024 + 126):
+        self.rep, self.min_new = rep, min_new
+        self.seen = torch.zeros(seats, VOCAB, dtype=torch.bool, device=device)
+        self.ngen = torch.zeros(seats, dtype=torch.long, device=device)
+        self.suppress = torch.zeros(VOCAB, device=device)
+        self.suppress[VOCAB - 1024:] = float("-inf")
+        self.suppress[eos] = 0.0
+        self.eos_col = torch.zeros(VOCAB, dtype=torch.bool, device=device)
+        self.eos_col[eos] = True
+
+    def process(self, lg, seat):
+        lg = torch.where(self.seen[seat], torch.where(lg < 0, lg * self.rep, lg / self.rep), lg) + self.suppress
+        return lg.masked_fill((self.ngen[seat] < self.min_new)[:, None] & self.eos_col[None, :], float("-inf"))
+
+    def update(self, seat, c0):
+        self.seen.index_put_((seat, c0), self.eos_col.new_ones(()).expand_as(c0))
+        self.ngen.index_copy_(0, seat, self.ngen[seat] + 1)
 
 
 class SyntheticTalker:
@@ -101,7 +118,7 @@ class SyntheticTalker:
         return rms(x, self.norm)
 
     def logits(self, h):
-        """Codebook-0 scores (engine/talker.py:92) before the per-stream penalties."""
+        """Raw codebook-0 scores (engine/talker.py:92), before Cb0State.process."""
         return F.linear(h, self.codec_head).float()
 
 

@@ -415,6 +415,9 @@ def _dense_rope(**kw):
     (dict(ws_bytes=1024), "workspace"), (dict(D=64), "head_dim"), (dict(Hq=12), "num_q_heads"),
     (dict(Hq=12, Hkv=6), "multiple of 4"), (dict(npre=0), "num_prefixes"), (dict(page=48), "power of two"),
     (dict(P=-1), "negative"),
+    # the prefix bank's token strides bound one 32-bit buffer extent per 16-row group, as k and v's do
+    (dict(pk_st=(1 << 26) + 8), "prefix token strides"), (dict(pv_st=(1 << 27)), "prefix token strides"),
+    (dict(pk_st=64), "prefix token strides"),
 ])
 def test_prefill_dense_append_rope_rejects_bad_arguments(kw, frag):
     assert _dense_rope(**kw) < 0

@@ -346,3 +346,67 @@ def test_compiled_code_predictor_step_with_fused_producers(cuda_device):
             assert torch.equal(static[1], o) and torch.equal(static[0], y)
             assert torch.equal(K, Ke)
         print(f"[compile] cp step with fused producers p={p}: equal to eager, no scratch copy", flush=True)
+
+
+def test_compiled_producers_against_fused_norm_rope_rows(cuda_device):
+    """The reference's producers compiled as the engine compiles them (rope(rms(k, kn), cos, sin), engine/ops.py:51-60,
+    under torch.compile like Talker._decode and CodePredictor._pre) against the k rows the fused norm/rope kernels write
+    into the pool (paged_decode_append_rope) and into the CP scratch slot (cp_attn_append_rope).  The kernels round
+    the normalised row to bf16 where the source casts it and round the rope once; inductor may keep the cast's operand
+    in fp32 and may round the rotated half where it materialises the concatenation, so a fraction of elements sits
+    one bf16 unit apart.  Printed: that fraction for both kernels, and which oracle rounding the compiled code follows
+    (cast kept: oracle.norm_rope(eager=False); cast dropped: the same chain without the cast).  Asserted: every element
+    within the rounding of the two rope products, and most elements equal."""
+    dev = cuda_device
+    torch._dynamo.reset()
+    g = torch.Generator(device=dev).manual_seed(21)
+    B = 256
+    k_raw = (torch.randn(B, NKV, HD, generator=g, device=dev) *
+             (0.2 + 3.0 * torch.rand(B, NKV, 1, generator=g, device=dev))).to(torch.bfloat16)
+    q_raw = torch.randn(B, NH, HD, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, NKV, HD, generator=g, device=dev).to(torch.bfloat16)
+    qn = (1.0 + 0.1 * torch.randn(HD, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(HD, generator=g, device=dev)).to(torch.bfloat16)
+    cos_t, sin_t = rope_bf16(1024, dev)
+    rng = np.random.default_rng(21)
+    pos = torch.from_numpy(rng.integers(0, 255, size=B)).to(dev)
+    produce = torch.compile(lambda x, w, c, s: rope(rms(x, w), c, s), dynamic=False)
+
+    # decode: each row's new k goes to position pos of its own 256-token table
+    P = 16
+    bt = torch.from_numpy(rng.permutation(NUM_PAGES)[: B * P].reshape(B, P).astype(np.int32)).to(dev)
+    kc = torch.zeros(NUM_PAGES, PAGE, NKV, HD, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    c, s = cos_t[pos], sin_t[pos]
+    q3attn.paged_decode_append_rope(q_raw, k_raw, v, qn, kn, c, s, kc, vc, pos.to(torch.int32), bt, SCALE, 1e-6)
+    slot = bt.gather(1, (pos // PAGE)[:, None].to(torch.int64))[:, 0].to(torch.int64) * PAGE + pos % PAGE
+    got_dec = kc.view(-1, NKV, HD)[slot]
+    want_dec = produce(k_raw, kn, c[:, None, :], s[:, None, :])
+
+    # code predictor: step p's k goes to slot p of every row (cos/sin of position p)
+    p = 9
+    K = torch.zeros(B, NKV, 16, HD, dtype=torch.bfloat16, device=dev)
+    V = torch.zeros_like(K)
+    q3attn.cp_attn_append_rope(q_raw, k_raw, v, K, V, p, SCALE, qn, kn, cos_t[p], sin_t[p])
+    got_cp = K[:, :, p]
+    want_cp = produce(k_raw, kn, cos_t[p], sin_t[p])
+    torch.cuda.synchronize()
+
+    xk, w = to_np(k_raw), to_np(kn)
+    for name, got, want, cs, sn in (("paged_decode_append_rope", got_dec, want_dec, to_np(c)[:, None], to_np(s)[:, None]),
+                                     ("cp_attn_append_rope", got_cp, want_cp, to_np(cos_t[p]), to_np(sin_t[p]))):
+        got, want = to_np(got), to_np(want)
+        same = float((got == want).mean())
+        kept = ora.norm_rope(xk, w, cs, sn, eager=False)
+        xf = xk.astype(np.float32)
+        y = w * (xf * ora._rsqrt_mean_sq(xf, 1e-6))          # the cast dropped
+        dropped = ora.bf16_round(y * cs + ora._rotate_half(y) * sn)
+        yk = w * ora._normalise(xf, ora._rsqrt_mean_sq(xf, 1e-6))
+        terms = np.abs(yk * cs) + np.abs(ora._rotate_half(yk) * sn)
+        d = np.abs(got - want)
+        print(f"[compile] {name}: k rows equal to the compiled producers on {same:.4f} of elements (max diff "
+              f"{d.max():.3e}); compiled producers equal the cast-kept chain on {float((want == kept).mean()):.4f}, "
+              f"the cast-dropped chain on {float((want == dropped).mean()):.4f}; kernel rows equal the cast-kept chain "
+              f"on {float((got == kept).mean()):.4f}", flush=True)
+        assert (d <= 2.0 ** -7 * terms + 2.0 ** -7 * np.abs(want) + 1e-30).all()
+        assert same >= 0.5

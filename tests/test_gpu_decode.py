@@ -275,3 +275,53 @@ def test_partial_records_keep_precision_at_extreme_v(cuda_device, split, max_ctx
     err = np.abs(out - ref) / scale
     print(f"[parity] v_scale={v_scale} split={split} max_rel={err.max():.2e} mean_rel={err.mean():.2e}", flush=True)
     assert err.max() <= 2e-2 and err.mean() <= 2e-3
+
+
+def _stream_k_cut_rows(wl):
+    """Rows of a stream-K call that a workgroup range boundary cuts (their partial records are merged by the combine
+    kernel).  The resident grid comes from the library's workspace size for stream-K (prefix sums, then 2 records of
+    528 B per KV head per workgroup); the ranges are the kernel's: [k NT / G, (k + 1) NT / G) over the rows' 16-token
+    tiles, with G = min(grid, max(min(NT, 8), ceil(NT / 4)))."""
+    from q3attn import _lib
+    B = wl.batch
+    L = wl.layers[0]
+    ws = _lib.lib().q3a_paged_decode_workspace_bytes(B, 16, 8, 128, L.block_table.shape[1], wl.page_size, SK)
+    grid = (ws - ((B + 1) * 4 + 255) // 256 * 256) // (2 * 8 * 528)
+    tiles = (wl.ctx + 15) // 16
+    pre = np.concatenate([[0], np.cumsum(tiles)])
+    NT = int(pre[-1])
+    G = min(grid, max(min(NT, 8), (NT + 3) // 4))
+    bounds = np.array([k * NT // G for k in range(1, G)])
+    cut = np.array([bool(((bounds > pre[r]) & (bounds < pre[r + 1])).any()) for r in range(B)])
+    return cut, grid, G
+
+
+def test_stream_k_cut_rows_keep_the_fp32_accuracy(cuda_device):
+    """The 576-row workload: rows cut by a stream-K range boundary are merged from partial records whose o is stored
+    in 16 bits (fp16, 11 significant bits, while the record's largest |o| is in [2^-6, 2^15]; bf16 beyond).  Against
+    the float64 oracle their error must match the uncut rows' (written straight from fp32 registers) and the
+    row-parallel kernel's on the same rows (fp32 merges in LDS, no 16-bit records); the measured figures are printed."""
+    wl = W.make_decode("decode576", cuda_device, layers=1, seed=3)
+    cut, grid, G = _stream_k_cut_rows(wl)
+    live = wl.ctx > 0
+    sk = to_np(run(wl, split=SK))
+    row = to_np(run(wl, split=ROW))
+    ref64 = decode_oracle(wl, acc=np.float64)
+    ok, st = ora.compare(sk, decode_oracle(wl))
+    assert ok, st
+    stats = {}
+    for name, out in (("stream_k", sk), ("row_parallel", row)):
+        err = np.abs(out - ref64)
+        for part, mask in (("cut", cut & live), ("uncut", ~cut & live)):
+            e = err[mask]
+            stats[name, part] = (float(e.max()), float(e.mean()), float((e / (np.abs(ref64[mask]) + 2.0 ** -20)
+                                                                         <= 2.0 ** -8).mean()))
+    print(f"[partials] grid {grid}, {G} ranges: {int((cut & live).sum())} cut rows of {int(live.sum())} live", flush=True)
+    for (name, part), (mx, mean, frac) in sorted(stats.items()):
+        print(f"[partials] {name} {part} rows vs float64 oracle: max abs {mx:.3e}, mean abs {mean:.3e}, "
+              f"within half a bf16 unit: {frac:.4f}", flush=True)
+    assert (cut & live).sum() >= 100
+    sk_cut, sk_un, row_cut = stats["stream_k", "cut"], stats["stream_k", "uncut"], stats["row_parallel", "cut"]
+    # the 16-bit records add at most 2^-12 |o| per record before the bf16 rounding (2^-9 |o|): no visible extra error
+    assert sk_cut[1] <= 1.1 * max(sk_un[1], row_cut[1])
+    assert sk_cut[0] <= 1.5 * max(sk_un[0], row_cut[0])

@@ -19,6 +19,7 @@ import torch
 import q3attn
 from helpers import to_np
 from oracle import attention as ora
+from oracle import torch_cpu as tc
 from q3attn import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -27,19 +28,13 @@ D = 128
 
 
 def _eager_norm_rope_np(x, w, cos, sin, eps=1e-6):
-    """engine/ops.py:51-60 as eager bf16 ops: y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), then
-    bf16(bf16(y * cos) + bf16(rot(y) * sin)) with rot(y) = cat(-y[64:], y[:64])."""
-    y = ora.bf16_round(w * ora.rms(x, None, eps, to_bf16=True))
-    rot = np.concatenate([-y[..., D // 2:], y[..., : D // 2]], axis=-1)
-    return ora.bf16_round(ora.bf16_round(y * cos) + ora.bf16_round(rot * sin))
+    """engine/ops.py:51-60 as eager bf16 ops (the oracle's eager form, pinned to torch's bf16 kernels on the CPU)."""
+    return ora.norm_rope(x, w, cos, sin, eps, eager=True)
 
 
 def _eager_norm_rope_torch(x, w, cos, sin, eps=1e-6):
-    """The same producers as the engine runs them: torch bf16 ops (engine/ops.py:51-60)."""
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    y = w * xf.to(x.dtype)
-    return y * cos + torch.cat((-y[..., D // 2:], y[..., : D // 2]), dim=-1) * sin
+    """The same producers as the engine runs them: the reference's torch ops, here on the GPU."""
+    return tc.rope(tc.rms(x, w, eps), cos, sin)
 
 
 def _inputs(dev, S, R, P, n_prefixes, seed):
@@ -83,17 +78,19 @@ def _assert_last_bit(a, b, what, frac=2e-3):
     print(f"[parity] {what}: {int(bad.sum())} of {bad.size} elements one bf16 step apart", flush=True)
 
 
-@pytest.mark.parametrize("S,R,P,page,first,indexed", [
-    (8, 42, 35, 16, 0, True),       # the admission shape: 8 seats, 42 new tokens after a 35-token voice prefix
-    (8, 42, 35, 16, 35, True),      # prefix already in the pool: the new rows only
-    (4, 42, 35, 256, 0, False),     # the reference's 256-token pages, one prefix per sequence
-    (3, 20, 0, 16, 0, False),       # no prefix
-    (5, 70, 50, 16, 3, True),       # one launch, 5 query groups, part of the prefix into the pool
-    (2, 120, 5, 16, 0, True),       # 125 keys but 8 query groups: the two-launch form on the short-key kernel
-    (2, 100, 200, 16, 0, True),     # 300 keys: the tiled attention kernel
-    (2, 40, 660, 32, 600, True),    # tiled, part of a long prefix
+@pytest.mark.parametrize("S,R,P,page,first,indexed,causal", [
+    (8, 42, 35, 16, 0, True, True),       # the admission shape: 8 seats, 42 new tokens after a 35-token voice prefix
+    (8, 42, 35, 16, 35, True, True),      # prefix already in the pool: the new rows only
+    (4, 42, 35, 256, 0, False, True),     # the reference's 256-token pages, one prefix per sequence
+    (3, 20, 0, 16, 0, False, True),       # no prefix
+    (5, 70, 50, 16, 3, True, True),       # one launch, 5 query groups, part of the prefix into the pool
+    (2, 120, 5, 16, 0, True, True),       # 125 keys but 8 query groups: the two-launch form on the short-key kernel
+    (2, 100, 200, 16, 0, True, True),     # 300 keys: the tiled attention kernel
+    (2, 40, 660, 32, 600, True, True),    # tiled, part of a long prefix
+    (4, 42, 35, 16, 0, True, False),      # non-causal, one launch (the last key tile's masking only)
+    (2, 120, 5, 16, 0, True, False),      # non-causal, the two-launch form
 ])
-def test_dense_append_rope_matches_oracle(cuda_device, S, R, P, page, first, indexed):
+def test_dense_append_rope_matches_oracle(cuda_device, S, R, P, page, first, indexed, causal):
     dev = cuda_device
     n = P + R
     nvoices = 3 if indexed else S
@@ -106,10 +103,10 @@ def test_dense_append_rope_matches_oracle(cuda_device, S, R, P, page, first, ind
     kc = torch.full((num_pages, page, 8, D), float("nan"), dtype=torch.bfloat16, device=dev)
     vc = torch.full_like(kc, float("nan"))
     scale = D ** -0.5
-    print(f"[case] prefill_dense_append_rope S={S} R={R} P={P} page={page} first={first} indexed={indexed}",
-          flush=True)
+    print(f"[case] prefill_dense_append_rope S={S} R={R} P={P} page={page} first={first} indexed={indexed} "
+          f"causal={causal}", flush=True)
     out = q3attn.prefill_dense_append_rope(q, k, v, pk, pv, qn, kn, cos, sin, kc, vc,
-                                           torch.from_numpy(bt).to(dev), scale, pidx, True, 1e-6, first)
+                                           torch.from_numpy(bt).to(dev), scale, pidx, causal, 1e-6, first)
     torch.cuda.synchronize()
     # the oracle's producers and attention
     sel = pidx.cpu().numpy() if indexed else np.arange(S)
@@ -118,8 +115,8 @@ def test_dense_append_rope_matches_oracle(cuda_device, S, R, P, page, first, ind
     k_o = _eager_norm_rope_np(to_np(k), to_np(kn), cn, sn)
     K = np.concatenate([to_np(pk)[sel], k_o], axis=1)
     V = np.concatenate([to_np(pv)[sel], to_np(v)], axis=1)
-    ok, st = ora.compare(to_np(out), ora.prefill_prefix(q_o, K, V, scale))
-    print(f"[parity] prefill_dense_append_rope S={S} R={R} P={P} vs oracle {st}", flush=True)
+    ok, st = ora.compare(to_np(out), ora.prefill_prefix(q_o, K, V, scale, causal=causal))
+    print(f"[parity] prefill_dense_append_rope S={S} R={R} P={P} causal={causal} vs oracle {st}", flush=True)
     assert ok, st
     # the pool: rows first..n-1 as the producers give them, every other slot still NaN
     kp, vp = _pool_rows(to_np(kc), bt, n, page), _pool_rows(to_np(vc), bt, n, page)

@@ -251,6 +251,20 @@ def test_prefill_prefix_reduces_and_bruteforce():
     np.testing.assert_allclose(a[0], b, atol=1e-12)
 
 
+def test_prefill_prefix_non_causal_is_sdpa_without_mask():
+    r = np.random.default_rng(43)
+    S, R, n, Hq, Hkv, D = 3, 6, 11, 8, 4, 16
+    q = _bf16(r.standard_normal((S, R, Hq, D)))
+    K = _bf16(r.standard_normal((S, n, Hkv, D)))
+    V = _bf16(r.standard_normal((S, n, Hkv, D)))
+    got = ora.prefill_prefix(q, K, V, 0.25, acc=np.float64, causal=False)
+    t = lambda x: torch.from_numpy(x.astype(np.float64)).transpose(1, 2)
+    want = torch.nn.functional.scaled_dot_product_attention(t(q), t(K), t(V), scale=0.25, enable_gqa=True)
+    np.testing.assert_allclose(got, want.transpose(1, 2).numpy(), atol=1e-12)
+    # and differs from the causal form wherever a query has keys past its diagonal
+    assert np.abs(got - ora.prefill_prefix(q, K, V, 0.25, acc=np.float64)).max() > 1e-3
+
+
 # ----------------------------------------------------------------------------- rms / rope
 def test_rms_rope_invariants():
     x = RNG.standard_normal((64, 128)).astype(np.float32) * 3
