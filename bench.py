@@ -922,6 +922,106 @@ def bench_admit_append(args, dev, wls):
     return res
 
 
+def bench_probe(args, dev):
+    """Measured HBM ceilings on this GPU (libq3probe.so, beside the attention library): the 576-row decode's exact K/V
+    access pattern read with no arithmetic, records or combine (q3p_tile_read over the same 28 per-layer tables and
+    contexts, one launch per layer in a captured graph, the resident grid over equal tile ranges), the decode itself on
+    the same frame, a plain streaming read of 4 GiB with and without the non-temporal hint (q3p_stream_read), and a
+    2 GiB device copy (read + write).  The decode's K/V rate over the probe's is the fraction of the practical ceiling
+    of its access pattern; the copy rate bounds kernels that read and write in equal measure."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    plib = ctypes.CDLL(os.path.join(ROOT, "qwen3-tts-engine_amd", "q3attn", "libq3probe.so"))
+    vp, i64, ci, u32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32
+    plib.q3p_tile_read.argtypes = [vp, vp, i64, i64, i64, ci, ci, ci, vp, ci, ci, u32, vp, vp]
+    plib.q3p_stream_read.argtypes = [vp, ctypes.c_size_t, ci, ci, u32, vp, vp]
+    plib.q3p_resident_grid.argtypes = [ci, ci]
+    magic = 0x9E3779B9
+    wl = W.make_decode("decode576", dev, layers=LAYERS, seed=args.seed)
+    kc, vc = wl.k_cache, wl.v_cache
+    kv_bytes = 2 * 8 * 128 * 2 * int(wl.ctx.sum())
+    tiles = []
+    for L in wl.layers:
+        bt = L.block_table.cpu().numpy()
+        rows = [np.stack([bt[b, : (c + 15) // 16], np.minimum(16, c - 16 * np.arange((c + 15) // 16))], 1)
+                for b, c in enumerate(wl.ctx) if c > 0]
+        tiles.append(torch.from_numpy(np.concatenate(rows).astype(np.int32)).to(dev))
+    nt = int(tiles[0].shape[0])
+    grid = plib.q3p_resident_grid(1, 8)
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)   # one word per workgroup of either probe
+    stream = lambda: torch.cuda.current_stream(dev).cuda_stream
+
+    def probe_frame():
+        for t in tiles:
+            rc = plib.q3p_tile_read(kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
+                                    kc.shape[0], 16, 8, t.data_ptr(), nt, grid, magic, sink.data_ptr(), stream())
+            if rc:
+                raise RuntimeError(f"q3p_tile_read failed ({rc})")
+        return [sink]
+
+    def decode_frame():
+        return [q3attn.paged_decode(L.q, kc, vc, wl.cache_seqlens, L.block_table, wl.scale, 0) for L in wl.layers]
+
+    res = {}
+    for name, fn in (("tile_read", probe_frame), ("decode", decode_frame), ("tile_read_again", probe_frame)):
+        _, frame_ms, _ = time_graph(dev, fn, args.steps, args.warmup, 1.0)
+        us = statistics.median(frame_ms) * 1e3 / LAYERS
+        res[name] = {"us_per_call": round(us, 2), "kv_gbps": round(kv_bytes / (us * 1e-6) / 1e9, 1)}
+        log(f"[probe] {name}: {us:.2f} us per layer call, K/V {kv_bytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    del wl, tiles
+    torch.cuda.empty_cache()
+    ceiling = min(res["tile_read"]["us_per_call"], res["tile_read_again"]["us_per_call"])
+    res["decode_over_probe"] = round(ceiling / res["decode"]["us_per_call"], 4)
+
+    sgrid = plib.q3p_resident_grid(0, 0) * 2
+    n = 4 << 30
+    buf = torch.empty(n, dtype=torch.uint8, device=dev)
+    buf.fill_(7)
+    for nt_flag in (1, 0):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        for _ in range(2):
+            plib.q3p_stream_read(buf.data_ptr(), n // 16, sgrid, nt_flag, magic, sink.data_ptr(), stream())
+        ev[0].record()
+        reps = 5
+        for _ in range(reps):
+            plib.q3p_stream_read(buf.data_ptr(), n // 16, sgrid, nt_flag, magic, sink.data_ptr(), stream())
+        ev[1].record()
+        torch.cuda.synchronize()
+        gbps = n * reps / (ev[0].elapsed_time(ev[1]) * 1e-3) / 1e9
+        res["stream_read_nt_gbps" if nt_flag else "stream_read_gbps"] = round(gbps, 1)
+        log(f"[probe] streaming read of 4 GiB ({'non-temporal' if nt_flag else 'plain'}): {gbps:.0f} GB/s")
+    src, dst = buf[: n // 2], buf[n // 2:]
+    for _ in range(2):
+        dst.copy_(src)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(5):
+        dst.copy_(src)
+    ev[1].record()
+    torch.cuda.synchronize()
+    gbps = 2 * (n // 2) * 5 / (ev[0].elapsed_time(ev[1]) * 1e-3) / 1e9
+    res["copy_read_plus_write_gbps"] = round(gbps, 1)
+    log(f"[probe] 2 GiB device copy: {gbps:.0f} GB/s read + write")
+    del buf
+    torch.cuda.empty_cache()
+    rec = base_record("HBM read ceiling of the 576-row decode's access pattern, 1×MI355X",
+                      res["tile_read"]["kv_gbps"], "GB/s", args, ceiling * LAYERS / 1e3, True, {
+                          "workload": "the 576-row decode's K/V tiles (518 live rows, ctx log-uniform [64, 1800], "
+                                      "16-token pages, 28 per-layer random tables over a 131072-page pool) read with "
+                                      "the decode's loads and no arithmetic; 4 GiB streaming reads; a 2 GiB copy",
+                          "tiles_per_call": nt, "grid": grid, "parallelism": "single GPU"})
+    rec.update(res)
+    rec["roofline"] = {"bound": "hbm", "achieved": res["tile_read"]["kv_gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                       "frac": round(res["tile_read"]["kv_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None}
+    return rec
+
+
 def other_workloads(args, dev):
     """Short runs of the other configurations beside the headline (20 graph replays each; `--workload NAME` gives the
     full line of each): the 256-row and 1-row x 64-token decodes (with their CPU baselines unless --no-cpu-baseline),
@@ -974,7 +1074,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="decode576",
-                    choices=["decode576", "decode256", "decode1x64", "decode-small", "cp512", "prefill32", "admit"],
+                    choices=["decode576", "decode256", "decode1x64", "decode-small", "cp512", "prefill32", "admit",
+                             "probe"],
                     help="c5 (default, the headline metric), c3 decode, c1 decode, decode at small batches (row-parallel "
                          "kernel vs stream-K), c2 code predictor, c4 prefill, admit fast-admission prefill")
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
@@ -1018,6 +1119,8 @@ def main() -> int:
                 rec["cpu_baseline"]["per_config"] = per
     elif args.workload == "decode-small":
         rec = bench_decode_small(args, dev)
+    elif args.workload == "probe":
+        rec = bench_probe(args, dev)
     elif args.workload == "cp512":
         rec = bench_cp(args, dev)
     elif args.workload == "admit":

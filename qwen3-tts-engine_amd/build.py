@@ -14,6 +14,9 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "q3attn", "libq3attn.so")
+# HBM probes (measurement infrastructure for bench.py --workload probe), a library of their own
+PROBE_SRC = os.path.join(HERE, "probe", "hbm_probe.hip")
+PROBE_OUT = os.path.join(HERE, "q3attn", "libq3probe.so")
 BUILD = os.path.join(HERE, "_build")
 ARCH = os.environ.get("Q3A_OFFLOAD_ARCH", "gfx950")
 
@@ -45,7 +48,7 @@ def scratch_users(remarks: str) -> list[str]:
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    obj = os.path.join(BUILD, os.path.basename(os.path.dirname(src)) + "_" + os.path.basename(src) + ".o")
     cmd = [HIPCC, *CFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     lines = [ln for ln in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in ln]
@@ -64,16 +67,17 @@ def _compile(src: str) -> str:
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = OUT + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
-    os.replace(tmp, OUT)
-    if verbose:
-        print(f"built {OUT}")
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs) + 1)) as ex:
+        objs = list(ex.map(_compile, srcs + [PROBE_SRC]))
+    for out, parts in ((OUT, objs[:-1]), (PROBE_OUT, objs[-1:])):
+        tmp = out + ".tmp"
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *parts, "-o", tmp]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
+        os.replace(tmp, out)
+        if verbose:
+            print(f"built {out}")
     return OUT
 
 
