@@ -29,8 +29,8 @@ Pinning (what independent check fixes each function; see tests/test_oracle.py):
 * ``norm_rope``         -- eager form: bit for bit against torch's CPU bf16 kernels running
                            engine/ops.py:51-60 (rows of RMS 1e-4..10, so eps matters); planted
                            mistakes (weight before the cast, no eps, swapped halves, cos/sin
-                           swapped) fail that check.  Compiled form: within one bf16 unit of the
-                           eager form and of the reference's chain in float64.
+                           swapped) fail that check.  Compiled form: equal to the same chain in
+                           float64 rounded once up to double roundings, within one bf16 unit.
 * ``rope_tables``       -- closed-form frequencies (theta**(-2i/D)) checked at chosen indices.
 """
 from __future__ import annotations
@@ -117,23 +117,24 @@ def norm_rope(x: np.ndarray, w: np.ndarray, cos: np.ndarray, sin: np.ndarray, ep
     engine/talker.py:69-70, 158-159 and engine/arrivals.py:112-118).  x, w, cos, sin hold bf16 values; the result is
     bf16 values in float32.
 
-    rms: r = 1 / sqrt(mean(x^2) + eps) in float32, n = bf16(x * r) (the explicit ``.to(x.dtype)``), y = w * n.
+    rms: r = 1 / sqrt(mean(x^2) + eps) in float32, n = (x * r).to(bf16) (the explicit cast), y = w * n.
     rope: y * cos + cat(-y[h:], y[:h]) * sin.
     * eager=True -- eager torch bf16 ops (``prefill_hidden`` and the admission layer are not compiled,
-      engine/arrivals.py:57-61): every op rounds its result, y = bf16(w * n), o = bf16(bf16(y cos) + bf16(rot(y) sin)).
-      Torch's CPU bf16 kernels give these bits exactly.
-    * eager=False -- the chain with the cast kept and nothing else rounded until the result: y = w * n in float32,
-      o = bf16(y cos + rot(y) sin).  This is the form the HIP kernels of the compiled callers (``Talker._decode``,
-      ``CodePredictor._pre``, engine/talker.py:56-59, engine/code_predictor.py:25-29) compute; what a compiler emits for
-      the same source depends on its backend (which intermediates it materialises or rounds).
-    The mean of squares is summed in numpy's order; another order moves mean(x^2) by an fp32 unit, which can move n,
-    and with it o, by a bf16 unit on rare elements."""
+      engine/arrivals.py:57-61): every op rounds its result, y = bf16(w * bf16(x * r)),
+      o = bf16(bf16(y cos) + bf16(rot(y) sin)).  Torch's CPU bf16 kernels give these bits exactly.
+    * eager=False -- the chain as torch.compile's GPU kernels evaluate it for the compiled callers (``Talker._decode``,
+      ``CodePredictor._pre``, engine/talker.py:56-59, engine/code_predictor.py:25-29): every intermediate stays in
+      float32, the cast inside rms included, and the result is rounded once: y = w * (x * r),
+      o = bf16(y cos + rot(y) sin), each product and the sum a separate float32 operation (measured on MI355X: the
+      compiled producers equal this on every element of 262,144).
+    The mean of squares is summed in numpy's order; another order moves mean(x^2) by an fp32 unit, which can move the
+    result by a bf16 unit on rare elements."""
     xf = np.asarray(x, np.float32)
-    n = _normalise(xf, _rsqrt_mean_sq(xf, eps))
+    r = _rsqrt_mean_sq(xf, eps)
     if eager:
-        y = bf16_round(np.asarray(w, np.float32) * n)
+        y = bf16_round(np.asarray(w, np.float32) * _normalise(xf, r))
         return bf16_round(bf16_round(y * cos) + bf16_round(_rotate_half(y) * sin))
-    y = (np.asarray(w, np.float32) * n).astype(np.float32)
+    y = (np.asarray(w, np.float32) * (xf * r).astype(np.float32)).astype(np.float32)
     return bf16_round((y * cos + _rotate_half(y) * sin).astype(np.float32))
 
 

@@ -158,14 +158,15 @@ __device__ __forceinline__ float max_xor16(float x) { const float2 r = swap16(x)
 
 // ---------------------------------------------------------------------------------- qk-norm + RoPE
 // One 128-dim bf16 head row x, its RMSNorm weight w and the row's RoPE cos/sin (engine/ops.py:51-60, the talker's
-// q/k producers at engine/talker.py:69-70):
-//   y = bf16(x * rsqrt(mean(x^2) + eps)) * w        (normalise in fp32, round to bf16, scale)
-//   o = bf16(y * cos + rot(y) * sin),  rot(y) = (-y[64:], y[:64])
-// The rope is evaluated in fp32 and rounded once, as the compiled talker evaluates the fused rms -> rope chain; its
-// products are exact in fp32 (bf16 x bf16 x bf16 needs at most 24 significant bits).  The sum of squares follows one
-// binary tree over the dims in index order (pairs, pairs of pairs, ...), so the 16-lane layout (8 dims per lane,
-// used where a row meets the tile engine) and the 64-lane layout (2 dims per lane, used where a row is stored) give
-// the same bits.  All lanes of the wave must be active.
+// q/k producers at engine/talker.py:69-70 and the code predictor's at engine/code_predictor.py:38-43), as the
+// compiled callers evaluate them (torch.compile'd Talker._decode and CodePredictor._pre, whose generated kernels
+// keep the whole chain in fp32 and round once at the store; the explicit cast inside rms is not materialised):
+//   y = (x * rsqrt(mean(x^2) + eps)) * w            (fp32)
+//   o = bf16(y * cos + rot(y) * sin),  rot(y) = (-y[64:], y[:64])   (two fp32 products and an fp32 sum, not fused)
+// Contraction into FMA is off in these helpers so the products round as separate multiplies.  The sum of squares
+// follows one binary tree over the dims in index order (pairs, pairs of pairs, ...), so the 16-lane layout (8 dims per
+// lane, used where a row meets the tile engine) and the 64-lane layout (2 dims per lane, used where a row is stored)
+// give the same bits.  All lanes of the wave must be active.
 constexpr int kDppRor8 = 0x128;  // row_ror:8 (lane i <- lane i^8 within each 16 lanes)
 
 __device__ __forceinline__ float rms_rsqrt(float sumsq, float eps) {
@@ -174,6 +175,7 @@ __device__ __forceinline__ float rms_rsqrt(float sumsq, float eps) {
 
 // Lane l of each aligned 16-lane group holds dims 8*(l%16)..+8 of its row (x, w, cos, sin alike).
 __device__ __forceinline__ uint4 qk_norm_rope16(uint4 x, uint4 w, uint4 c, uint4 s, float eps) {
+#pragma clang fp contract(off)
   const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ws[4] = {w.x, w.y, w.z, w.w};
   const uint32_t cs[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
   float v[8];
@@ -191,14 +193,14 @@ __device__ __forceinline__ uint4 qk_norm_rope16(uint4 x, uint4 w, uint4 c, uint4
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float y[2], out[2];
-    y[0] = round_bf16(v[2 * i] * r) * bf16_lo(ws[i]);
-    y[1] = round_bf16(v[2 * i + 1] * r) * bf16_hi(ws[i]);
+    y[0] = (v[2 * i] * r) * bf16_lo(ws[i]);
+    y[1] = (v[2 * i + 1] * r) * bf16_hi(ws[i]);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const float yp = dpp_f32<kDppRor8>(y[e]);
       const float cv = e ? bf16_hi(cs[i]) : bf16_lo(cs[i]);
       const float sv = e ? bf16_hi(ss[i]) : bf16_lo(ss[i]);
-      out[e] = fmaf(y[e], cv, (lo ? -yp : yp) * sv);
+      out[e] = y[e] * cv + (lo ? -yp : yp) * sv;
     }
     o[i] = pack_bf16x2(out[0], out[1]);
   }
@@ -243,6 +245,7 @@ __device__ __forceinline__ uint4 qk_norm_rope16_eager(uint4 x, uint4 w, uint4 c,
 // s), for kernels whose tile pipeline leaves few registers free: same arithmetic, same bits.
 __device__ __forceinline__ uint4 qk_norm_rope16_lds(uint4 x, const uint8_t* w, const uint8_t* c, const uint8_t* s,
                                                     float eps) {
+#pragma clang fp contract(off)
   const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
   float p[4];
 #pragma unroll
@@ -258,27 +261,28 @@ __device__ __forceinline__ uint4 qk_norm_rope16_lds(uint4 x, const uint8_t* w, c
     const uint32_t ww = *reinterpret_cast<const uint32_t*>(w + 4 * i);
     const uint32_t cw = *reinterpret_cast<const uint32_t*>(c + 4 * i);
     const uint32_t sw = *reinterpret_cast<const uint32_t*>(s + 4 * i);
-    const float y0 = round_bf16(bf16_lo(xs[i]) * r) * bf16_lo(ww);
-    const float y1 = round_bf16(bf16_hi(xs[i]) * r) * bf16_hi(ww);
+    const float y0 = (bf16_lo(xs[i]) * r) * bf16_lo(ww);
+    const float y1 = (bf16_hi(xs[i]) * r) * bf16_hi(ww);
     const float p0 = dpp_f32<kDppRor8>(y0), p1 = dpp_f32<kDppRor8>(y1);
-    o[i] = pack_bf16x2(fmaf(y0, bf16_lo(cw), (lo ? -p0 : p0) * bf16_lo(sw)),
-                       fmaf(y1, bf16_hi(cw), (lo ? -p1 : p1) * bf16_hi(sw)));
+    o[i] = pack_bf16x2(y0 * bf16_lo(cw) + (lo ? -p0 : p0) * bf16_lo(sw),
+                       y1 * bf16_hi(cw) + (lo ? -p1 : p1) * bf16_hi(sw));
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // Lane l holds dims 2l, 2l+1 of the row.
 __device__ __forceinline__ uint32_t qk_norm_rope64(uint32_t x, uint32_t w, uint32_t c, uint32_t s, float eps) {
+#pragma clang fp contract(off)
   const float v0 = bf16_lo(x), v1 = bf16_hi(x);
   const float p = row16_sum(v0 * v0 + v1 * v1);
   const float r = rms_rsqrt(sum_xor32(sum_xor16(p)), eps);
-  const float y0 = round_bf16(v0 * r) * bf16_lo(w);
-  const float y1 = round_bf16(v1 * r) * bf16_hi(w);
+  const float y0 = (v0 * r) * bf16_lo(w);
+  const float y1 = (v1 * r) * bf16_hi(w);
   const float2 e0 = swap32(y0), e1 = swap32(y1);  // (lane l & ~32's value, lane l | 32's value)
   const bool lo = (threadIdx.x & 32) == 0;
   const float yp0 = lo ? e0.y : e0.x, yp1 = lo ? e1.y : e1.x;
-  const float o0 = fmaf(y0, bf16_lo(c), (lo ? -yp0 : yp0) * bf16_lo(s));
-  const float o1 = fmaf(y1, bf16_hi(c), (lo ? -yp1 : yp1) * bf16_hi(s));
+  const float o0 = y0 * bf16_lo(c) + (lo ? -yp0 : yp0) * bf16_lo(s);
+  const float o1 = y1 * bf16_hi(c) + (lo ? -yp1 : yp1) * bf16_hi(s);
   return pack_bf16x2(o0, o1);
 }
 

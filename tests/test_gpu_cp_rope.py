@@ -25,11 +25,9 @@ D = 128
 
 
 def _compiled_norm_rope_np(x, w, cos, sin, eps=1e-6):
-    """engine/ops.py:51-60 as the compiled step evaluates it: y = bf16(x * rsqrt(mean(x^2) + eps)) * w (exact in
-    fp32), then one rounding of y * cos + rot(y) * sin (both products exact in fp32)."""
-    y = ora.rms(x, None, eps, to_bf16=True) * w
-    rot = np.concatenate([-y[..., D // 2:], y[..., : D // 2]], axis=-1)
-    return ora.bf16_round(y * cos + rot * sin)
+    """engine/ops.py:51-60 as the compiled step evaluates it (the oracle's compiled form: float32 throughout, one
+    rounding at the end)."""
+    return ora.norm_rope(x, w, cos, sin, eps, eager=False)
 
 
 def _step_inputs(dev, B, seed):

@@ -172,9 +172,10 @@ def test_chunks_append_bit_identical_to_index_copy(cuda_device, max_ctx, ctx):
 
 
 def test_chunks_rope_form_exact_rows(cuda_device):
-    """+-1 head rows: mean(x^2) = 1, the normalised rows are exact, so the norm/rope form equals the append form on
-    the oracle's q', k' bit for bit (output and pool)."""
-    EPS = 1e-6
+    """+-1 head rows with eps = 0: mean(x^2) = 1 and 1/sqrt of it 1, the normalised rows are exactly +-w and the rope
+    products exact, so the norm/rope form equals the append form on the oracle's q', k' bit for bit (output and
+    pool)."""
+    EPS = 0.0
     ctx = np.array([1, 129, 1800, 256, 2048, 0])
     wl = W.make_decode("chunks_rope", cuda_device, ctx=ctx, num_pages=2048, max_ctx=2048, seed=77)
     dev = cuda_device
@@ -188,8 +189,8 @@ def test_chunks_rope_form_exact_rows(cuda_device):
     cos_t, sin_t = ora.rope_tables(2048)
     pos = np.maximum(ctx - 1, 0)
     cos, sin = r(cos_t[pos]), r(sin_t[pos])
-    qq = ora.bf16_round(ora.rope(ora.rms(q, qn, eps=EPS), cos[:, None], sin[:, None]))
-    kk = ora.bf16_round(ora.rope(ora.rms(k, kn, eps=EPS), cos[:, None], sin[:, None]))
+    qq = ora.norm_rope(q, qn, cos[:, None], sin[:, None], EPS, eager=False)
+    kk = ora.norm_rope(k, kn, cos[:, None], sin[:, None], EPS, eager=False)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev).to(torch.bfloat16)
     old = torch.from_numpy(ctx - 1).to(torch.int32).to(dev)
     L = wl.layers[0]

@@ -2,12 +2,13 @@
 
 The reference block is engine/talker.py:69-77: q = rope(rms(q_raw, qn)), k = rope(rms(k_raw, kn)) (engine/ops.py:51-60),
 k and v written into the pool with index_copy_, then the paged attention.  Expected values come from the oracle's
-restatement of rms/rope (oracle.attention.rms / rope, fp32 rope rounded once to bf16) and its decode attention.
+restatement of the producers as the compiled talker evaluates them (oracle.attention.norm_rope, eager=False: float32
+throughout, one rounding) and its decode attention.
 
 Two kinds of check:
-* exact inputs: head rows of +-1 entries have mean(x^2) = 1, so the normalised row is exactly +-1 in bf16 and the
-  whole transform is exact arithmetic; the fused call must then match paged_decode_append on the oracle's q and k
-  bit for bit, output and pool (this also proves the slot receives the k the new token was attended with);
+* exact inputs: head rows of +-1 entries with eps = 0 have mean(x^2) = 1 and 1/sqrt of it 1, so the normalised row is
+  exactly +-w and the rope products are exact; the fused call must then match paged_decode_append on the oracle's q
+  and k bit for bit, output and pool (this also proves the slot receives the k the new token was attended with);
 * random inputs: output within the 2e-2 / 2e-3 bar of the oracle, the written k rows within the bound a one-unit
   change of the normalised value allows (fp32 sums of squares in another order, _k_rows_close) and at least 99 %
   bit-identical."""
@@ -63,9 +64,9 @@ def _inputs(wl, seed, exact):
 
 
 def _k_rows_close(got, k, kn, kk):
-    """The written k rows against the oracle's: a sum of squares taken in another order can move the normalised value
-    y = bf16(x * r) by one bf16 unit, which moves y*cos + rot(y)*sin by up to 2^-8 (|y| + |rot(y)|) before its own
-    rounding (2^-8 |k'|); beyond that bound a row is wrong.  Returns (all within, fraction bit-identical)."""
+    """The written k rows against the oracle's: a sum of squares taken in another order moves r by an fp32 unit, which
+    moves y*cos + rot(y)*sin by far less than 2^-8 (|y| + |rot(y)|) before its own rounding (2^-8 |k'|); beyond that
+    bound a row is wrong.  Returns (all within, fraction bit-identical)."""
     y = ora.rms(k, kn, eps=EPS)
     rot = np.concatenate([-y[..., 64:], y[..., :64]], axis=-1)
     bound = 2.0 ** -8 * (np.abs(y) + np.abs(rot)) + 2.0 ** -7 * np.abs(kk) + 1e-30
@@ -73,14 +74,15 @@ def _k_rows_close(got, k, kn, kk):
     return bool((d <= bound).all()), float((d == 0).mean())
 
 
-def _oracle_qk(q, k, qn, kn, cos, sin):
+def _oracle_qk(q, k, qn, kn, cos, sin, eps=EPS):
     """q' and k' as the oracle computes them (bf16 values in float32)."""
-    qq = ora.bf16_round(ora.rope(ora.rms(q, qn, eps=EPS), cos[:, None, :], sin[:, None, :]))
-    kk = ora.bf16_round(ora.rope(ora.rms(k, kn, eps=EPS), cos[:, None, :], sin[:, None, :]))
+    qq = ora.norm_rope(q, qn, cos[:, None, :], sin[:, None, :], eps, eager=False)
+    kk = ora.norm_rope(k, kn, cos[:, None, :], sin[:, None, :], eps, eager=False)
     return qq, kk
 
 
 def _run(wl, seed, exact, qkv_views=False, cs3=False):
+    eps = 0.0 if exact else EPS
     dev = wl.k_cache.device
     q, k, v, qn, kn, cos, sin = _inputs(wl, seed, exact)
     B = wl.batch
@@ -105,9 +107,9 @@ def _run(wl, seed, exact, qkv_views=False, cs3=False):
         ct, st = ct[:, None, :], st[:, None, :]
     L = wl.layers[0]
     out = q3attn.paged_decode_append_rope(qt, kt, vt, _bf16(qn, dev), _bf16(kn, dev), ct, st, wl.k_cache, wl.v_cache,
-                                          old, L.block_table, wl.scale, EPS)
+                                          old, L.block_table, wl.scale, eps)
     torch.cuda.synchronize()
-    qq, kk = _oracle_qk(q, k, qn, kn, cos, sin)
+    qq, kk = _oracle_qk(q, k, qn, kn, cos, sin, eps)
     return out, qq, kk, v, old, pristine_k, pristine_v, slots
 
 

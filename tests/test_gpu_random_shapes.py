@@ -96,8 +96,8 @@ def test_decode_random_shapes(cuda_device, seed):
             out = q3attn.paged_decode_append_rope(_bf16(q, dev), _bf16(kn, dev), _bf16(vn, dev), _bf16(qn, dev),
                                                   _bf16(knw, dev), _bf16(cos, dev), _bf16(sin, dev), kc, vc, old,
                                                   bt_d, scale, EPS)
-            qq = ora.bf16_round(ora.rope(ora.rms(q, qn, eps=EPS), cos[:, None], sin[:, None]))
-            kk = ora.bf16_round(ora.rope(ora.rms(kn, knw, eps=EPS), cos[:, None], sin[:, None]))
+            qq = ora.norm_rope(q, qn, cos[:, None], sin[:, None], EPS, eager=False)
+            kk = ora.norm_rope(kn, knw, cos[:, None], sin[:, None], EPS, eager=False)
         torch.cuda.synchronize()
         # The oracle's pool: the kernel's own writes are checked against kk / vn, then replaced by them.
         k, v, table = _compact(kc, vc, bt, ctx, page)

@@ -6,9 +6,10 @@ them (oracle.attention.norm_rope) and as the tests' torch copies run them (oracl
   matters at the low end), random weights and RoPE rows of positions 0..2047.
 * Mistakes planted in the oracle (the weight applied before the bf16 cast, eps dropped, the rotate-half halves
   swapped, cos and sin swapped, the sum of squares in place of the mean) each fail that check.
-* Compiled form (the cast kept, nothing else rounded until the result; what the HIP kernels of the compiled callers
-  compute): equal to the float64 evaluation of the same chain rounded once, up to the rare double rounding of its
-  fp32 sum, and within the eager form's per-term roundings of it.
+* Compiled form (every intermediate in float32 and one rounding at the end, as torch.compile's GPU kernels evaluate
+  the chain; what the HIP kernels of the compiled callers compute): within one bf16 unit of the float64 evaluation of
+  the same chain rounded once, equal on all but the elements its fp32 roundings move across a bf16 rounding boundary,
+  and within the eager form's per-term roundings of it.
 """
 import numpy as np
 import pytest
@@ -88,21 +89,21 @@ def test_planted_mistakes_fail_the_torch_check(monkeypatch, name):
 def test_compiled_form_is_the_chain_rounded_once():
     x, w, cos, sin = _inputs(5)
     got = ora.norm_rope(x, w, cos, sin, eager=False)
-    # the same chain in float64: n = bf16(x * r) with r from the float64 mean, y = w * n, one rounding at the end
+    # the same chain in float64: y = w * x * r with r from the float64 mean, one rounding at the end
     xd = x.astype(np.float64)
     r = 1.0 / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-6)
-    n = _bf16((xd * r).astype(np.float32))
-    y = w.astype(np.float64) * n
+    y = w.astype(np.float64) * xd * r
     rot = np.concatenate([-y[..., D // 2:], y[..., : D // 2]], axis=-1)
     ref = _bf16((y * cos + rot * sin).astype(np.float32))
     ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
     d = np.abs(got - ref)
-    assert (d <= ulp).all() and (d == 0).mean() > 0.995, (d.max(), (d == 0).mean())
+    bound_terms = 2.0 ** -22 * (np.abs(y * cos) + np.abs(rot * sin))   # the fp32 products' and sum's rounding
+    assert (d <= ulp + bound_terms).all() and (d == 0).mean() > 0.99, (d.max(), (d == 0).mean())
     # eager rounds y, y cos and rot(y) sin separately: where the two terms cancel the difference is bounded by the
     # terms' rounding, not the result's
     eager = ora.norm_rope(x, w, cos, sin, eager=True)
     de = np.abs(got - eager)
-    bound = 2.0 ** -7 * (np.abs(y * cos) + np.abs(rot * sin)) + ulp
+    bound = 2.0 ** -6 * (np.abs(y * cos) + np.abs(rot * sin)) + ulp
     assert (de <= bound).all() and (de == 0).mean() > 0.5, ((de / bound).max(), (de == 0).mean())
     print(f"[producers] compiled form: {(d == 0).mean():.5f} equal to the float64 chain, "
           f"{(de == 0).mean():.4f} equal to the eager form", flush=True)
