@@ -1068,6 +1068,35 @@ def other_workloads(args, dev):
     return out
 
 
+def rocprof_summary(src: str, dst: str) -> None:
+    """Condense rocprofv3 CSV output (one directory per run under src) into small files under dst: each run's
+    kernel_stats.csv as it is, and for counter runs the dispatch count, median and mean of every counter per kernel
+    (this library's kernels, the probe's and the device copy used for calibration).  Raw per-dispatch counter files of
+    a full bench run are tens of MB; these summaries are what profiles/*.md cite."""
+    import csv
+    import glob
+
+    os.makedirs(dst, exist_ok=True)
+    for d in sorted(glob.glob(os.path.join(src, "*"))):
+        name = os.path.basename(d)
+        for f in glob.glob(os.path.join(d, "*kernel_stats.csv")):
+            with open(f) as i, open(os.path.join(dst, f"{name}_kernel_stats.csv"), "w") as o:
+                o.write(i.read())
+        for f in glob.glob(os.path.join(d, "*counter_collection.csv")):
+            vals = {}
+            with open(f) as i:
+                for r in csv.DictReader(i):
+                    k = r["Kernel_Name"]
+                    if "q3a" in k or "q3p" in k or "copyBuffer" in k:
+                        vals.setdefault((k, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+            with open(os.path.join(dst, f"{name}_pmc.csv"), "w", newline="") as o:
+                w = csv.writer(o)
+                w.writerow(["kernel", "counter", "dispatches", "median", "mean"])
+                for (k, c), v in sorted(vals.items()):
+                    w.writerow([k, c, len(v), statistics.median(v), statistics.mean(v)])
+    print(json.dumps({"rocprof_summary": sorted(os.listdir(dst))}), flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1087,7 +1116,12 @@ def main() -> int:
                     help="576-row decode only: skip the short GPU-only runs of the other workloads (other_workloads field)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates rocprof byte counters)")
+    ap.add_argument("--rocprof-summary", nargs=2, metavar=("SRC", "DST"),
+                    help="no GPU work: condense the rocprofv3 CSV runs under SRC into per-kernel summaries under DST")
     args = ap.parse_args()
+    if args.rocprof_summary:
+        rocprof_summary(*args.rocprof_summary)
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
