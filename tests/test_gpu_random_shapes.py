@@ -78,6 +78,16 @@ def test_decode_random_shapes(cuda_device, seed):
         torch.cuda.synchronize()
         k, v, table = _compact(kc, vc, bt, ctx, page)
         ref = ora.paged_decode(q, k, v, ctx, table, scale)
+        # the same inputs through each decomposition the shape allows (the path codes force one kernel)
+        for code in (q3attn.DECODE_ROW, q3attn.DECODE_CHUNKS, q3attn.DECODE_STREAMK):
+            if code == q3attn.DECODE_ROW and P * page > 2048:
+                continue
+            o = q3attn.paged_decode(_bf16(q, dev), kc, vc, seq, bt_d, scale, code)
+            torch.cuda.synchronize()
+            ok, st = ora.compare(to_np(o), ref)
+            print(f"[random] decode {label} path {code} {st}", flush=True)
+            assert ok, (label, code, st)
+            assert not o[torch.from_numpy(ctx == 0).to(dev)].float().abs().sum().item(), (label, code)
     else:
         kn = ora.bf16_round(rng.standard_normal((B, hkv, 128)).astype(np.float32) *
                             (1.0 if mode == "append" else rng.uniform(0.3, 3.0, (B, hkv, 1)).astype(np.float32)))

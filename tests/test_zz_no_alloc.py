@@ -50,6 +50,22 @@ def test_noalloc_matches_workspace_entry_point_twice(cuda_device):
     assert not out2[ctx == 0].float().abs().sum().item()
 
 
+def test_noalloc_chunked_path_twice(cuda_device):
+    """Small batches of long tables take the chunked kernel, whose fp32 chunk records live in the scratch: two calls
+    in a row (8 rows, then 2 rows with shorter contexts, so the second call's combine meets the first call's stale
+    records past its rows' ends) each equal the workspace entry point bit for bit."""
+    for B, hi, seed in ((8, 2048, 41), (2, 700, 42)):
+        rng = np.random.default_rng(seed)
+        ctx = rng.integers(1, hi + 1, size=B)
+        ctx[0] = hi
+        wl = W.make_decode("small", cuda_device, ctx=ctx, num_pages=4 * B * 128 + 64, max_ctx=2048, seed=seed)
+        print(f"[noalloc] chunked path: {B} rows, {int(ctx.sum())} tokens", flush=True)
+        out, want = _case(wl)
+        assert torch.equal(out, want)
+        del wl
+        torch.cuda.empty_cache()
+
+
 def test_noalloc_rejects_shapes_beyond_the_scratch(cuda_device):
     B, P = 5000, 128                       # fixed splits: 5000 rows x 32 splits x 8 heads x 528 B >> 8 MiB
     q = torch.zeros(B, 16, 128, dtype=torch.bfloat16, device=cuda_device)
