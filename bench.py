@@ -1105,15 +1105,19 @@ def main() -> int:
     ap.add_argument("--workload", default="decode576",
                     choices=["decode576", "decode256", "decode1x64", "decode-small", "cp512", "prefill32", "admit",
                              "probe"],
-                    help="c5 (default, the headline metric), c3 decode, c1 decode, decode at small batches (row-parallel "
-                         "kernel vs stream-K), c2 code predictor, c4 prefill, admit fast-admission prefill")
-    ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = stream-K)")
+                    help="c5 (default, the headline metric), c3 decode, c1 decode, decode at small batches (each "
+                         "decode kernel by path code and the library's choice), c2 code predictor, c4 prefill, admit "
+                         "fast-admission prefill, probe (HBM read ceilings of the decode's access pattern)")
+    ap.add_argument("--split", type=int, default=0,
+                    help="decode split_tokens: 0 = the library's choice (stream-K at 576 rows), -1 row-parallel, "
+                         "-2 chunked, -3 stream-K, > 0 fixed split of that many tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-append", action="store_true",
                     help="skip the KV-append comparisons (decode: fused append; prefill: the prompt step)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-extra", action="store_true",
-                    help="576-row decode only: skip the short GPU-only runs of the other workloads (other_workloads field)")
+                    help="576-row decode only: skip the short runs of the other workloads and their CPU baselines "
+                         "(other_workloads field)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates rocprof byte counters)")
     ap.add_argument("--rocprof-summary", nargs=2, metavar=("SRC", "DST"),
