@@ -360,15 +360,20 @@ int q3a_prefill_dense_append_rope(
  * The talker's prompt step with its q/k producers, in two launches (engine/talker.py:157-169): q = rope(rms(q_raw,
  * q_norm_w)) and k = rope(rms(k_raw, k_norm_w)) of every prompt token with the token's own cos/sin row (engine/ops.py:
  * 51-60 as eager bf16 ops: prefill_hidden is not compiled), the index_copy_ pair into the pool (:161-162) and
- * flash_attn_varlen_func(q, k, v, cu, cu, ...) (:169).  The first launch writes the normalised k (and, when not
- * causal, q) into the workspace; the second is q3a_prefill_append's attention on them and on v where it is
- * (cu_seqlens for both q and k), normalising and rotating the raw q itself when causal.
+ * flash_attn_varlen_func(q, k, v, cu, cu, ...) (:169).  Causal: the first launch stores the normalised k rows
+ * straight into the pool at their positions; the second is the attention with K read back from the pool, v where it
+ * is and the raw q normalised and rotated as it is loaded, and it stores the V rows into the pool.  So the attention
+ * sees a key only through a valid table entry: a key whose page id is outside [0, num_pages), or whose position is
+ * past the table, attends with zeros for K (the engine's index_copy_ would fail on such a slot).  Not causal: the first launch writes the
+ * normalised q and k into the workspace and the second is q3a_prefill_append's attention on them (cu_seqlens for
+ * both q and k).
  *
  *   q          [T, Hq, D] bf16 raw projections of the T = total_tokens packed prompt tokens (q_stride_t/h)
  *   k, v       [T, Hkv, D] bf16 raw keys and the values (their own strides)
  *   cos, sin   [T, D] bf16: token t's rows at its position in its sequence (row stride rope_stride_t)
  *   cu_seqlens [num_seqs + 1] int32;  pool, table, out: as q3a_prefill_append
- *   workspace  q3a_prefill_append_rope_workspace_bytes(T, Hq, Hkv, D) bytes, 16-byte aligned
+ *   workspace  not causal: q3a_prefill_append_rope_workspace_bytes(T, Hq, Hkv, D) bytes, 16-byte aligned;
+ *              causal: unused (may be NULL with workspace_bytes 0)
  * Requirements as q3a_prefill_dense_append_rope.
  */
 size_t q3a_prefill_append_rope_workspace_bytes(int total_tokens, int num_q_heads, int num_kv_heads, int head_dim);

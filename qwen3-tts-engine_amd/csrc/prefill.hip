@@ -156,11 +156,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
   // The sequence's first 64 page ids depend only on s: fetch them before cu_seqlens so the first tile's
   // loads wait for one memory round trip, not two.
-  const bool paged = a.bt != nullptr;
-  const int64_t bt_row = (int64_t)s * a.bt_sb;
   // Waves 0 and 1 copy K tiles, waves 2 and 3 V tiles (below); each uses its operand's own strides, which are
-  // wave-uniform and stay in scalar registers.
+  // wave-uniform and stay in scalar registers.  The norm/rope-q form reads K paged (the pool, where its producer
+  // pass stored the normalised rows) and V packed.
   const bool copies_k = wave < 2;
+  const bool paged = a.bt != nullptr && (!kRopeQ || copies_k);
+  const int64_t bt_row = (int64_t)s * a.bt_sb;
   const int64_t c_sp = copies_k ? a.k_sp : a.v_sp;
   const int64_t c_st = copies_k ? a.k_st : a.v_st;
   const int64_t c_sh = copies_k ? a.k_sh : a.v_sh;
@@ -197,7 +198,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     vrow0 = (int64_t)s * a.v_ss;
   }
   if (qt * kQT >= Lq) return;
-  if (a.bt != nullptr) Lk = min(Lk, a.max_pages * a.page_size);
+  // Keys past the table are not attended; the norm/rope-q form (K paged, V packed, the prompt's own rows stored
+  // from the last tiles) keeps them, and their K reads arrive as zeros (the window entry past the table is -1).
+  if (a.bt != nullptr && !kRopeQ) Lk = min(Lk, a.max_pages * a.page_size);
   Lk = max(Lk, 0);
 
   const int tq = qt * kQT + wave * 16 + col;  // this lane's query token
@@ -501,10 +504,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) {
             auto half = [h2](uint32_t v) { return h2 ? bf16_hi(v) : bf16_lo(v); };
-            const float yl = round_bf16(half(wl[i]) * round_bf16(half(xl[i]) * r));
-            const float yh = round_bf16(half(wh[i]) * round_bf16(half(xh[i]) * r));
-            el[h2] = round_bf16(yl * half(cl[i])) + round_bf16(-yh * half(sl[i]));
-            eh[h2] = round_bf16(yh * half(ch[i])) + round_bf16(yl * half(sh[i]));
+            const float yl = round_bf16_1op(half(wl[i]) * round_bf16_1op(half(xl[i]) * r));
+            const float yh = round_bf16_1op(half(wh[i]) * round_bf16_1op(half(xh[i]) * r));
+            el[h2] = round_bf16_1op(yl * half(cl[i])) + round_bf16_1op(-yh * half(sl[i]));
+            eh[h2] = round_bf16_1op(yh * half(ch[i])) + round_bf16_1op(yl * half(sh[i]));
           }
           ol[i] = pack_bf16x2(el[0], el[1]);
           oh[i] = pack_bf16x2(eh[0], eh[1]);
@@ -549,14 +552,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
   if (pool_from_lds) {
     // Token kown0 + tl's K (part 0) and V (part 1) rows, chunk ch, from the stage its tile was copied into (tile t
-    // sits in stage t & 1; its LDS slot c holds global chunk c ^ (row & 15)).
+    // sits in stage t & 1; its LDS slot c holds global chunk c ^ (row & 15)).  The norm/rope-q form stores the V
+    // rows only (its K rows are already in the pool).
     const int kown1 = min(Lk, kown0 + kQT);
     const int pi0 = kown0 >> a.p_shift;
+    constexpr int kParts = kRopeQ ? 1 : 2;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
+    for (int it = 0; it < 4 * kParts; ++it) {
       const int idx = tid + 256 * it;
-      const int tl = idx >> 5;
-      const int part = (idx >> 4) & 1;
+      const int tl = idx >> (3 + kParts);
+      const int part = kRopeQ ? 1 : (idx >> 4) & 1;
       const int ch = idx & 15;
       const int key = kown0 + tl;
       const int pi = key >> a.p_shift;
@@ -970,6 +975,16 @@ struct AdmitPrepArgs {
   uint16_t* vo;  // [S, n, Hkv, D]
   int R, P, Hq, Hkv;
   int64_t jq, jk, jv, jp, jall;  // job block ends: q | new K | new V | prefix K | prefix V
+  // Pool form of the new K rows (cu != nullptr; one packed sequence of R rows, P = 0): row t belongs to the sequence
+  // s with cu[s] <= t < cu[s + 1] (nseq sequences) and goes to the page pool at position t - cu[s] of s (table pbt,
+  // rows whose page is outside [0, p_pages) or past the table are not stored) instead of to ko.
+  const int32_t* cu;
+  int nseq;
+  uint16_t* kpool;
+  int64_t p_sp, p_st, p_sh;
+  const int32_t* pbt;
+  int64_t pbt_sb;
+  int p_pages, p_shift, p_max_pages;
 };
 
 __global__ __launch_bounds__(256) void admit_prep_kernel(const AdmitPrepArgs a) {
@@ -996,11 +1011,36 @@ __global__ __launch_bounds__(256) void admit_prep_kernel(const AdmitPrepArgs a) 
     const uint4 w = ld16((isq ? a.qn : a.kn) + c8);
     const uint4 c = ld16(a.cs + (int64_t)t * a.cs_st + c8);
     const uint4 sn = ld16(a.sn + (int64_t)t * a.cs_st + c8);
-    const uint4 y = qk_norm_rope16_eager(x, w, c, sn, a.eps);
+    int64_t pdst = -1;  // pool form: the row's element offset in the pool, -1 when it is not stored
+    if (!isq && a.cu != nullptr) {
+      // The sequence of row t (wave-uniform): the last s in 0..nseq with cu[s] <= t, 64 entries per ballot.  The
+      // lengths are non-decreasing, so each ballot is a prefix of the lanes.
+      int sidx = -1, start = 0;
+      for (int base = 0; base <= a.nseq; base += 64) {
+        const int i = base + lane;
+        const int ci = i <= a.nseq ? a.cu[i] : 0x7fffffff;
+        const int nle = __popcll(__ballot(ci <= t));
+        if (nle > 0) {
+          sidx = base + nle - 1;
+          start = __builtin_amdgcn_readlane(ci, nle - 1);
+        }
+        if (nle < 64) break;
+      }
+      if (sidx >= 0 && sidx < a.nseq) {
+        const int pos = t - start;
+        const int pi = pos >> a.p_shift;
+        const int page = pos >= 0 && pi < a.p_max_pages ? a.pbt[(int64_t)sidx * a.pbt_sb + pi] : -1;
+        if ((unsigned)page < (unsigned)a.p_pages)
+          pdst = (int64_t)page * a.p_sp + (int64_t)(pos & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)h * a.p_sh + c8;
+      }
+    }
+    const uint4 y = qk_norm_rope16_eager<true>(x, w, c, sn, a.eps);
     if (isq)
       st16(a.qo + ((sq * a.R + t) * a.Hq + h) * kD + c8, y);
-    else
+    else if (a.cu == nullptr)
       st16(a.ko + ((sq * n + a.P + t) * a.Hkv + h) * kD + c8, y);
+    else if (pdst >= 0)
+      st16(a.kpool + pdst, y);
   } else if (j0 < jv) {
     const uint32_t jj = j0 - jk, ht = jj / (uint32_t)a.Hkv;  // new V rows
     const int h = (int)(jj - ht * a.Hkv) + hsub;
@@ -1223,6 +1263,19 @@ static int prefill_append_impl(PrefillArgs& a, const void* q, int64_t q_stride_t
   a.hkv = num_kv_heads;
   set_pool(a, k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size, block_table,
            bt_stride_b, max_pages_per_seq, -1);
+  if (a.qn != nullptr) {
+    // The norm/rope-q form reads K from the pool, where the producer pass stored the normalised rows (V packed).
+    a.k = static_cast<const uint16_t*>(k_cache);
+    a.k_sp = kv_stride_page;
+    a.k_st = kv_stride_tok;
+    a.k_sh = kv_stride_head;
+    a.bt = block_table;
+    a.bt_sb = bt_stride_b;
+    a.max_pages = max_pages_per_seq;
+    a.num_pages = num_pages;
+    a.page_size = page_size;
+    a.page_shift = a.p_shift;
+  }
   return launch(a, num_seqs, max_seqlen_q, stream, who);
 }
 
@@ -1505,7 +1558,8 @@ extern "C" int q3a_prefill_dense_append_rope(
                             causal, stream, who);
 }
 
-// Workspace of q3a_prefill_append_rope: the normalised q [T, Hq, D] and k [T, Hkv, D] (v is read where it is).
+// Workspace of q3a_prefill_append_rope when not causal: the normalised q [T, Hq, D] and k [T, Hkv, D] (v is read
+// where it is).  The causal form uses none.
 extern "C" size_t q3a_prefill_append_rope_workspace_bytes(int total_tokens, int num_q_heads, int num_kv_heads,
                                                           int head_dim) {
   if (total_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
@@ -1528,25 +1582,33 @@ extern "C" int q3a_prefill_append_rope(
   if (head_dim != kD) return fail(Q3A_EINVAL, "%s: head_dim %d unsupported (need %d)", who, head_dim, kD);
   if (num_kv_heads < 1 || num_q_heads != kG * num_kv_heads)
     return fail(Q3A_EINVAL, "%s: num_q_heads %d must be %d * num_kv_heads %d", who, num_q_heads, kG, num_kv_heads);
-  if (!q || !k || !v || !q_norm_w || !k_norm_w || !cos || !sin || !cu_seqlens || !out || !workspace)
+  // Causal, nothing goes through the workspace (k rows straight into the pool, q normalised in the attention).
+  const bool uses_ws = causal == 0;
+  if (!q || !k || !v || !q_norm_w || !k_norm_w || !cos || !sin || !cu_seqlens || !out || (uses_ws && !workspace))
     return fail(Q3A_EINVAL, "%s: null pointer argument", who);
   const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)q_norm_w | (uintptr_t)k_norm_w |
-                          (uintptr_t)cos | (uintptr_t)sin | (uintptr_t)workspace;
+                          (uintptr_t)cos | (uintptr_t)sin | (uses_ws ? (uintptr_t)workspace : 0);
   if (align % 16 != 0) return fail(Q3A_EINVAL, "%s: tensors and the workspace must be 16-byte aligned", who);
   if ((q_stride_t | q_stride_h | k_stride_t | k_stride_h | v_stride_t | v_stride_h | rope_stride_t) % 8 != 0 ||
       q_stride_t < 0 || q_stride_h < 0 || k_stride_t < 0 || k_stride_h < 0 || v_stride_t < 0 || v_stride_h < 0 ||
       rope_stride_t < 0)
     return fail(Q3A_EINVAL, "%s: strides must be non-negative multiples of 8 elements", who);
   const size_t need = q3a_prefill_append_rope_workspace_bytes(total_tokens, num_q_heads, num_kv_heads, head_dim);
-  if (workspace_bytes < need)
+  if (uses_ws && workspace_bytes < need)
     return fail(Q3A_EINVAL, "%s: workspace of %zu bytes, need %zu", who, workspace_bytes, need);
   int rc = check_pool(k_cache, v_cache, kv_stride_page, kv_stride_tok, kv_stride_head, num_pages, page_size,
                       block_table, max_pages_per_seq, head_dim, who);
   if (rc != Q3A_OK) return rc;
+  // The attention's own checks, before the producer pass writes anything (K read back from the pool).
+  rc = check_common(q, k_cache, v, out, q_stride_t, q_stride_h, kv_stride_tok, kv_stride_head, v_stride_t, v_stride_h,
+                    o_stride_t, o_stride_h, num_q_heads, num_kv_heads, head_dim, who);
+  if (rc != Q3A_OK) return rc;
 
   // The producers over all T tokens as one sequence with no prefix: token t takes rope row t; no V rows (the
-  // attention reads v where it is).  Causal: k rows only, the attention kernel normalises and rotates q as it loads
-  // it (its pool rows then always go out from the last tiles it streams); otherwise q rows too.
+  // attention reads v where it is).  Causal: k rows only, stored straight into the pool at each token's position in
+  // its sequence (cu_seqlens), where the attention kernel reads them back as paged K; it normalises and rotates q
+  // as it loads it and stores only the V rows into the pool (from the last tiles it streams).  Otherwise q and k
+  // rows into the workspace, and the plain append form on them.
   const int64_t T = total_tokens;
   const bool q_in_kernel = causal != 0;
   AdmitPrepArgs p{};
@@ -1575,6 +1637,20 @@ extern "C" int q3a_prefill_append_rope(
   p.jv = p.jk;
   p.jp = p.jv;
   p.jall = p.jv;
+  if (q_in_kernel) {
+    p.cu = cu_seqlens;
+    p.nseq = num_seqs;
+    p.kpool = static_cast<uint16_t*>(k_cache);
+    p.p_sp = kv_stride_page;
+    p.p_st = kv_stride_tok;
+    p.p_sh = kv_stride_head;
+    p.pbt = block_table;
+    p.pbt_sb = bt_stride_b;
+    p.p_pages = num_pages;
+    p.p_shift = 0;
+    while ((1 << p.p_shift) < page_size) ++p.p_shift;
+    p.p_max_pages = max_pages_per_seq;
+  }
   rc = launch_prep(p, stream, who);
   if (rc != Q3A_OK) return rc;
   PrefillArgs a{};
@@ -1584,10 +1660,14 @@ extern "C" int q3a_prefill_append_rope(
     a.rsin = p.sn;
     a.rs_st = rope_stride_t;
     a.eps = eps;
+    return prefill_append_impl(a, q, q_stride_t, q_stride_h, cu_seqlens, k_cache, kv_stride_tok, kv_stride_head, v,
+                               v_stride_t, v_stride_h, cu_seqlens, k_cache, v_cache, kv_stride_page, kv_stride_tok,
+                               kv_stride_head, num_pages, page_size, block_table, bt_stride_b, max_pages_per_seq, out,
+                               o_stride_t, o_stride_h, num_seqs, max_seqlen, num_q_heads, num_kv_heads, head_dim,
+                               softmax_scale, causal, stream, who);
   }
-  return prefill_append_impl(a, q_in_kernel ? q : p.qo, q_in_kernel ? q_stride_t : (int64_t)num_q_heads * kD,
-                             q_in_kernel ? q_stride_h : kD, cu_seqlens, p.ko, (int64_t)num_kv_heads * kD, kD, v,
-                             v_stride_t, v_stride_h, cu_seqlens, k_cache, v_cache, kv_stride_page, kv_stride_tok,
+  return prefill_append_impl(a, p.qo, (int64_t)num_q_heads * kD, kD, cu_seqlens, p.ko, (int64_t)num_kv_heads * kD, kD,
+                             v, v_stride_t, v_stride_h, cu_seqlens, k_cache, v_cache, kv_stride_page, kv_stride_tok,
                              kv_stride_head, num_pages, page_size, block_table, bt_stride_b, max_pages_per_seq, out,
                              o_stride_t, o_stride_h, num_seqs, max_seqlen, num_q_heads, num_kv_heads, head_dim,
                              softmax_scale, causal, stream, who);

@@ -36,9 +36,20 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t 
 constexpr uint32_t kPermLoLo = 0x05040100u;
 constexpr uint32_t kPermHiHi = 0x07060302u;
 
-// Round a float to the nearest bf16 value, returned as float.
+// Round a float to the nearest bf16 value (round to nearest even), returned as float.
 __device__ __forceinline__ float round_bf16(float x) {
   return __uint_as_float(pack_bf16x2(x, 0.f) << 16);
+}
+
+// The same rounding in one instruction: v_cvt_pk_bf16_f32 with bf16(x) in the high half and bf16(+0) = 0 in the low
+// half is bf16(x)'s fp32 bit pattern.  The compiler lowers every C form of it to a conversion into the low half plus
+// a shift or permute, so it is written as assembly; the scheduler then knows nothing of its latency.  Used where
+// chains of eager roundings are issue-bound (the prompt step's q prologue and its k producer pass: 62.1 -> 59.0 us per
+// layer call); in the short-key admission kernel it measured slower (9.46 -> 9.85 us), which keeps round_bf16.
+__device__ __forceinline__ float round_bf16_1op(float x) {
+  float r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+  return r;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -210,8 +221,10 @@ __device__ __forceinline__ uint4 qk_norm_rope16(uint4 x, uint4 w, uint4 c, uint4
 // The same producers as eager bf16 torch ops evaluate them (engine/ops.py:51-60 outside torch.compile; the
 // admission layer runs this way by default, engine/arrivals.py:57-61): every op rounds to bf16,
 //   y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))),  o = bf16(bf16(y * cos) + bf16(rot(y) * sin)).
-// Layout and reduction tree as qk_norm_rope16.
+// Layout and reduction tree as qk_norm_rope16.  kOneOpRound: each rounding is round_bf16_1op (same bits).
+template <bool kOneOpRound = false>
 __device__ __forceinline__ uint4 qk_norm_rope16_eager(uint4 x, uint4 w, uint4 c, uint4 s, float eps) {
+  auto rb = [](float v) { return kOneOpRound ? round_bf16_1op(v) : round_bf16(v); };
   const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ws[4] = {w.x, w.y, w.z, w.w};
   const uint32_t cs[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
   float p[4];
@@ -230,11 +243,11 @@ __device__ __forceinline__ uint4 qk_norm_rope16_eager(uint4 x, uint4 w, uint4 c,
     for (int e = 0; e < 2; ++e) {
       const float xv = e ? bf16_hi(xs[i]) : bf16_lo(xs[i]);
       const float wv = e ? bf16_hi(ws[i]) : bf16_lo(ws[i]);
-      const float y = round_bf16(wv * round_bf16(xv * r));
+      const float y = rb(wv * rb(xv * r));
       const float yp = dpp_f32<kDppRor8>(y);
       const float cv = e ? bf16_hi(cs[i]) : bf16_lo(cs[i]);
       const float sv = e ? bf16_hi(ss[i]) : bf16_lo(ss[i]);
-      out[e] = round_bf16(y * cv) + round_bf16((lo ? -yp : yp) * sv);
+      out[e] = rb(y * cv) + rb((lo ? -yp : yp) * sv);
     }
     o[i] = pack_bf16x2(out[0], out[1]);
   }

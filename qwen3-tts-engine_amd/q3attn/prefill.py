@@ -226,7 +226,9 @@ def prefill_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_nor
     ([T, D], or [T, 1, D] as the engine gathers them) with the rounding of eager bf16 ops (engine/ops.py:51-60), k and
     v go into the pool at each token's position through block_table [n, max_pages], and the result is
     flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, ...) over the normalised q and k [T, Hq, D].  Causal, the
-    first launch normalises k and the attention kernel q; otherwise the first launch normalises both."""
+    first launch normalises k straight into the pool and the attention kernel reads K back from there and normalises
+    q itself (a key whose table entry is invalid or missing attends with zeros for K); otherwise the first launch
+    normalises both into a workspace."""
     who = "q3attn.prefill_append_rope"
     _req(q.is_cuda, f"{who}: tensors must be on a GPU (there is no CPU path)")
     dev = q.device
@@ -258,16 +260,17 @@ def prefill_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_nor
     if n <= 0 or T == 0:
         return out.zero_() if T else out
     L = lib()
-    ws_bytes = L.q3a_prefill_append_rope_workspace_bytes(T, Hq, Hkv, D)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    # causal: the k rows go straight into the pool and q is normalised in the attention, so no workspace
+    ws_bytes = 0 if causal else L.q3a_prefill_append_rope_workspace_bytes(T, Hq, Hkv, D)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev) if ws_bytes else None
     num_pages, page = k_cache.shape[0], k_cache.shape[1]
     rc = L.q3a_prefill_append_rope(
         q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
         v.stride(1), q_norm_w.data_ptr(), k_norm_w.data_ptr(), c2.data_ptr(), s2.data_ptr(), c2.stride(0), float(eps),
         cu_seqlens.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
         k_cache.stride(2), num_pages, page, block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
-        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws_bytes, n, T, int(max_seqlen), Hq, Hkv, D,
-        float(softmax_scale), 1 if causal else 0, torch.cuda.current_stream(dev).cuda_stream)
+        out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr() if ws is not None else None, ws_bytes, n, T,
+        int(max_seqlen), Hq, Hkv, D, float(softmax_scale), 1 if causal else 0, torch.cuda.current_stream(dev).cuda_stream)
     check(rc, "q3a_prefill_append_rope")
     return out
 

@@ -447,9 +447,11 @@ def _prompt_rope(**kw):
 
 
 @pytest.mark.parametrize("kw,frag", [
-    (dict(kn=None), "null pointer"), (dict(cu=None), "null pointer"), (dict(ws=None), "null pointer"),
+    (dict(kn=None), "null pointer"), (dict(cu=None), "null pointer"), (dict(ws=None, causal=0), "null pointer"),
     (dict(bt=None), "null pointer"), (dict(sin=24), "aligned"), (dict(k_st=4100), "strides"),
-    (dict(ws_bytes=4096), "workspace"), (dict(D=256), "head_dim"), (dict(Hq=8), "num_q_heads"),
+    (dict(ws_bytes=4096, causal=0), "workspace"), (dict(ws=24, causal=0), "aligned"), (dict(out=24), "aligned"),
+    (dict(o_st=2052), "strides"), (dict(v_st=64), "token strides"), (dict(D=256), "head_dim"),
+    (dict(Hq=8), "num_q_heads"),
     (dict(Hq=12, Hkv=6), "multiple of 4"), (dict(page=24), "power of two"), (dict(T=-5), "negative"),
 ])
 def test_prefill_append_rope_rejects_bad_arguments(kw, frag):

@@ -280,6 +280,47 @@ def test_prompt_step_rope_matches_torch_producers(cuda_device, causal):
     assert ok, st
 
 
+def test_prompt_step_rope_invalid_pages_attend_zero_keys(cuda_device):
+    """Causal, the attention reads K back from the pool where the producer pass stored it: a key whose table entry is
+    outside [0, num_pages) (-1, num_pages) or past the table (sequence 0 needs 10 pages of a 9-entry table) is not
+    stored and attends with zero K, while its V comes from the packed values.  (The engine's index_copy_ would raise
+    on such a slot.)  Every other row is stored and attended as usual."""
+    dev = cuda_device
+    lens = np.array([150, 40, 64])
+    q, k, v, qn, kn, cos_t, sin_t, cu = _prompt_inputs(dev, lens, seed=56)
+    n, page, Pn, num_pages = len(lens), 16, 9, 64
+    bt = _table(n, Pn, num_pages, seed=57)
+    bt[0, 3] = -1            # keys 48..63 of sequence 0
+    bt[2, 1] = num_pages     # keys 16..31 of sequence 2
+    kc = torch.full((num_pages, page, 8, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, float("nan"))
+    scale = D ** -0.5
+    print(f"[case] prefill_append_rope with invalid table entries, lens {lens.tolist()}", flush=True)
+    out = q3attn.prefill_append_rope(q, k, v, qn, kn, cos_t, sin_t, cu, int(lens.max()), kc, vc,
+                                     torch.from_numpy(bt).to(dev), scale)
+    torch.cuda.synchronize()
+    cn, sn = to_np(cos_t), to_np(sin_t)
+    q_o = _eager_norm_rope_np(to_np(q), to_np(qn), cn, sn)
+    k_o = _eager_norm_rope_np(to_np(k), to_np(kn), cn, sn)
+    rows = np.concatenate([np.arange(L) for L in lens])
+    seq = np.repeat(np.arange(n), lens)
+    pi = rows // page
+    page_id = np.where(pi < Pn, bt[seq, np.minimum(pi, Pn - 1)], -1)
+    valid = (page_id >= 0) & (page_id < num_pages)
+    assert (~valid).sum() == 16 + 6 + 16
+    k_eff = np.where(valid[:, None, None], k_o, 0.0).astype(np.float32)
+    ok, st = ora.compare(to_np(out), ora.prefill_varlen(q_o, k_eff, to_np(v), cu.cpu().numpy(), scale))
+    print(f"[parity] prefill_append_rope, invalid entries, vs oracle with zero keys {st}", flush=True)
+    assert ok, st
+    kcn, vcn = to_np(kc), to_np(vc)
+    pages, offs = page_id[valid], rows[valid] % page
+    assert np.array_equal(vcn[pages, offs], to_np(v)[valid])
+    _assert_last_bit(kcn[pages, offs], k_o[valid], "pool K rows with valid entries")
+    written = np.zeros(kc.shape[:2], dtype=bool)
+    written[pages, offs] = True
+    assert np.isnan(kcn[~written]).all() and np.isnan(vcn[~written]).all()
+
+
 def test_prompt_step_rope_in_graph_replays(cuda_device):
     dev = cuda_device
     lens = np.array([150, 33, 260, 1, 97])
