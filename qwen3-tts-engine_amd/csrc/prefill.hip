@@ -172,6 +172,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     pwin = (paged && i < a.max_pages) ? a.bt[bt_row + i] : -1;
   };
   if (paged) load_window(0);
+  // Tile 0's page id for this wave's 16-key group, a scalar load through the constant address space (the table is
+  // not written by this kernel): tile 0's copies then wait for it on the scalar counter, not for the window's vector
+  // load, which the compiler's count merges with every vector load of the prologue (q, the pool window) in flight.
+  int page0 = -1;
+  if (paged) {
+    typedef __attribute__((address_space(4))) const int32_t cint32;
+    const int pi0 = (16 * (wave & 1)) >> a.page_shift;
+    if (pi0 < a.max_pages) page0 = ((const cint32*)a.bt)[bt_row + pi0];
+  }
 
   // Element offsets of the sequence's first query/output row and first packed key row.
   int Lq, Lk;
@@ -339,9 +348,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int rr = 4 * i + (lane >> 4);
     dma_off[i] = (uint32_t)((rr * c_st + 8 * ((lane & 15) ^ rr)) * 2);
   }
-  auto issue = [&](int t, uint8_t* Kst, uint8_t* Vst) __attribute__((always_inline)) {
+  // Tile 0 (first = true) takes its page id from the scalar load above.
+  auto issue = [&](int t, uint8_t* Kst, uint8_t* Vst, bool first = false) __attribute__((always_inline)) {
     int page = 0;
-    if (paged) {
+    if (paged && first) {
+      page = page0;
+    } else if (paged) {
       const int pi = (t * kKT + 16 * cgrp) >> a.page_shift;
       if (pi < pwin_base || pi >= pwin_base + 64) load_window(pi & ~63);
       page = readlane(pwin, pi - pwin_base);
@@ -471,11 +483,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // publishes the next tile (every wave has waited for its own copies) and frees the stage just read.
   // The wait is unconditional so that no path into the loop carries outstanding loads (the q fragments): a
   // pending load on any entry path makes the compiler drain every copy before the first MFMA of each tile.
-  if (ntiles > 0) issue(0, sK0, sV0);
+  if (ntiles > 0) issue(0, sK0, sV0, true);
   wait_vmem();
   __syncthreads();
   if constexpr (kRopeQ) {
-    // The norm/rope-q form's arithmetic, on the loads the prologue issued beside tile 0's copies.
+    // The norm/rope-q form's arithmetic, on the loads the prologue issued beside tile 0's copies.  (Run while the
+    // copies are still in flight, before the wait, it measured slower: 56.7 -> 57.5 us per prompt-step call.)
 #pragma unroll
     for (int hh = 0; hh < kG; ++hh) {
       float ss = 0.f;
@@ -975,9 +988,9 @@ struct AdmitPrepArgs {
   uint16_t* vo;  // [S, n, Hkv, D]
   int R, P, Hq, Hkv;
   int64_t jq, jk, jv, jp, jall;  // job block ends: q | new K | new V | prefix K | prefix V
-  // Pool form of the new K rows (cu != nullptr; one packed sequence of R rows, P = 0): row t belongs to the sequence
-  // s with cu[s] <= t < cu[s + 1] (nseq sequences) and goes to the page pool at position t - cu[s] of s (table pbt,
-  // rows whose page is outside [0, p_pages) or past the table are not stored) instead of to ko.
+  // prompt_k_kernel (the prompt step's k rows, R packed tokens): token t belongs to the sequence s with
+  // cu[s] <= t < cu[s + 1] (nseq sequences) and its normalised rows go to the page pool at position t - cu[s] of s
+  // (table pbt; rows whose page is outside [0, p_pages) or past the table are not stored).
   const int32_t* cu;
   int nseq;
   uint16_t* kpool;
@@ -1011,36 +1024,11 @@ __global__ __launch_bounds__(256) void admit_prep_kernel(const AdmitPrepArgs a) 
     const uint4 w = ld16((isq ? a.qn : a.kn) + c8);
     const uint4 c = ld16(a.cs + (int64_t)t * a.cs_st + c8);
     const uint4 sn = ld16(a.sn + (int64_t)t * a.cs_st + c8);
-    int64_t pdst = -1;  // pool form: the row's element offset in the pool, -1 when it is not stored
-    if (!isq && a.cu != nullptr) {
-      // The sequence of row t (wave-uniform): the last s in 0..nseq with cu[s] <= t, 64 entries per ballot.  The
-      // lengths are non-decreasing, so each ballot is a prefix of the lanes.
-      int sidx = -1, start = 0;
-      for (int base = 0; base <= a.nseq; base += 64) {
-        const int i = base + lane;
-        const int ci = i <= a.nseq ? a.cu[i] : 0x7fffffff;
-        const int nle = __popcll(__ballot(ci <= t));
-        if (nle > 0) {
-          sidx = base + nle - 1;
-          start = __builtin_amdgcn_readlane(ci, nle - 1);
-        }
-        if (nle < 64) break;
-      }
-      if (sidx >= 0 && sidx < a.nseq) {
-        const int pos = t - start;
-        const int pi = pos >> a.p_shift;
-        const int page = pos >= 0 && pi < a.p_max_pages ? a.pbt[(int64_t)sidx * a.pbt_sb + pi] : -1;
-        if ((unsigned)page < (unsigned)a.p_pages)
-          pdst = (int64_t)page * a.p_sp + (int64_t)(pos & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)h * a.p_sh + c8;
-      }
-    }
     const uint4 y = qk_norm_rope16_eager<true>(x, w, c, sn, a.eps);
     if (isq)
       st16(a.qo + ((sq * a.R + t) * a.Hq + h) * kD + c8, y);
-    else if (a.cu == nullptr)
+    else
       st16(a.ko + ((sq * n + a.P + t) * a.Hkv + h) * kD + c8, y);
-    else if (pdst >= 0)
-      st16(a.kpool + pdst, y);
   } else if (j0 < jv) {
     const uint32_t jj = j0 - jk, ht = jj / (uint32_t)a.Hkv;  // new V rows
     const int h = (int)(jj - ht * a.Hkv) + hsub;
@@ -1060,6 +1048,74 @@ __global__ __launch_bounds__(256) void admit_prep_kernel(const AdmitPrepArgs a) 
       x = isk ? ld16(a.pk + src * a.pk_ss + (int64_t)r * a.pk_st + (int64_t)h * a.pk_sh + c8)
               : ld16(a.pv + src * a.pv_ss + (int64_t)r * a.pv_st + (int64_t)h * a.pv_sh + c8);
     st16((isk ? a.ko : a.vo) + ((sq * n + r) * a.Hkv + h) * kD + c8, x);
+  }
+}
+
+// The prompt step's k producer (engine/talker.py:158 as eager bf16 ops): every packed token's Hkv raw k rows
+// normalised and rotated with the token's cos/sin row, straight into the pool at the token's position in its
+// sequence.  A wave takes kGroups consecutive groups of 4 rows (4 heads of one token, 16 lanes per row in the
+// qk_norm_rope16 layout) and issues every group's loads before the first is used, so each wave keeps kGroups KiB of
+// rows in flight: with one group per wave the pass was bound by the bytes the resident waves had in flight.  The
+// token's sequence comes from one ballot over 64 cu_seqlens entries per group (the lengths are non-decreasing, so
+// each ballot is a prefix of the lanes), its page from the table.
+constexpr int kPromptKGroups = 2;
+
+__global__ __launch_bounds__(256) void prompt_k_kernel(const AdmitPrepArgs a) {
+  constexpr int kGroups = kPromptKGroups;
+  const int lane = threadIdx.x & 63;
+  const int hsub = lane >> 4;      // the lane's row of a group's 4
+  const int c8 = 8 * (lane & 15);  // this lane's 8 dims
+  const uint32_t per_tok = (uint32_t)a.Hkv >> 2;
+  const uint32_t ngroups = (uint32_t)a.R * per_tok;  // below 2^31 (checked on the host)
+  const uint32_t g0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4u + (threadIdx.x >> 6)) * (uint32_t)kGroups);
+  if (g0 >= ngroups) return;
+  int t[kGroups], h[kGroups];
+  uint4 x[kGroups], c[kGroups], sn[kGroups];
+  const uint4 w = ld16(a.kn + c8);
+#pragma unroll
+  for (int i = 0; i < kGroups; ++i) {
+    const uint32_t g = min(g0 + (uint32_t)i, ngroups - 1u);  // a wave's tail groups repeat the last one, unstored
+    t[i] = (int)(g / per_tok);
+    h[i] = (int)(g - (uint32_t)t[i] * per_tok) * 4 + hsub;
+    x[i] = ld16(a.k + (int64_t)t[i] * a.k_st + (int64_t)h[i] * a.k_sh + c8);
+    c[i] = ld16(a.cs + (int64_t)t[i] * a.cs_st + c8);
+    sn[i] = ld16(a.sn + (int64_t)t[i] * a.cs_st + c8);
+  }
+  int sidx[kGroups], start[kGroups];
+#pragma unroll
+  for (int i = 0; i < kGroups; ++i) sidx[i] = -1, start[i] = 0;
+  for (int base = 0; base <= a.nseq; base += 64) {
+    const int j = base + lane;
+    const int cj = j <= a.nseq ? a.cu[j] : 0x7fffffff;
+    bool more = false;
+#pragma unroll
+    for (int i = 0; i < kGroups; ++i) {
+      const int nle = __popcll(__ballot(cj <= t[i]));
+      if (nle > 0) {
+        sidx[i] = base + nle - 1;
+        start[i] = __builtin_amdgcn_readlane(cj, nle - 1);
+      }
+      more = more || nle == 64;
+    }
+    if (!more) break;
+  }
+  int64_t dst[kGroups];
+#pragma unroll
+  for (int i = 0; i < kGroups; ++i) {
+    dst[i] = -1;
+    const int pos = t[i] - start[i];
+    const int pi = pos >> a.p_shift;
+    if (g0 + (uint32_t)i < ngroups && sidx[i] >= 0 && sidx[i] < a.nseq && pos >= 0 && pi < a.p_max_pages) {
+      const int page = a.pbt[(int64_t)sidx[i] * a.pbt_sb + pi];
+      if ((unsigned)page < (unsigned)a.p_pages)
+        dst[i] = (int64_t)page * a.p_sp + (int64_t)(pos & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)h[i] * a.p_sh +
+                 c8;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kGroups; ++i) {
+    const uint4 y = qk_norm_rope16_eager<true>(x[i], w, c[i], sn[i], a.eps);
+    if (dst[i] >= 0) st16(a.kpool + dst[i], y);
   }
 }
 
@@ -1422,6 +1478,19 @@ static int launch_prep(const AdmitPrepArgs& p, void* stream, const char* who) {
   return Q3A_OK;
 }
 
+static int launch_prompt_k(const AdmitPrepArgs& p, void* stream, const char* who) {
+  if (p.Hkv % 4 != 0) return fail(Q3A_EINVAL, "%s: num_kv_heads %d must be a multiple of 4", who, p.Hkv);
+  const int64_t groups = (int64_t)p.R * (p.Hkv / 4);
+  if (groups >= ((int64_t)1 << 31) - 64) return fail(Q3A_EINVAL, "%s: grid too large (%lld row groups)", who, (long long)groups);
+  const int64_t waves = (groups + kPromptKGroups - 1) / kPromptKGroups;
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks == 0) return Q3A_OK;
+  hipLaunchKernelGGL(prompt_k_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: producer launch failed: %s", who, hipGetErrorString(e));
+  return Q3A_OK;
+}
+
 // Workspace of q3a_prefill_dense_append_rope: the normalised q [S, R, Hq, D] and the dense K, V [S, P + R, Hkv, D],
 // each part 256-byte aligned.
 static size_t admit_ws_part(int64_t elems) { return (size_t)((elems * 2 + 255) / 256 * 256); }
@@ -1624,19 +1693,10 @@ extern "C" int q3a_prefill_append_rope(
   p.sn = static_cast<const uint16_t*>(sin);
   p.cs_st = rope_stride_t;
   p.eps = eps;
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
-  p.qo = reinterpret_cast<uint16_t*>(ws);
-  p.ko = reinterpret_cast<uint16_t*>(ws + admit_ws_part(T * num_q_heads * kD));
-  p.vo = nullptr;
   p.R = total_tokens;
   p.P = 0;
   p.Hq = num_q_heads;
   p.Hkv = num_kv_heads;
-  p.jq = q_in_kernel ? 0 : T * num_q_heads;
-  p.jk = p.jq + T * num_kv_heads;
-  p.jv = p.jk;
-  p.jp = p.jv;
-  p.jall = p.jv;
   if (q_in_kernel) {
     p.cu = cu_seqlens;
     p.nseq = num_seqs;
@@ -1650,8 +1710,18 @@ extern "C" int q3a_prefill_append_rope(
     p.p_shift = 0;
     while ((1 << p.p_shift) < page_size) ++p.p_shift;
     p.p_max_pages = max_pages_per_seq;
+    rc = launch_prompt_k(p, stream, who);
+  } else {
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    p.qo = reinterpret_cast<uint16_t*>(ws);
+    p.ko = reinterpret_cast<uint16_t*>(ws + admit_ws_part(T * num_q_heads * kD));
+    p.jq = T * num_q_heads;
+    p.jk = p.jq + T * num_kv_heads;
+    p.jv = p.jk;
+    p.jp = p.jv;
+    p.jall = p.jv;
+    rc = launch_prep(p, stream, who);
   }
-  rc = launch_prep(p, stream, who);
   if (rc != Q3A_OK) return rc;
   PrefillArgs a{};
   if (q_in_kernel) {
