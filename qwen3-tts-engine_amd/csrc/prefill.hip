@@ -1062,6 +1062,7 @@ constexpr int kPromptKGroups = 2;
 
 __global__ __launch_bounds__(256) void prompt_k_kernel(const AdmitPrepArgs a) {
   constexpr int kGroups = kPromptKGroups;
+  typedef __attribute__((address_space(4))) const int32_t cint32;
   const int lane = threadIdx.x & 63;
   const int hsub = lane >> 4;      // the lane's row of a group's 4
   const int c8 = 8 * (lane & 15);  // this lane's 8 dims
@@ -1069,6 +1070,10 @@ __global__ __launch_bounds__(256) void prompt_k_kernel(const AdmitPrepArgs a) {
   const uint32_t ngroups = (uint32_t)a.R * per_tok;  // below 2^31 (checked on the host)
   const uint32_t g0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4u + (threadIdx.x >> 6)) * (uint32_t)kGroups);
   if (g0 >= ngroups) return;
+  // The sequence boundaries first (up to 63 sequences in one load; more take the loop below), then the rows: the
+  // first wait covers the boundaries alone, and the page ids (scalar loads) are in flight with the rows.
+  const bool one_load = a.nseq < 64;
+  const int cfirst = one_load ? (lane <= a.nseq ? a.cu[lane] : 0x7fffffff) : 0;
   int t[kGroups], h[kGroups];
   uint4 x[kGroups], c[kGroups], sn[kGroups];
   const uint4 w = ld16(a.kn + c8);
@@ -1081,23 +1086,36 @@ __global__ __launch_bounds__(256) void prompt_k_kernel(const AdmitPrepArgs a) {
     c[i] = ld16(a.cs + (int64_t)t[i] * a.cs_st + c8);
     sn[i] = ld16(a.sn + (int64_t)t[i] * a.cs_st + c8);
   }
+  // The sequence of each group's token (wave-uniform): the last s in 0..nseq with cu[s] <= t.  The lengths are
+  // non-decreasing, so each ballot is a prefix of the lanes.
   int sidx[kGroups], start[kGroups];
 #pragma unroll
   for (int i = 0; i < kGroups; ++i) sidx[i] = -1, start[i] = 0;
-  for (int base = 0; base <= a.nseq; base += 64) {
-    const int j = base + lane;
-    const int cj = j <= a.nseq ? a.cu[j] : 0x7fffffff;
-    bool more = false;
+  if (one_load) {
 #pragma unroll
     for (int i = 0; i < kGroups; ++i) {
-      const int nle = __popcll(__ballot(cj <= t[i]));
+      const int nle = __popcll(__ballot(cfirst <= t[i]));
       if (nle > 0) {
-        sidx[i] = base + nle - 1;
-        start[i] = __builtin_amdgcn_readlane(cj, nle - 1);
+        sidx[i] = nle - 1;
+        start[i] = __builtin_amdgcn_readlane(cfirst, nle - 1);
       }
-      more = more || nle == 64;
     }
-    if (!more) break;
+  } else {
+    for (int base = 0; base <= a.nseq; base += 64) {
+      const int j = base + lane;
+      const int cj = j <= a.nseq ? a.cu[j] : 0x7fffffff;
+      bool more = false;
+#pragma unroll
+      for (int i = 0; i < kGroups; ++i) {
+        const int nle = __popcll(__ballot(cj <= t[i]));
+        if (nle > 0) {
+          sidx[i] = base + nle - 1;
+          start[i] = __builtin_amdgcn_readlane(cj, nle - 1);
+        }
+        more = more || nle == 64;
+      }
+      if (!more) break;
+    }
   }
   int64_t dst[kGroups];
 #pragma unroll
@@ -1106,7 +1124,7 @@ __global__ __launch_bounds__(256) void prompt_k_kernel(const AdmitPrepArgs a) {
     const int pos = t[i] - start[i];
     const int pi = pos >> a.p_shift;
     if (g0 + (uint32_t)i < ngroups && sidx[i] >= 0 && sidx[i] < a.nseq && pos >= 0 && pi < a.p_max_pages) {
-      const int page = a.pbt[(int64_t)sidx[i] * a.pbt_sb + pi];
+      const int page = ((const cint32*)a.pbt)[(int64_t)sidx[i] * a.pbt_sb + pi];  // the table is read-only here
       if ((unsigned)page < (unsigned)a.p_pages)
         dst[i] = (int64_t)page * a.p_sp + (int64_t)(pos & ((1 << a.p_shift) - 1)) * a.p_st + (int64_t)h[i] * a.p_sh +
                  c8;
