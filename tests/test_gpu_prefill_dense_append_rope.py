@@ -218,10 +218,19 @@ def _prompt_inputs(dev, lens, seed):
     return q, k, v, qn, kn, cos_t, sin_t, cu
 
 
-@pytest.mark.parametrize("lens", [[1, 7, 16, 33, 150, 400], "prefill32", [300, 5]])
+@pytest.mark.parametrize("lens", [[1, 7, 16, 33, 150, 400], "prefill32", [300, 5], "70seqs"])
 def test_prompt_step_rope_matches_oracle(cuda_device, lens):
+    """"70seqs": more sequences than one 64-lane load of cu_seqlens holds (the producer's search loops over them),
+    with empty sequences among them."""
     dev = cuda_device
-    lens = W.prefill_lengths("prefill32") if lens == "prefill32" else np.array(lens)
+    if lens == "prefill32":
+        lens = W.prefill_lengths("prefill32")
+    elif lens == "70seqs":
+        lens = np.random.default_rng(7).integers(0, 40, size=70)
+        lens[[3, 64, 65]] = 0
+        lens[-1] = 97
+    else:
+        lens = np.array(lens)
     q, k, v, qn, kn, cos_t, sin_t, cu = _prompt_inputs(dev, lens, seed=50 + len(lens))
     n, page = len(lens), 16
     Pn = int(-(-lens.max() // page))
