@@ -516,13 +516,20 @@ constexpr int kLast = 2;      // tile closes a segment
 constexpr int kRowStart = 4;  // tile is tile 0 of its row
 constexpr int kRowEnd = 8;    // tile is the last tile of its row
 
-template <bool kAppend, bool kRope = false>
+// kHalves == 2 (8 KV heads): each workgroup runs two waves per KV head, the first taking the first half of the
+// workgroup's tile range and the second the other half, so a CU holds one workgroup of 16 waves instead of two of 8.
+// The row that straddles the midpoint is merged in LDS (the two waves' states) instead of through two partial
+// records in memory, which halves the records: each costs ~1.6 us per MB written inside the call's read stream.
+// Every record keeps its meaning for the combine (slot 0: the segment opened at the range start, slot 1: the one
+// closed at the range end), and a row held whole by the workgroup is written directly.
+template <bool kAppend, bool kRope = false, int kHalves = 1>
 __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs a) {
   static_assert(kAppend || !kRope, "the norm/rope form is an append form");
+  static_assert(kHalves == 1 || kHalves == 2, "one or two waves per KV head");
   // The norm/rope form's larger stages are sized for 8 KV heads (the host rejects more), so two workgroups still
-  // share a CU's LDS.
+  // share a CU's LDS; with two halves, one workgroup of 16 waves per CU.
   constexpr int kSt = kRope ? kStageBytesRope : kStageBytes;
-  constexpr int kW = kRope ? 8 : kMaxWaves;
+  constexpr int kW = (kRope && kHalves == 1) ? 8 : kMaxWaves;
   __shared__ int s_ctx[kSkMaxRows];
   __shared__ int s_prefix[kSkMaxRows + 1];
   __shared__ int s_wsum[16];
@@ -535,9 +542,14 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   // start), written to the workspace only after the tile loop: in a 576-row, 296k-token call these writes cost
   // 4.5 us inside the read stream and ~1.5 us less at the end of the range.
   __shared__ __align__(16) float s_first[kW][kPartFloats];
+  // Two halves: the straddling row's state of each half (o unnormalised in fp32, then m, l), per KV head.
+  constexpr int kMidFloats = kG * kD + 2 * kG;
+  __shared__ __align__(16) float s_mid[kHalves == 2 ? 2 : 1][kHalves == 2 ? 8 : 1][kMidFloats];
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
-  const int g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform KV head
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index
+  const int half = kHalves == 2 ? (wv >= a.hkv ? 1 : 0) : 0;
+  const int g = wv - half * a.hkv;                           // wave-uniform KV head
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int dl = (lane & 15) * 8;
@@ -565,10 +577,10 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     const int y = __shfl_up(x, o);
     if (lane >= o) x += y;
   }
-  if (lane == 63) s_wsum[g] = x;
+  if (lane == 63) s_wsum[wv] = x;
   __syncthreads();
   int wbase = 0;
-  for (int w = 0; w < g; ++w) wbase += s_wsum[w];
+  for (int w = 0; w < wv; ++w) wbase += s_wsum[w];
   int run = wbase + x - sum;
   for (int r = r0; r < r1; ++r) {
     s_prefix[r] = run;
@@ -582,18 +594,40 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   }
   const int ge = sk_effective_grid(a.grid, NT);
   if ((int)blockIdx.x >= ge) return;
-  const int lo = (int)sk_lo(blockIdx.x, NT, ge);
-  const int hi = (int)sk_lo(blockIdx.x + 1, NT, ge);
+  // The workgroup's tile range [lo_w, hi_w) and, with two halves, its midpoint; the row that runs across the
+  // midpoint (tiles mid - 1 and mid in the same row), if any.  Only two values stay live through the tile loop (the
+  // kernel is at its register limit): slot0_tile, the tile whose segment is the range's first (record slot 0), and
+  // mid_cut_tile, the midpoint when a row runs across it, else -1.
+  auto range_of = [&](int& lo_w, int& hi_w, int& mid, int& mid_row) __attribute__((always_inline)) {
+    lo_w = (int)sk_lo(blockIdx.x, NT, ge);
+    hi_w = (int)sk_lo(blockIdx.x + 1, NT, ge);
+    mid = kHalves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
+    mid_row = -1;
+    if (kHalves == 2 && lo_w < mid && mid < hi_w) {
+      int lo_r = 0, hi_r = B;  // largest row with prefix[row] <= mid
+      while (hi_r - lo_r > 1) {
+        const int mr = (lo_r + hi_r) >> 1;
+        if (s_prefix[mr] <= mid) lo_r = mr; else hi_r = mr;
+      }
+      mid_row = __builtin_amdgcn_readfirstlane(s_prefix[lo_r] < mid ? lo_r : -1);  // uniform: a scalar
+    }
+  };
+  int lo_w, hi_w, mid, mid_row;
+  range_of(lo_w, hi_w, mid, mid_row);
+  const int lo = half == 0 ? lo_w : mid;                 // this wave's half
+  const int hi = half == 0 ? mid : hi_w;
+  const int slot0_tile = (half == 0 || mid == lo_w) ? lo : -1;
+  const int mid_cut_tile = mid_row >= 0 ? mid : -1;
 
   const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
   float* part = a.ws + (int64_t)blockIdx.x * kSkSlots * a.hkv * kPartFloats;
 
-  uint8_t* const st0 = s_stage0 + g * kSt;
-  uint8_t* const st1 = s_stage1 + g * kSt;
+  uint8_t* const st0 = s_stage0 + wv * kSt;
+  uint8_t* const st1 = s_stage1 + wv * kSt;
   uint4 q[kG];
   float m[kG], l[kG], acc[kG][8];
   reset_state(m, l, acc);
-  int seg_row = 0, seg_flags = 0, seg_slot = 0;
+  int seg_row = 0, seg_flags = 0, seg_slot = 0;  // seg_slot 2: the second half's part of the straddling row
   bool first_deferred = false;
   q[0] = q[1] = make_uint4(0u, 0u, 0u, 0u);
 
@@ -630,7 +664,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       if (fl & kFirst) {
         seg_row = readlane(vrow, j);
         seg_flags = fl;
-        seg_slot = (cb + j == lo) ? 0 : 1;
+        seg_slot = cb + j == slot0_tile ? 0 : (cb + j == mid_cut_tile ? 2 : 1);
         reset_state(m, l, acc);
       }
     };
@@ -660,9 +694,23 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         merge_lanes(32, m, l, acc);
         if ((seg_flags & kRowStart) && (fl & kRowEnd)) {
           write_output(a, seg_row, g, grp, dl, l, acc);
+        } else if (kHalves == 2 && mid_cut_tile >= 0 && (half == 0 ? cb + j == mid_cut_tile - 1 : seg_slot == 2)) {
+          // The straddling row's part in this half: its state goes to LDS, merged after the loop.
+          float* r = s_mid[kHalves == 2 ? half : 0][kHalves == 2 ? g : 0];
+          if (grp == 0) {
+#pragma unroll
+            for (int h = 0; h < kG; ++h) {
+              st16(r + h * kD + dl, make_uint4(__float_as_uint(acc[h][0]), __float_as_uint(acc[h][1]),
+                                               __float_as_uint(acc[h][2]), __float_as_uint(acc[h][3])));
+              st16(r + h * kD + dl + 4, make_uint4(__float_as_uint(acc[h][4]), __float_as_uint(acc[h][5]),
+                                                   __float_as_uint(acc[h][6]), __float_as_uint(acc[h][7])));
+            }
+          }
+          if (lane == 0)
+            st16(r + kG * kD, __builtin_bit_cast(uint4, make_float4(m[0], m[1], l[0], l[1])));
         } else {
           if (seg_slot == 0) {
-            write_partial(&s_first[g][0], lane, grp, dl, m, l, acc);
+            write_partial(&s_first[wv][0], lane, grp, dl, m, l, acc);
             first_deferred = true;
           } else {
             write_partial(part + (a.hkv + g) * kPartFloats, lane, grp, dl, m, l, acc);
@@ -737,10 +785,45 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       prep(j + 2, st0);
     }
   }
-  if (first_deferred && lane < kPartFloats / 4) st16(part + g * kPartFloats + lane * 4, ld16(&s_first[g][lane * 4]));
+  if (first_deferred && lane < kPartFloats / 4) st16(part + g * kPartFloats + lane * 4, ld16(&s_first[wv][lane * 4]));
   // The last issue() targets tiles past the list; let its (out-of-bounds) copies into LDS land before the
   // wave ends.
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  if constexpr (kHalves == 2) {
+    // The straddling row: the first half's wave of each KV head merges both halves' states (the same arithmetic as
+    // merge_lanes) and writes the row, or, when the row runs past the workgroup's range, its record.
+    __syncthreads();
+    range_of(lo_w, hi_w, mid, mid_row);
+    if (mid_row >= 0 && half == 0) {
+      const float* r0 = s_mid[0][kHalves == 2 ? g : 0];
+      const float* r1 = s_mid[kHalves == 2 ? 1 : 0][kHalves == 2 ? g : 0];
+      const float4 ml0 = __builtin_bit_cast(float4, ld16(r0 + kG * kD));
+      const float4 ml1 = __builtin_bit_cast(float4, ld16(r1 + kG * kD));
+      const float m0[kG] = {ml0.x, ml0.y}, l0[kG] = {ml0.z, ml0.w};
+      const float m1[kG] = {ml1.x, ml1.y}, l1[kG] = {ml1.z, ml1.w};
+#pragma unroll
+      for (int h = 0; h < kG; ++h) {
+        const float mn = fmaxf(m0[h], m1[h]);
+        const float w0 = fast_exp2(m0[h] - mn);
+        const float w1 = fast_exp2(m1[h] - mn);
+        l[h] = l0[h] * w0 + l1[h] * w1;
+        m[h] = mn;
+        const uint4 a0 = ld16(r0 + h * kD + dl), a1 = ld16(r0 + h * kD + dl + 4);
+        const uint4 b0 = ld16(r1 + h * kD + dl), b1 = ld16(r1 + h * kD + dl + 4);
+        const uint32_t av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const uint32_t bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[h][d] = __uint_as_float(av[d]) * w0 + __uint_as_float(bv[d]) * w1;
+      }
+      // Slot 0 is the segment opened at the range's first tile (the row starts there or before), as the combine
+      // expects; slot 1 one that runs past the range's end and started after its first tile.
+      const bool from_lo = s_prefix[mid_row] <= lo_w;
+      if (s_prefix[mid_row] >= lo_w && s_prefix[mid_row + 1] <= hi_w)
+        write_output(a, mid_row, g, grp, dl, l, acc);
+      else
+        write_partial(part + ((from_lo ? 0 : 1) * a.hkv + g) * kPartFloats, lane, grp, dl, m, l, acc);
+    }
+  }
 }
 
 // One workgroup per row: merges the partial records of rows that straddle workgroup ranges, and
@@ -1145,6 +1228,10 @@ int default_split(int batch, int hkv, int max_pages, int page_size) {
 // The workspace is sized for the larger of the two forms, so one buffer serves both.  Entries are atomics: two
 // host threads may fill the same entry at once (both store the same value).
 // form: 0 plain, 1 append, 2 append with the q/k norm and rope.
+// Waves per KV head in a stream-K workgroup: two halves of the range for 8 KV heads (16 waves), else one.  The
+// norm/rope form keeps one: at 16 waves a wave has 128 registers, which its q/k transform would exceed (spills).
+int sk_halves(int hkv, int form) { (void)form; return hkv == 8 ? 2 : 1; }
+
 int sk_grid_of(int hkv, int form) {
   static std::atomic<int> cache[64][17][3];
   int dev = 0;
@@ -1154,10 +1241,16 @@ int sk_grid_of(int hkv, int form) {
   if (cached > 0) return cached;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return kSkMaxGrid;
-  const hipError_t e =
-      form == 2   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true, true>, 64 * hkv, 0)
-      : form == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true>, 64 * hkv, 0)
-                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<false>, 64 * hkv, 0);
+  const int threads = 64 * hkv * sk_halves(hkv, form);
+  hipError_t e;
+  if (sk_halves(hkv, form) == 2)
+    e = form == 2   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true, true, 2>, threads, 0)
+        : form == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true, false, 2>, threads, 0)
+                    : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<false, false, 2>, threads, 0);
+  else
+    e = form == 2   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true, true>, threads, 0)
+        : form == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true>, threads, 0)
+                    : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<false>, threads, 0);
   if (e != hipSuccess) return kSkMaxGrid;
   int g = cus * (per_cu > 0 ? per_cu : 1);
   g = g < 1 ? 1 : (g > kSkMaxGrid ? kSkMaxGrid : g);
@@ -1414,12 +1507,22 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     a.grid = sk_effective_grid_host(a.grid, nt_bound);
     a.prefix = static_cast<int*>(workspace);
     a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256((size_t)(batch + 1) * sizeof(int)));
-    if (rope)
-      hipLaunchKernelGGL((paged_decode_sk_kernel<true, true>), dim3(a.grid), block, 0, st, a);
-    else if (append)
-      hipLaunchKernelGGL(paged_decode_sk_kernel<true>, dim3(a.grid), block, 0, st, a);
-    else
-      hipLaunchKernelGGL(paged_decode_sk_kernel<false>, dim3(a.grid), block, 0, st, a);
+    if (sk_halves(num_kv_heads, rope ? 2 : (append ? 1 : 0)) == 2) {
+      const dim3 block2(2 * 64 * num_kv_heads);
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_sk_kernel<true, true, 2>), dim3(a.grid), block2, 0, st, a);
+      else if (append)
+        hipLaunchKernelGGL((paged_decode_sk_kernel<true, false, 2>), dim3(a.grid), block2, 0, st, a);
+      else
+        hipLaunchKernelGGL((paged_decode_sk_kernel<false, false, 2>), dim3(a.grid), block2, 0, st, a);
+    } else {
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_sk_kernel<true, true>), dim3(a.grid), block, 0, st, a);
+      else if (append)
+        hipLaunchKernelGGL(paged_decode_sk_kernel<true>, dim3(a.grid), block, 0, st, a);
+      else
+        hipLaunchKernelGGL(paged_decode_sk_kernel<false>, dim3(a.grid), block, 0, st, a);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: stream-K launch failed: %s", who, hipGetErrorString(e));
     if (rope)
