@@ -142,17 +142,14 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
       kr[2] = kn0;
       kr[3] = kn1;
     }
-#pragma unroll
-    for (int s = 0; s < kNV; ++s)
-      if (s == last) vr[s] = vn;
     const __amdgpu_buffer_rsrc_t wk = make_rsrc(kb + (int64_t)last * a.k_ss, kD * 2);
-    const __amdgpu_buffer_rsrc_t wv = make_rsrc(vb + (int64_t)last * a.v_ss, kD * 2);
     // Non-temporal slot and output stores (the lines stream out instead of staying dirty in the L2): 6.83 -> 6.79 us
     // per call in the 512-row frame.
     __builtin_amdgcn_raw_buffer_store_b128(
         __builtin_bit_cast(u32x4, knc), wk,
         (int)((unsigned)(lane - kKL) < 16u ? (uint32_t)(lane - kKL) * 16 : kOutOfRange), 0, kCacheNT);
-    __builtin_amdgcn_raw_buffer_store_b32(vn, wv, lane * 4, 0, kCacheNT);
+    // The new v row (the youngest load) is swapped in and stored after the scores (below), so the scores wait for
+    // the K loads only, not for every V load.
   }
 
   auto dot16 = [](const uint4& q0, const uint4& k0, const uint4& q1, const uint4& k1) {
@@ -191,6 +188,12 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpAr
     pb[h] = round_bf16(eb * r);
   }
 
+  if constexpr (kAppend) {
+#pragma unroll
+    for (int s = 0; s < kNV; ++s)
+      if (s == last) vr[s] = vn;
+    __builtin_amdgcn_raw_buffer_store_b32(vn, make_rsrc(vb + (int64_t)last * a.v_ss, kD * 2), lane * 4, 0, kCacheNT);
+  }
   float o[kG][2];
 #pragma unroll
   for (int h = 0; h < kG; ++h) o[h][0] = o[h][1] = 0.f;
