@@ -1228,9 +1228,10 @@ int default_split(int batch, int hkv, int max_pages, int page_size) {
 // The workspace is sized for the larger of the two forms, so one buffer serves both.  Entries are atomics: two
 // host threads may fill the same entry at once (both store the same value).
 // form: 0 plain, 1 append, 2 append with the q/k norm and rope.
-// Waves per KV head in a stream-K workgroup: two halves of the range for 8 KV heads (16 waves), else one.  The
-// norm/rope form keeps one: at 16 waves a wave has 128 registers, which its q/k transform would exceed (spills).
-int sk_halves(int hkv, int form) { (void)form; return hkv == 8 ? 2 : 1; }
+// Waves per KV head in a stream-K workgroup: two halves of the range for 8 KV heads (16 waves), else one.  Every form
+// takes the same decomposition, so the append form stays bitwise equal to a scatter followed by the plain form, and
+// the norm/rope form to the append form on normalised q/k.
+int sk_halves(int hkv) { return hkv == 8 ? 2 : 1; }
 
 int sk_grid_of(int hkv, int form) {
   static std::atomic<int> cache[64][17][3];
@@ -1241,9 +1242,9 @@ int sk_grid_of(int hkv, int form) {
   if (cached > 0) return cached;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return kSkMaxGrid;
-  const int threads = 64 * hkv * sk_halves(hkv, form);
+  const int threads = 64 * hkv * sk_halves(hkv);
   hipError_t e;
-  if (sk_halves(hkv, form) == 2)
+  if (sk_halves(hkv) == 2)
     e = form == 2   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true, true, 2>, threads, 0)
         : form == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<true, false, 2>, threads, 0)
                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_sk_kernel<false, false, 2>, threads, 0);
@@ -1507,7 +1508,7 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     a.grid = sk_effective_grid_host(a.grid, nt_bound);
     a.prefix = static_cast<int*>(workspace);
     a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256((size_t)(batch + 1) * sizeof(int)));
-    if (sk_halves(num_kv_heads, rope ? 2 : (append ? 1 : 0)) == 2) {
+    if (sk_halves(num_kv_heads) == 2) {
       const dim3 block2(2 * 64 * num_kv_heads);
       if (rope)
         hipLaunchKernelGGL((paged_decode_sk_kernel<true, true, 2>), dim3(a.grid), block2, 0, st, a);
