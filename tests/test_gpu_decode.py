@@ -296,6 +296,20 @@ def _stream_k_cut_rows(wl):
     return cut, grid, G
 
 
+@pytest.mark.parametrize("rows,tiles", [(256, [48]), (128, [96]), (170, [72]), (200, [1, 95]), (96, [129, 7, 0])])
+def test_stream_k_rows_aligned_with_ranges_and_midpoints(cuda_device, rows, tiles):
+    """Rows whose tiles line up with the stream-K workgroup ranges and their midpoints (8 KV heads: two waves per
+    head, each taking half of its workgroup's range; the row across the midpoint is merged in LDS): rows that are
+    exactly one range (merged at the midpoint, then written whole), rows that start exactly at a range's first tile
+    and run past its end (their merged piece is record slot 0), rows spanning several ranges, and ragged mixes with
+    empty rows.  Against the oracle, through the stream-K path code."""
+    ctx = np.resize(np.array(tiles) * 16, rows)
+    wl = W.make_decode("aligned", cuda_device, ctx=ctx, num_pages=rows * 129 + 64, max_ctx=SK_CTX, seed=rows)
+    cut, grid, G = _stream_k_cut_rows(wl)
+    print(f"[case] {rows} rows of {tiles} tiles: grid {grid}, {G} ranges, {int(cut.sum())} rows cut", flush=True)
+    assert_parity(run(wl, split=SK), decode_oracle(wl), f"stream-K, {rows} rows of {tiles} tiles")
+
+
 def test_stream_k_cut_rows_keep_the_fp32_accuracy(cuda_device):
     """The 576-row workload: rows cut by a stream-K range boundary are merged from partial records whose o is stored
     in 16 bits (fp16, 11 significant bits, while the record's largest |o| is in [2^-6, 2^15]; bf16 beyond).  Against
