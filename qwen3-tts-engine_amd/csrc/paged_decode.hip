@@ -545,6 +545,14 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   // Two halves: the straddling row's state of each half (o unnormalised in fp32, then m, l), per KV head.
   constexpr int kMidFloats = kG * kD + 2 * kG;
   __shared__ __align__(16) float s_mid[kHalves == 2 ? 2 : 1][kHalves == 2 ? 8 : 1][kMidFloats];
+  // Two halves: the outputs of the first kOutRing rows a wave holds whole, staged here and stored after the tile
+  // loop, outside the read stream (further rows are stored at once).  Not in the norm/rope form, which has no
+  // register left for the count.
+  constexpr bool kStageOut = kHalves == 2 && !kRope;
+  constexpr int kOutRing = kStageOut ? 4 : 1;
+  __shared__ __align__(16) uint32_t s_out[kStageOut ? kW : 1][kOutRing][kG * kD / 2];
+  __shared__ int s_out_row[kStageOut ? kW : 1][kOutRing];
+  int n_out = 0;
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index
@@ -693,7 +701,22 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         merge_lanes(16, m, l, acc);
         merge_lanes(32, m, l, acc);
         if ((seg_flags & kRowStart) && (fl & kRowEnd)) {
-          write_output(a, seg_row, g, grp, dl, l, acc);
+          if (kStageOut && n_out < kOutRing) {
+            if (grp == 0) {
+              uint32_t* o = s_out[kStageOut ? wv : 0][kStageOut ? n_out : 0];
+#pragma unroll
+              for (int h = 0; h < kG; ++h) {
+                const float s = l[h] > 0.f ? 1.f / l[h] : 0.f;
+                const float* x = acc[h];
+                st16(o + h * kD / 2 + dl / 2, make_uint4(pack_bf16x2(x[0] * s, x[1] * s), pack_bf16x2(x[2] * s, x[3] * s),
+                                                         pack_bf16x2(x[4] * s, x[5] * s), pack_bf16x2(x[6] * s, x[7] * s)));
+              }
+              s_out_row[kStageOut ? wv : 0][kStageOut ? n_out : 0] = seg_row;
+            }
+            ++n_out;
+          } else {
+            write_output(a, seg_row, g, grp, dl, l, acc);
+          }
         } else if (kHalves == 2 && mid_cut_tile >= 0 && (half == 0 ? cb + j == mid_cut_tile - 1 : seg_slot == 2)) {
           // The straddling row's part in this half: its state goes to LDS, merged after the loop.
           float* r = s_mid[kHalves == 2 ? half : 0][kHalves == 2 ? g : 0];
@@ -786,6 +809,16 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     }
   }
   if (first_deferred && lane < kPartFloats / 4) st16(part + g * kPartFloats + lane * 4, ld16(&s_first[wv][lane * 4]));
+  if constexpr (kStageOut) {
+    if (grp == 0) {
+      for (int i = 0; i < n_out; ++i) {
+        const int row = s_out_row[wv][i];
+#pragma unroll
+        for (int h = 0; h < kG; ++h)
+          *reinterpret_cast<uint4*>(a.out + row * a.o_sb + (kG * g + h) * a.o_sh + dl) = ld16(&s_out[wv][i][h * kD / 2 + dl / 2]);
+      }
+    }
+  }
   // The last issue() targets tiles past the list; let its (out-of-bounds) copies into LDS land before the
   // wave ends.
   __builtin_amdgcn_s_waitcnt(0x0F70);
