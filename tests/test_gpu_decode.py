@@ -204,7 +204,8 @@ def test_row_parallel_small_batches(cuda_device, max_ctx, ctx):
 
 def test_stream_k_many_short_rows(cuda_device):
     """Thousands of short rows: many segments per workgroup, rows split at every range boundary (the table is
-    wider than the 128-token capacity below which rows are never split)."""
+    wider than the 128-token capacity below which rows are never split), and more whole rows per wave than the
+    four whose outputs are staged in LDS until after the tile loop (the rest are stored at once)."""
     rng = np.random.default_rng(17)
     ctx = rng.integers(0, 41, size=4000)
     wl = W.make_decode("short_rows", cuda_device, ctx=ctx, num_pages=40960, max_ctx=144, seed=17)
