@@ -95,11 +95,13 @@ def test_flash_attn_kvcache_k_v_form_strided_v(cuda_device, max_ctx):
     assert torch.equal(wl.k_cache, ref_k) and torch.equal(wl.v_cache, ref_v)
 
 
-def test_append_many_short_rows_stream_k(cuda_device):
-    """2,000 rows of 1..40 tokens: many rows end inside each stream-K range."""
+@pytest.mark.parametrize("rows", [2000, 4000])
+def test_append_many_short_rows_stream_k(cuda_device, rows):
+    """Thousands of rows of 1..40 tokens: many rows end inside each stream-K range; at 4,000 rows a wave holds more
+    whole rows than the four whose outputs wait in LDS until after its tile loop."""
     rng = np.random.default_rng(23)
-    ctx = rng.integers(1, 41, size=2000)
-    wl = W.make_decode("short", cuda_device, ctx=ctx, num_pages=20480, max_ctx=144, seed=23)
+    ctx = rng.integers(1, 41, size=rows)
+    wl = W.make_decode("short", cuda_device, ctx=ctx, num_pages=rows * 10 + 480, max_ctx=144, seed=23)
     k, v, old, ref_k, ref_v = _split_step(wl)
     ref = _reference(wl, ref_k, ref_v)
     L = wl.layers[0]
