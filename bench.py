@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import subprocess
@@ -275,6 +276,57 @@ def decode_kernel_name(wl, split):
 SMALL_SHAPES = ((1, 64), (1, 256), (1, 1024), (1, 1800), (2, 1800), (4, 1024), (4, 1800), (8, 512), (8, 1800),
                 (16, 1024), (16, 1800), (32, 512), (32, 1024), (32, 1800), (64, 256), (64, 512), (64, 1024))
 SMALL_PATHS = (("row_parallel", -1), ("chunks", -2), ("stream_k", -3), ("auto", 0))
+
+
+def bench_decode_scaling(args, dev):
+    """The 576-row workload with every row's context scaled by 1/2, 1 and 2 (the same rows, each scale its own
+    131,072-page pool and tables of the scaled capacity, all three built first; 28 layer calls per graph replay, each
+    timing after a second of warm replays), timed in the order 1, 1/2, 2, 2, 1/2, 1 so that a drift of the GPU's
+    clocks over the run falls on every scale alike.  The least-squares line through (bytes per call, mean us per call)
+    gives the decode's marginal read rate (its slope) and its fixed cost per call (its intercept), the figures to set
+    beside the access pattern's own ceiling (`--workload probe`)."""
+    import numpy as np
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    base = W.draw_contexts("decode576", args.seed)
+    scales = (0.5, 1.0, 2.0)
+    wls = {}
+    for scale in scales:
+        ctx = np.rint(base * scale).astype(np.int64)
+        wls[scale] = W.make_decode("decode576", dev, layers=LAYERS, seed=args.seed, ctx=ctx,
+                                   max_ctx=int(math.ceil(W.MAX_CTX["decode576"] * scale)))
+    times = {scale: [] for scale in scales}
+    for scale in (1.0, 0.5, 2.0, 2.0, 0.5, 1.0):
+        wl = wls[scale]
+        _, frame_ms, _ = time_graph(dev, lambda: [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens,
+                                                                       L.block_table, wl.scale, args.split)
+                                                  for L in wl.layers], args.steps, args.warmup, 1.0)
+        us = statistics.mean(frame_ms) * 1e3 / LAYERS
+        times[scale].append(us)
+        log(f"[bench] contexts x{scale}: {us:.1f} us/call")
+    pts = []
+    for scale in scales:
+        wl = wls[scale]
+        nbytes = wl.algorithmic_bytes()
+        us = statistics.mean(times[scale])
+        pts.append({"ctx_scale": scale, "sum_ctx": int(wl.ctx.sum()), "bytes_per_call": nbytes,
+                    "us_per_layer_call": [round(t, 2) for t in times[scale]], "gbps": round(nbytes / us / 1e3, 1)})
+        log(f"[bench] contexts x{scale}: sum_ctx {int(wl.ctx.sum())}, {nbytes / 1e6:.1f} MB per call, "
+            f"{us:.1f} us/call (mean of {len(times[scale])}), {nbytes / us / 1e3:.0f} GB/s")
+    del wls
+    torch.cuda.empty_cache()
+    x = np.array([p["bytes_per_call"] for p in pts], dtype=np.float64)
+    y = np.array([statistics.mean(times[p["ctx_scale"]]) for p in pts], dtype=np.float64)
+    slope, icpt = np.polyfit(x, y, 1)
+    rate = 1.0 / slope / 1e3  # bytes per us -> GB/s
+    log(f"[bench] least squares over the three scales: marginal rate {rate:.0f} GB/s = {rate / HBM_PEAK_GBPS:.1%} of "
+        f"peak, fixed cost {icpt:.1f} us per call")
+    return {"metric": "paged decode us/call against bytes/call at context scales 1/2, 1, 2 (576 rows)",
+            "points": pts, "marginal_gbps": round(float(rate), 1),
+            "marginal_pct_peak": round(float(rate) / HBM_PEAK_GBPS * 100, 2), "fixed_us_per_call": round(float(icpt), 2)}
 
 
 def bench_decode_small(args, dev):
@@ -1103,10 +1155,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="decode576",
-                    choices=["decode576", "decode256", "decode1x64", "decode-small", "cp512", "prefill32", "admit",
-                             "probe"],
+                    choices=["decode576", "decode256", "decode1x64", "decode-small", "decode-scaling", "cp512",
+                             "prefill32", "admit", "probe"],
                     help="c5 (default, the headline metric), c3 decode, c1 decode, decode at small batches (each "
-                         "decode kernel by path code and the library's choice), c2 code predictor, c4 prefill, admit "
+                         "decode kernel by path code and the library's choice), c5 with its contexts scaled by 1/2, "
+                         "1, 2 (marginal read rate and fixed cost per call), c2 code predictor, c4 prefill, admit "
                          "fast-admission prefill, probe (HBM read ceilings of the decode's access pattern)")
     ap.add_argument("--split", type=int, default=0,
                     help="decode split_tokens: 0 = the library's choice (stream-K at 576 rows), -1 row-parallel, "
@@ -1157,6 +1210,8 @@ def main() -> int:
                 rec["cpu_baseline"]["per_config"] = per
     elif args.workload == "decode-small":
         rec = bench_decode_small(args, dev)
+    elif args.workload == "decode-scaling":
+        rec = bench_decode_scaling(args, dev)
     elif args.workload == "probe":
         rec = bench_probe(args, dev)
     elif args.workload == "cp512":
