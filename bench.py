@@ -6,7 +6,8 @@ ctx = 0, GQA 16/8, head_dim 128, bf16, 16-token pages, every layer with its own 
 page table over one 131,072-page pool (8.59 GB of K+V).  Inputs are resident in HBM before the
 timed region.  Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra] [--workload decode576|decode256|cp512|prefill32|admit]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra]
+                  [--workload decode576|decode256|decode1x64|decode-small|decode-scaling|cp512|prefill32|admit|probe]
 """
 from __future__ import annotations
 
