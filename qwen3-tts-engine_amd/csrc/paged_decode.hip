@@ -500,7 +500,14 @@ __device__ __forceinline__ void write_zero_row(const DecodeArgs& a, int b, int g
 }
 
 // ------------------------------------------------------------------------------ stream-K path
-__device__ __forceinline__ int64_t sk_lo(int64_t k, int64_t nt, int64_t grid) { return k * nt / grid; }
+// p / c with 32-bit arithmetic whenever p fits (the tile-range bounds of every call below 2^32 tile-workgroup
+// products): the 64-bit division is a chain of ~150 scalar instructions on the prologue's critical path.
+__device__ __forceinline__ int64_t udiv_fit(uint64_t p, uint32_t c) {
+  return (p >> 32) == 0 ? (int64_t)((uint32_t)p / c) : (int64_t)(p / c);
+}
+__device__ __forceinline__ int64_t sk_lo(int64_t k, int64_t nt, int64_t grid) {
+  return udiv_fit((uint64_t)k * (uint64_t)nt, (uint32_t)grid);
+}
 
 // Workgroups that take part in a call of NT tiles: at most the resident grid and at most NT (each owns at least one
 // tile, so the workgroups covering a row are a contiguous index range, which the combine relies on), and at most
@@ -899,14 +906,16 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const Dec
       }
     }
   };
-  if (p1 == p0) {
+  // (G == 0 only when NT == 0, which implies p1 == p0; testing it here keeps the load of prefix[batch] beside the
+  // other two, one round trip, instead of behind this branch.)
+  const int64_t G = sk_effective_grid(a.grid, NT);
+  if (p1 == p0 || G == 0) {
     write_zero_row(a, b, g, lane);
     store_slot();
     return;
   }
-  const int64_t G = sk_effective_grid(a.grid, NT);
-  const int kf = (int)(((int64_t)(p0 + 1) * G - 1) / NT);
-  const int kl = (int)(((int64_t)p1 * G - 1) / NT);
+  const int kf = (int)udiv_fit((uint64_t)(p0 + 1) * (uint64_t)G - 1, (uint32_t)NT);
+  const int kl = (int)udiv_fit((uint64_t)p1 * (uint64_t)G - 1, (uint32_t)NT);
   if (kf != kl) {
     const int first_slot = sk_lo(kf, NT, G) < p0 ? 1 : 0;
     merge_records(a, b, g, lane, kl - kf + 1, [&](int i) -> const float* {
