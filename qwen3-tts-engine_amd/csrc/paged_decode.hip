@@ -509,6 +509,36 @@ __device__ __forceinline__ int64_t sk_lo(int64_t k, int64_t nt, int64_t grid) {
   return udiv_fit((uint64_t)k * (uint64_t)nt, (uint32_t)grid);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave: four DPP row shifts within each 16 lanes, then the two row
+// broadcasts across rows (lanes outside the shifted range or the masked rows add zero).  Seven VALU steps where a
+// shuffle-based scan waits for six LDS-crossbar round trips.
+__device__ __forceinline__ int wave_scan_incl(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15, into rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31, into rows 2 and 3
+  return x;
+}
+
+// The largest row r in [0, n) with pre[r] <= t, for a wave-uniform t with pre[0] <= t over the non-decreasing pre
+// (the rows' first tiles; an empty row shares its successor's), found by the whole wave: each lane tests one row of
+// an evenly spaced sample and a ballot counts the sampled rows at or before t, which narrows the range 64-fold per
+// LDS round trip (4,096 rows: two round trips, where a binary search waits for twelve).  All lanes must be active.
+__device__ __forceinline__ int row_at_or_before(const int* pre, int n, int t, int lane) {
+  int lo = 0, hi = n;
+  while (hi - lo > 1) {
+    const int stride = (hi - lo + 63) >> 6;
+    const int r = lo + lane * stride;
+    const int k = __builtin_popcountll(__ballot(r < hi && pre[r] <= t));  // lanes 0 .. k-1: rows at or before t
+    const int nlo = lo + (k - 1) * stride;
+    hi = min(hi, nlo + stride);
+    lo = nlo;
+  }
+  return __builtin_amdgcn_readfirstlane(lo);
+}
+
 // Workgroups that take part in a call of NT tiles: at most the resident grid and at most NT (each owns at least one
 // tile, so the workgroups covering a row are a contiguous index range, which the combine relies on), and at most
 // NT / 4 unless that leaves fewer than min(NT, 8): with one tile each, small batches split every row into
@@ -586,16 +616,13 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     s_ctx[r] = c;
     sum += (c + kTile - 1) / kTile;
   }
-  int x = sum;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
+  const int x = wave_scan_incl(sum);
   if (lane == 63) s_wsum[wv] = x;
   __syncthreads();
-  int wbase = 0;
-  for (int w = 0; w < wv; ++w) wbase += s_wsum[w];
+  // This wave's base: the sum of the earlier waves' totals (one LDS read per lane and a second wave scan).
+  const int nw = nthr >> 6;
+  const int wt = wave_scan_incl(lane < nw ? s_wsum[lane] : 0);
+  const int wbase = wv == 0 ? 0 : __builtin_amdgcn_readlane(wt, wv - 1);
   int run = wbase + x - sum;
   for (int r = r0; r < r1; ++r) {
     s_prefix[r] = run;
@@ -619,12 +646,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     mid = kHalves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
     mid_row = -1;
     if (kHalves == 2 && lo_w < mid && mid < hi_w) {
-      int lo_r = 0, hi_r = B;  // largest row with prefix[row] <= mid
-      while (hi_r - lo_r > 1) {
-        const int mr = (lo_r + hi_r) >> 1;
-        if (s_prefix[mr] <= mid) lo_r = mr; else hi_r = mr;
-      }
-      mid_row = __builtin_amdgcn_readfirstlane(s_prefix[lo_r] < mid ? lo_r : -1);  // uniform: a scalar
+      const int r = row_at_or_before(s_prefix, B, mid, lane);  // uniform: a scalar
+      mid_row = s_prefix[r] < mid ? r : -1;
     }
   };
   int lo_w, hi_w, mid, mid_row;
@@ -653,9 +676,16 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     L.off = 0;
     L.nvalid = 0;
     int vrow = 0, vflags = 0;
+    // The rows of the list's first and last tiles, by the whole wave; each lane then searches only between them.
+    // (Not in the norm/rope form: at its register limit the two bounds spilled.)
+    int lo0 = 0, hi0 = B;
+    if constexpr (!kRope) {
+      lo0 = row_at_or_before(s_prefix, B, cb, lane);
+      hi0 = row_at_or_before(s_prefix, B, cb + L.n - 1, lane) + 1;
+    }
     if (lane < L.n) {
       const int t = cb + lane;
-      int lo_r = 0, hi_r = B;  // largest row with prefix[row] <= t
+      int lo_r = lo0, hi_r = hi0;  // largest row with prefix[row] <= t
       while (hi_r - lo_r > 1) {
         const int mid = (lo_r + hi_r) >> 1;
         if (s_prefix[mid] <= t) lo_r = mid; else hi_r = mid;
