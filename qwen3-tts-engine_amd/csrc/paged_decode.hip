@@ -109,14 +109,13 @@ __device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int c) {
 // Tokens row b attends over.  Append form: the cached tokens plus the new one; a row whose new
 // token would not fit the table (or with cache_seqlens < 0) is skipped: zero output, nothing written.
 template <bool kAppend>
+__device__ __forceinline__ int ctx_of(int c, int cap) {
+  if constexpr (kAppend) return (c < 0 || c >= cap) ? 0 : c + 1;
+  else return c < 0 ? 0 : (c > cap ? cap : c);
+}
+template <bool kAppend>
 __device__ __forceinline__ int row_ctx(const DecodeArgs& a, int b) {
-  const int c = a.seqlens[b];
-  if constexpr (kAppend) {
-    const int cap = a.max_pages * a.page_size;
-    return (c < 0 || c >= cap) ? 0 : c + 1;
-  } else {
-    return clamp_ctx(a, c);
-  }
+  return ctx_of<kAppend>(a.seqlens[b], a.max_pages * a.page_size);
 }
 
 __device__ __forceinline__ int readlane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
@@ -1083,31 +1082,42 @@ __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_k
   const int CT = W * a.row_per;              // tiles per chunk (the one-launch path: the whole table)
   const int tb = (int)blockIdx.z * CT;       // first tile of this workgroup's chunk
 
+  // Every load that does not depend on the context goes out together with the row's cache_seqlens entry: the
+  // table entry of this lane's tile, q, (append form) the new k/v rows, (norm/rope form) the weights and cos/sin.
+  // The empty asm with a memory clobber keeps the compiler from sinking them below the exit test of chunks past the
+  // row's end, which would put the table and q behind the seqlens round trip.
+  const int c_row = a.seqlens[b];
   const int cap = a.max_pages * a.page_size;
   const int t = kTile * (tb + w + lane * W);  // first token of this lane's tile
   const int pidx = min(t, cap - 1) / a.page_size;
   const int page = a.bt[(int64_t)b * a.bt_sb + pidx];
   uint4 q[kG];
   load_q(a, b, g, dl, q);
-  uint4 rc = make_uint4(0u, 0u, 0u, 0u), rs = rc;
+  uint4 rc = make_uint4(0u, 0u, 0u, 0u), rs = rc, qw = rc, kw = rc, kn = rc, vn = rc;
   if constexpr (kRope) {
     rc = ld16(a.rcos + (int64_t)b * a.rs_sb + dl);
     rs = ld16(a.rsin + (int64_t)b * a.rs_sb + dl);
-    const uint4 w = ld16(a.qn_w + dl);
-#pragma unroll
-    for (int h = 0; h < kG; ++h) q[h] = qk_norm_rope16(q[h], w, rc, rs, a.eps);
+    qw = ld16(a.qn_w + dl);
+    if constexpr (kAppend) kw = ld16(a.kn_w + dl);
   }
   if constexpr (kAppend) {
     const uint32_t dim_off = (uint32_t)(lane & 15) * 16;
-    uint4 kn = buffer_load16_s(make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2), dim_off, 0);
-    const uint4 vn = buffer_load16_s(make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2), dim_off, 0);
-    if constexpr (kRope) kn = qk_norm_rope16(kn, ld16(a.kn_w + dl), rc, rs, a.eps);
+    kn = buffer_load16_s(make_rsrc(a.k_new + (int64_t)b * a.kn_sb + g * kD, kD * 2), dim_off, 0);
+    vn = buffer_load16_s(make_rsrc(a.v_new + (int64_t)b * a.vn_sb + g * kD, kD * 2), dim_off, 0);
+  }
+  __asm__ volatile("" ::: "memory");
+  if constexpr (kRope) {
+#pragma unroll
+    for (int h = 0; h < kG; ++h) q[h] = qk_norm_rope16(q[h], qw, rc, rs, a.eps);
+  }
+  if constexpr (kAppend) {
+    if constexpr (kRope) kn = qk_norm_rope16(kn, kw, rc, rs, a.eps);
     if (lane < kD / 8) {
       snew[w][0][lane] = kn;
       snew[w][1][lane] = vn;
     }
   }
-  const int ctx = row_ctx<kAppend>(a, b);
+  const int ctx = ctx_of<kAppend>(c_row, cap);
   const int nrow = (ctx + kTile - 1) / kTile;  // tiles of the row
   const int nch = (nrow + CT - 1) / CT;        // chunks holding tiles of the row
   // Chunks past the row's end have nothing to do (chunk 0 stays: it writes the zero row of an empty one).  The
