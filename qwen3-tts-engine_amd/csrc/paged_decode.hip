@@ -74,6 +74,7 @@ struct DecodeArgs {
   int64_t o_sb, o_sh;
   float* ws;            // partial records
   int* prefix;          // stream-K: [batch + 1] tile prefix sums
+  int* slot_page;       // stream-K append forms: [batch] page id of each row's new-token slot (from the decode kernel)
   int batch, hkv, split_tokens, max_splits, grid;
   int row_per;          // row-parallel path: tiles per wave of the table capacity (the host picks the kernel)
   float scale_log2;
@@ -730,7 +731,12 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
         q[1] = ld16(st + kD * 2 + dl * 2);
       }
       if constexpr (kAppend) {
-        if (fl & kRowEnd) take_staged_token(a, L, grp, j, st, T);
+        if (fl & kRowEnd) {
+          take_staged_token(a, L, grp, j, st, T);
+          // The new token's slot lies in this tile's page: hand its id to the combine kernel, which stores the slot
+          // (one wave per row; the combine then needs no table lookup of its own).
+          if (g == 0 && lane == 0) a.slot_page[readlane(vrow, j)] = readlane(L.page, j);
+        }
       }
       tile_update(a, L, q, T, j, grp, m, l, acc);
       if (fl & kLast) {
@@ -901,8 +907,10 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
 // Append form: it also writes each row's new k/v row into its page slot.  The decode kernel attends with the staged
 // copies and never reads the slot, and no other row reads it in the same call, so the store can wait for this
 // kernel, which runs without a read stream to disturb: the same 2.1 MB of 256 B stores cost ~5 us inside the decode
-// kernel's read stream (576 rows, 296k tokens).  Its loads are issued beside the merge's (the slot's page id next
-// to the record loads) and the stores come last, so the slot write adds no round trip to the merge's chain.
+// kernel's read stream (576 rows, 296k tokens).  The slot's page id comes from the decode kernel (the wave holding
+// the row's last tile writes it to the workspace), so the slot's loads (the new rows, the row's cache_seqlens, that
+// id) all go out with the prefix, one round trip, and the stores come last: the slot write adds no round trip to
+// the merge's chain (the table lookup it used to make here was a second one).
 template <bool kAppend, bool kRope = false>
 __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
@@ -923,7 +931,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const Dec
       kw = qk_norm_rope64(kw, reinterpret_cast<const uint32_t*>(a.kn_w)[lane],
                           reinterpret_cast<const uint32_t*>(a.rcos + (int64_t)b * a.rs_sb)[lane],
                           reinterpret_cast<const uint32_t*>(a.rsin + (int64_t)b * a.rs_sb)[lane], a.eps);
-    if (c >= 0 && c < a.max_pages * a.page_size) page = a.bt[(int64_t)b * a.bt_sb + c / a.page_size];
+    if (c >= 0 && c < a.max_pages * a.page_size) page = a.slot_page[b];
   }
   auto store_slot = [&]() {
     if constexpr (kAppend) {
@@ -1411,7 +1419,7 @@ size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int spl
       return n <= 1 ? 0 : (size_t)batch * n * hkv * kRowRec * sizeof(float);
     }
     case Path::kStreamK:
-      return align256((size_t)(batch + 1) * sizeof(int)) +
+      return align256((size_t)(batch + 1) * sizeof(int)) + align256((size_t)batch * sizeof(int)) +
              (size_t)sk_grid(hkv) * kSkSlots * hkv * kPartFloats * sizeof(float);
     case Path::kFixed: break;
   }
@@ -1589,7 +1597,9 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     a.grid = sk_grid_of(num_kv_heads, rope ? 2 : (append ? 1 : 0));
     a.grid = sk_effective_grid_host(a.grid, nt_bound);
     a.prefix = static_cast<int*>(workspace);
-    a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256((size_t)(batch + 1) * sizeof(int)));
+    const size_t pb = align256((size_t)(batch + 1) * sizeof(int));
+    a.slot_page = reinterpret_cast<int*>(static_cast<char*>(workspace) + pb);
+    a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + pb + align256((size_t)batch * sizeof(int)));
     if (sk_halves(num_kv_heads) == 2) {
       const dim3 block2(2 * 64 * num_kv_heads);
       if (rope)
