@@ -65,6 +65,13 @@ template <bool kAppend, int kNV, bool kRope = false>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void cp_attn_kernel(const CpArgs a) {
   static_assert(kAppend || !kRope, "the norm/rope form is an append form");
   const int wave = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  // Every argument the wave uses is read before the exit test of the waves past the last (row, head) pair: left to
+  // itself the compiler reads the pair count alone, waits, and only then the rest, two more argument round trips
+  // ahead of the first memory load.
+  __asm__ volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.out), "s"(a.q_sb), "s"(a.k_sb), "s"(a.k_sh), "s"(a.k_ss),
+                   "s"(a.v_sb), "s"(a.v_sh), "s"(a.v_ss), "s"(a.o_sb), "s"(a.hkv), "s"(a.n_live), "s"(a.scale_log2));
+  if constexpr (kAppend) __asm__ volatile("" ::"s"(a.k_new), "s"(a.v_new), "s"(a.kn_sb), "s"(a.vn_sb));
+  if constexpr (kRope) __asm__ volatile("" ::"s"(a.qn), "s"(a.kn), "s"(a.cs), "s"(a.sn), "s"(a.eps));
   if (wave >= a.pairs) return;
   const int b = __builtin_amdgcn_readfirstlane(wave / a.hkv);
   const int g = __builtin_amdgcn_readfirstlane(wave - b * a.hkv);
