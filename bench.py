@@ -193,13 +193,33 @@ def bench_decode(args, dev, name, cpu_budget_s: float = 12.0):
         return q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table,
                                    wl.scale, args.split)
 
-    ms_per_step, frame_ms, _ = time_graph(dev, lambda: [layer_call(L) for L in wl.layers], args.steps, args.warmup,
-                                          getattr(args, "min_warm_s", 0.0))
+    # The engine's frame passes one ctx and one table to all 28 calls (engine/talker.py:77, 107-112), so one plan per
+    # frame serves them (q3attn.decode_plan); here each layer has its own table, so the frame's plan launch builds 28
+    # plans, one per table, inside the timed graph.
+    bts = torch.stack([L.block_table for L in wl.layers])
+    plan_ok = args.split == 0 and not args.no_plan and q3attn.decode_plan(
+        wl.cache_seqlens, bts, wl.page_size) is not None
+
+    def planned_frame():
+        plans = q3attn.decode_plan(wl.cache_seqlens, bts, wl.page_size)
+        return [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, bts[i], wl.scale, plan=plans[i])
+                for i, L in enumerate(wl.layers)]
+
+    unplanned_ms, unplanned_frame_ms, _ = time_graph(dev, lambda: [layer_call(L) for L in wl.layers], args.steps,
+                                                     args.warmup, getattr(args, "min_warm_s", 0.0))
+    unplanned_us = statistics.mean(unplanned_frame_ms) * 1e3 / LAYERS
+    log(f"[bench] unplanned: {args.steps} graph replays of {LAYERS} calls: events "
+        f"{statistics.mean(unplanned_frame_ms):.3f} ms/frame = {unplanned_us:.1f} us/call")
+    if plan_ok:
+        ms_per_step, frame_ms, _ = time_graph(dev, planned_frame, args.steps, args.warmup,
+                                              getattr(args, "min_warm_s", 0.0))
+    else:
+        ms_per_step, frame_ms = unplanned_ms, unplanned_frame_ms
     avg_call_us = statistics.mean(frame_ms) * 1e3 / LAYERS
     achieved = nbytes / (avg_call_us * 1e-6) / 1e9
-    log(f"[bench] {args.steps} graph replays of {LAYERS} calls: wall {ms_per_step:.3f} ms/step; events "
-        f"{statistics.mean(frame_ms):.3f} ms/frame (min {min(frame_ms):.3f}) = {avg_call_us:.1f} us/call; "
-        f"{achieved:.0f} GB/s = {achieved / HBM_PEAK_GBPS:.1%} of peak")
+    log(f"[bench] {'planned' if plan_ok else 'unplanned'}: {args.steps} graph replays of {LAYERS} calls: wall "
+        f"{ms_per_step:.3f} ms/step; events {statistics.mean(frame_ms):.3f} ms/frame (min {min(frame_ms):.3f}) = "
+        f"{avg_call_us:.1f} us/call; {achieved:.0f} GB/s = {achieved / HBM_PEAK_GBPS:.1%} of peak")
 
     # Eager calls with an event pair around each (host launch gaps excluded): extra information.
     cur = torch.cuda.current_stream(dev)
@@ -236,9 +256,11 @@ def bench_decode(args, dev, name, cpu_budget_s: float = 12.0):
         metric = "paged decode attn µs/step at 1 seat x 64 tokens, 1×MI355X"
     rec = base_record(metric, round(ms_per_step * 1e3, 2), "us/step", args, ms_per_step, False, {
         "workload": desc, "rows": wl.batch, "sum_ctx": int(wl.ctx.sum()), "layers_per_step": LAYERS,
-        "split_tokens": args.split or "stream-K", "parallelism": "single GPU"})
+        "split_tokens": args.split or "stream-K", "parallelism": "single GPU",
+        "decode_plan": "one plan launch per frame (28 tables) inside the timed graph" if plan_ok else "none"})
     rec.update({
         "us_per_layer_call": round(avg_call_us, 2),
+        "us_per_layer_call_unplanned": round(unplanned_us, 2),
         "us_per_layer_call_eager": round(eager_call_us, 2),
         "hbm_gbps": round(achieved, 1),
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBPS, 2),
@@ -246,7 +268,7 @@ def bench_decode(args, dev, name, cpu_budget_s: float = 12.0):
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic() if name == "decode576" else None,
-            "kernel": decode_kernel_name(wl, args.split) + ", per call inside the graph",
+            "kernel": decode_kernel_name(wl, args.split, plan_ok) + ", per call inside the graph",
             "bytes_per_call": nbytes,
         },
         "cpu_baseline": cpu,
@@ -256,10 +278,13 @@ def bench_decode(args, dev, name, cpu_budget_s: float = 12.0):
     return rec
 
 
-def decode_kernel_name(wl, split):
+def decode_kernel_name(wl, split, planned=False):
     """The kernels one decode call of this workload launches (the library needs no workspace exactly when it takes
     the row-parallel path, for split 0)."""
     from q3attn import _lib
+
+    if planned:
+        return "paged decode call (planned stream-K decode kernel + combine kernel; the frame's plan kernel shared)"
 
     L = wl.layers[0]
     lib = _lib.lib()
@@ -1166,6 +1191,9 @@ def main() -> int:
                     help="decode split_tokens: 0 = the library's choice (stream-K at 576 rows), -1 row-parallel, "
                          "-2 chunked, -3 stream-K, > 0 fixed split of that many tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-plan", action="store_true",
+                    help="decode frames without the per-frame plan (q3attn.decode_plan): every call scans the lengths "
+                         "and looks its pages up itself")
     ap.add_argument("--no-append", action="store_true",
                     help="skip the KV-append comparisons (decode: fused append; prefill: the prompt step)")
     ap.add_argument("--seed", type=int, default=0)

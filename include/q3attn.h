@@ -28,8 +28,9 @@ extern "C" {
 /* ABI version of this header (bumped on any signature change or new entry point); q3a_abi_version() returns the
  * library's.  2: K and V carry separate strides in the prefill and code-predictor entry points.  3: q3a_prefill_append.  4: q3a_paged_decode_append_rope.
  * 5: q3a_prefill_dense_append.  6: q3a_prefill_dense_append_rope, q3a_prefill_append_rope,
- * q3a_cp_attn_append_rope.  7: the decode path codes below (negative split_tokens). */
-#define Q3A_ABI_VERSION 7
+ * q3a_cp_attn_append_rope.  7: the decode path codes below (negative split_tokens).  8: per-frame decode plans
+ * (q3a_paged_decode_plan_bytes, q3a_paged_decode_plan, Q3A_DECODE_PLANNED). */
+#define Q3A_ABI_VERSION 8
 
 /* Decode decomposition codes, passed as split_tokens to the q3a_paged_decode* entry points (0 lets the library
  * choose, a positive multiple of 16 is a fixed split of that many tokens):
@@ -44,6 +45,10 @@ extern "C" {
 #define Q3A_DECODE_ROW (-1)
 #define Q3A_DECODE_CHUNKS (-2)
 #define Q3A_DECODE_STREAMK (-3)
+/*   Q3A_DECODE_PLANNED  stream-K with the partition, the tile lists and the page ids read from a plan that
+ *                       q3a_paged_decode_plan built for this call's cache_seqlens and block table; the workspace
+ *                       argument is that plan (see q3a_paged_decode_plan) */
+#define Q3A_DECODE_PLANNED (-4)
 int q3a_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -85,6 +90,45 @@ int q3a_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
                      int num_kv_heads, int head_dim, float softmax_scale, int split_tokens,
                      void* stream);
+
+/*
+ * Per-frame decode plan: the stream-K decomposition of a decode call, computed once and read by every call that
+ * shares its cache_seqlens and block table.
+ *
+ * No reference counterpart as a function: flash-attn 2 recomputes its split scheduling inside every
+ * flash_attn_with_kvcache call (engine/talker.py:77, 28 calls per frame from Talker._decode, engine/talker.py:63-80,
+ * all with the same ctx and bt, engine/talker.py:107-112); flash-attn 3 exposes the same idea as
+ * get_scheduler_metadata / scheduler_metadata.  Here the plan holds the tile prefix sums, every stream-K workgroup's
+ * tile range, each wave's first tile list and, for every 16-token tile, its row, offset, valid tokens and page id,
+ * so a planned call's waves issue their first K/V loads one memory round trip after launch.
+ *
+ *   cache_seqlens [batch] int32   as the calls will pass it (plain form: context lengths; append forms: tokens
+ *                                 already cached)
+ *   block_table   num_tables tables [batch, max_pages_per_seq] int32 (row stride bt_stride_b, table stride
+ *                 bt_stride_table): plan t is for table t (one table in the engine; one per layer where each layer
+ *                 has its own table)
+ *   form          Q3A_PLAN_PLAIN (q3a_paged_decode), Q3A_PLAN_APPEND (q3a_paged_decode_append),
+ *                 Q3A_PLAN_APPEND_ROPE (q3a_paged_decode_append_rope)
+ *   plans         num_tables plans of q3a_paged_decode_plan_bytes() bytes each, plan t at plans + t * plan_stride
+ *                 (bytes; 256-aligned), plans_bytes in all
+ *
+ * A call uses plan t by passing split_tokens = Q3A_DECODE_PLANNED and the plan as its workspace (with the plan's
+ * size as workspace_bytes); it must pass the same cache_seqlens pointer, table t, shape and form, which the library
+ * checks on the host (Q3A_EINVAL otherwise).  The plan reflects the lengths and table entries at the time the plan
+ * kernel ran: rebuild it (on the same stream, before the calls) whenever either changes.  A planned call also writes
+ * its partial records into the plan buffer, so calls that share one plan must not overlap (calls on one stream do
+ * not).  Plans exist for the shapes the library decodes with stream-K by itself (split_tokens 0: tables over 128
+ * tokens with more than 64 rows, or more than 16 rows of tables over 2,048 tokens) with 8 KV heads, batch <= 4096 and
+ * page_size <= 4096; q3a_paged_decode_plan_bytes() returns 0 for other shapes.
+ */
+#define Q3A_PLAN_PLAIN 0
+#define Q3A_PLAN_APPEND 1
+#define Q3A_PLAN_APPEND_ROPE 2
+size_t q3a_paged_decode_plan_bytes(int batch, int num_kv_heads, int max_pages_per_seq, int page_size);
+int q3a_paged_decode_plan(const int32_t* cache_seqlens, const int32_t* block_table, int64_t bt_stride_b,
+                          int64_t bt_stride_table, int num_tables, int max_pages_per_seq, int page_size, int batch,
+                          int num_kv_heads, int form, void* plans, int64_t plan_stride, size_t plans_bytes,
+                          void* stream);
 
 /*
  * Talker decode attention with this step's K/V append fused in.

@@ -34,6 +34,8 @@
 // drain the tile in flight.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
+#include <unordered_map>
 
 #include "q3a_common.h"
 #include "../../include/q3attn.h"
@@ -75,6 +77,11 @@ struct DecodeArgs {
   float* ws;            // partial records
   int* prefix;          // stream-K: [batch + 1] tile prefix sums
   int* slot_page;       // stream-K append forms: [batch] page id of each row's new-token slot (from the decode kernel)
+  // Planned stream-K calls (kPlan): the per-frame plan's workgroup ranges, each wave's first tile list and every
+  // tile's entry (see paged_decode_plan_kernel).
+  const int* plan_wg;
+  const int2* plan_first;
+  const int2* plan_tiles;
   int batch, hkv, split_tokens, max_splits, grid;
   int row_per;          // row-parallel path: tiles per wave of the table capacity (the host picks the kernel)
   float scale_log2;
@@ -553,13 +560,156 @@ constexpr int kLast = 2;      // tile closes a segment
 constexpr int kRowStart = 4;  // tile is tile 0 of its row
 constexpr int kRowEnd = 8;    // tile is the last tile of its row
 
+// Block-wide: each row's clamped context into s_ctx, the exclusive prefix sum of its 16-token tile counts into
+// s_prefix[0..B] (s_prefix[B] = NT, the call's tile count), with a DPP scan per wave and one over the waves'
+// totals.  Every thread of the block must call it; it ends with a barrier and returns NT.
+template <bool kAppend>
+__device__ __forceinline__ int sk_tile_scan(const DecodeArgs& a, int* s_ctx, int* s_prefix, int* s_wsum) {
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int B = a.batch;
+  const int per = (B + nthr - 1) / nthr;
+  const int r0 = min(B, tid * per), r1 = min(B, r0 + per);
+  int sum = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int c = row_ctx<kAppend>(a, r);
+    s_ctx[r] = c;
+    sum += (c + kTile - 1) / kTile;
+  }
+  const int x = wave_scan_incl(sum);
+  if (lane == 63) s_wsum[wv] = x;
+  __syncthreads();
+  // This wave's base: the sum of the earlier waves' totals (one LDS read per lane and a second wave scan).
+  const int nw = nthr >> 6;
+  const int wt = wave_scan_incl(lane < nw ? s_wsum[lane] : 0);
+  const int wbase = wv == 0 ? 0 : __builtin_amdgcn_readlane(wt, wv - 1);
+  int run = wbase + x - sum;
+  for (int r = r0; r < r1; ++r) {
+    s_prefix[r] = run;
+    run += (s_ctx[r] + kTile - 1) / kTile;
+  }
+  if (tid == nthr - 1) s_prefix[B] = wbase + x;
+  __syncthreads();
+  return s_prefix[B];
+}
+
+// ------------------------------------------------------------------------------ per-frame plan (stream-K)
+// The 28 decode calls of a talker frame share cache_seqlens (and, in the engine, the block table), so the stream-K
+// partition, each wave's tile list and the tiles' page ids can be computed once per frame and read by every call:
+// a planned call's waves load their first tile list (page ids included) in one round trip, where the unplanned
+// prologue waits for cache_seqlens, a block-wide scan, row searches in LDS and then the table.
+//
+// A tile's entry (int2): x = its page id (as the table holds it), y = row | (offset in page / 16) << 13 |
+// valid tokens << 21 | segment flags << 26, with the flags of the wave range that holds the tile.
+constexpr int kPlanWgInts = 8;  // per decode workgroup: lo, hi, mid, mid_row, mid_whole, mid_from_lo, 0, 0
+constexpr int kPlanRowBits = 13;
+constexpr int kPlanOffBits = 8;
+
+__device__ __forceinline__ int plan_pack(int row, int off_tiles, int nvalid, int flags) {
+  return row | (off_tiles << kPlanRowBits) | (nvalid << (kPlanRowBits + kPlanOffBits)) |
+         (flags << (kPlanRowBits + kPlanOffBits + 5));
+}
+
+// One launch per frame: grid (x, tables), 1,024 threads.  Every workgroup scans the rows itself (at most 4,096
+// ints); workgroup (0, t) writes table t's prefix sums (the combine kernel's input), and the tiles and decode
+// workgroups are spread over x.  Plan t lives at plans + t * plan_stride with the layout of the host's plan_layout.
+struct PlanArgs {
+  char* plans;
+  int64_t plan_stride;
+  int64_t bt_stable;  // element stride between the tables
+  int64_t wg_off, first_off, tiles_off;  // byte offsets inside one plan
+  int halves;
+};
+
+template <bool kAppend>
+__global__ __launch_bounds__(1024) void paged_decode_plan_kernel(const DecodeArgs a, const PlanArgs p) {
+  __shared__ int s_ctx[kSkMaxRows];
+  __shared__ int s_prefix[kSkMaxRows + 1];
+  __shared__ int s_wsum[16];
+  const int NT = sk_tile_scan<kAppend>(a, s_ctx, s_prefix, s_wsum);
+  const int ge = sk_effective_grid(a.grid, NT);
+  const int B = a.batch;
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  const int64_t tbl = blockIdx.y;
+  const int32_t* bt = a.bt + tbl * p.bt_stable;
+  char* base = p.plans + tbl * p.plan_stride;
+  int* wg = reinterpret_cast<int*>(base + p.wg_off);
+  int2* first = reinterpret_cast<int2*>(base + p.first_off);
+  int2* tiles = reinterpret_cast<int2*>(base + p.tiles_off);
+  if (blockIdx.x == 0) {
+    int* prefix = reinterpret_cast<int*>(base);
+    for (int r = tid; r <= B; r += nthr) prefix[r] = s_prefix[r];
+  }
+  // The largest row r with s_prefix[r] <= t (t < NT; an empty row shares its successor's prefix).
+  auto row_of = [&](int t) {
+    int lo = 0, hi = B;
+    while (hi - lo > 1) {
+      const int md = (lo + hi) >> 1;
+      if (s_prefix[md] <= t) lo = md; else hi = md;
+    }
+    return lo;
+  };
+  const int stride = gridDim.x * nthr;
+  // Decode workgroup ranges, exactly as the unplanned kernel computes them; workgroups past the effective grid get
+  // an empty range and exit.
+  for (int w = blockIdx.x * nthr + tid; w < a.grid; w += stride) {
+    int v[kPlanWgInts] = {0, 0, 0, -1, 0, 0, 0, 0};
+    if (w < ge) {
+      const int lo_w = (int)sk_lo(w, NT, ge), hi_w = (int)sk_lo(w + 1, NT, ge);
+      const int mid = p.halves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
+      int mid_row = -1;
+      if (p.halves == 2 && lo_w < mid && mid < hi_w) {
+        const int r = row_of(mid);
+        mid_row = s_prefix[r] < mid ? r : -1;
+      }
+      v[0] = lo_w;
+      v[1] = hi_w;
+      v[2] = mid;
+      v[3] = mid_row;
+      if (mid_row >= 0) {
+        v[4] = s_prefix[mid_row] >= lo_w && s_prefix[mid_row + 1] <= hi_w;
+        v[5] = s_prefix[mid_row] <= lo_w;
+      }
+    }
+    int4* d = reinterpret_cast<int4*>(wg + (int64_t)w * kPlanWgInts);
+    d[0] = make_int4(v[0], v[1], v[2], v[3]);
+    d[1] = make_int4(v[4], v[5], v[6], v[7]);
+  }
+  // Tiles: the workgroup that holds tile t is the largest k with sk_lo(k) <= t, i.e. ((t + 1) ge - 1) / NT.
+  for (int t = blockIdx.x * nthr + tid; t < NT; t += stride) {
+    const int k = (int)udiv_fit((uint64_t)(t + 1) * (uint64_t)ge - 1, (uint32_t)NT);
+    const int lo_w = (int)sk_lo(k, NT, ge), hi_w = (int)sk_lo(k + 1, NT, ge);
+    const int mid = p.halves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
+    const int half = t >= mid ? 1 : 0;
+    const int lo = half ? mid : lo_w, hi = half ? hi_w : mid;
+    const int row = row_of(t);
+    const int mt = t - s_prefix[row];
+    const int ntr = s_prefix[row + 1] - s_prefix[row];
+    const int tok = mt * kTile;
+    const int pidx = tok / a.page_size;
+    const int page = bt[(int64_t)row * a.bt_sb + pidx];
+    const int off = tok - pidx * a.page_size;
+    const int nvalid = min(kTile, s_ctx[row] - tok);
+    const int flags = ((mt == 0 || t == lo) ? kFirst : 0) | ((mt == ntr - 1 || t == hi - 1) ? kLast : 0) |
+                      (mt == 0 ? kRowStart : 0) | (mt == ntr - 1 ? kRowEnd : 0);
+    const int2 e = make_int2(page, plan_pack(row, off / kTile, nvalid, flags));
+    tiles[t] = e;
+    if (t - lo < 64) first[((int64_t)k * p.halves + half) * 64 + (t - lo)] = e;
+  }
+}
+
 // kHalves == 2 (8 KV heads): each workgroup runs two waves per KV head, the first taking the first half of the
 // workgroup's tile range and the second the other half, so a CU holds one workgroup of 16 waves instead of two of 8.
 // The row that straddles the midpoint is merged in LDS (the two waves' states) instead of through two partial
 // records in memory, which halves the records: each costs ~1.6 us per MB written inside the call's read stream.
 // Every record keeps its meaning for the combine (slot 0: the segment opened at the range start, slot 1: the one
 // closed at the range end), and a row held whole by the workgroup is written directly.
-template <bool kAppend, bool kRope = false, int kHalves = 1>
+//
+// kPlan: a planned call (the range and the waves' first tile lists come from the per-frame plan).
+template <bool kAppend, bool kRope = false, int kHalves = 1, bool kPlan = false>
 __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs a) {
   static_assert(kAppend || !kRope, "the norm/rope form is an append form");
   static_assert(kHalves == 1 || kHalves == 2, "one or two waves per KV head");
@@ -589,6 +739,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   constexpr int kOutRing = kStageOut ? 4 : 1;
   __shared__ __align__(16) uint32_t s_out[kStageOut ? kW : 1][kOutRing][kG * kD / 2];
   __shared__ int s_out_row[kStageOut ? kW : 1][kOutRing];
+  // Planned calls: each wave's first tile list (64 entries and the 512 B its copy zero-fills).
+  __shared__ __align__(16) int2 s_plan[kPlan ? kW : 1][kPlan ? 128 : 1];
   int n_out = 0;
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
@@ -607,40 +759,37 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     }
   }
 
-  // Prologue: tiles per row and their exclusive prefix sum (block-wide scan).
-  const int per = (B + nthr - 1) / nthr;
-  const int r0 = min(B, tid * per), r1 = min(B, r0 + per);
-  int sum = 0;
-  for (int r = r0; r < r1; ++r) {
-    const int c = row_ctx<kAppend>(a, r);
-    s_ctx[r] = c;
-    sum += (c + kTile - 1) / kTile;
+  // Prologue: tiles per row and their exclusive prefix sum (block-wide scan).  A planned call reads its range and
+  // its waves' first tile lists from the plan instead (one round trip, no scan, no table lookup).
+  int NT = 0, ge = 0;
+  if constexpr (!kPlan) {
+    NT = sk_tile_scan<kAppend>(a, s_ctx, s_prefix, s_wsum);
+    if (blockIdx.x == 0) {
+      for (int r = tid; r <= B; r += nthr) a.prefix[r] = s_prefix[r];
+    }
+    ge = sk_effective_grid(a.grid, NT);
+    if ((int)blockIdx.x >= ge) return;
   }
-  const int x = wave_scan_incl(sum);
-  if (lane == 63) s_wsum[wv] = x;
-  __syncthreads();
-  // This wave's base: the sum of the earlier waves' totals (one LDS read per lane and a second wave scan).
-  const int nw = nthr >> 6;
-  const int wt = wave_scan_incl(lane < nw ? s_wsum[lane] : 0);
-  const int wbase = wv == 0 ? 0 : __builtin_amdgcn_readlane(wt, wv - 1);
-  int run = wbase + x - sum;
-  for (int r = r0; r < r1; ++r) {
-    s_prefix[r] = run;
-    run += (s_ctx[r] + kTile - 1) / kTile;
+  const int* const pwg = kPlan ? a.plan_wg + (int64_t)blockIdx.x * kPlanWgInts : nullptr;
+  if constexpr (kPlan) {
+    // The wave's first tile list goes straight into LDS (lanes 0-31 copy 16 B each; the other lanes' out-of-range
+    // copies write zeros over the next 512 B), issued beside the scalar loads of the range: no register holds it
+    // through the tile loop.
+    lds_copy16(make_rsrc(a.plan_first + ((int64_t)blockIdx.x * kHalves + half) * 64, 64 * sizeof(int2)),
+               &s_plan[kPlan ? wv : 0][0], lane < 32 ? (uint32_t)lane * 16 : kOutOfRange);
   }
-  if (tid == nthr - 1) s_prefix[B] = wbase + x;
-  __syncthreads();
-  const int NT = s_prefix[B];
-  if (blockIdx.x == 0) {
-    for (int r = tid; r <= B; r += nthr) a.prefix[r] = s_prefix[r];
-  }
-  const int ge = sk_effective_grid(a.grid, NT);
-  if ((int)blockIdx.x >= ge) return;
   // The workgroup's tile range [lo_w, hi_w) and, with two halves, its midpoint; the row that runs across the
   // midpoint (tiles mid - 1 and mid in the same row), if any.  Only two values stay live through the tile loop (the
   // kernel is at its register limit): slot0_tile, the tile whose segment is the range's first (record slot 0), and
   // mid_cut_tile, the midpoint when a row runs across it, else -1.
   auto range_of = [&](int& lo_w, int& hi_w, int& mid, int& mid_row) __attribute__((always_inline)) {
+    if constexpr (kPlan) {
+      lo_w = pwg[0];
+      hi_w = pwg[1];
+      mid = pwg[2];
+      mid_row = pwg[3];
+      return;
+    }
     lo_w = (int)sk_lo(blockIdx.x, NT, ge);
     hi_w = (int)sk_lo(blockIdx.x + 1, NT, ge);
     mid = kHalves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
@@ -652,6 +801,7 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   };
   int lo_w, hi_w, mid, mid_row;
   range_of(lo_w, hi_w, mid, mid_row);
+  if (kPlan && lo_w >= hi_w) return;  // past the effective grid
   const int lo = half == 0 ? lo_w : mid;                 // this wave's half
   const int hi = half == 0 ? mid : hi_w;
   const int slot0_tile = (half == 0 || mid == lo_w) ? lo : -1;
@@ -676,14 +826,32 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     L.off = 0;
     L.nvalid = 0;
     int vrow = 0, vflags = 0;
+    if constexpr (kPlan) {
+      // The wave's first list was loaded with the range; later ones (more than 64 tiles per wave) by one load.
+      int2 e = make_int2(-1, 0);
+      if (cb == lo) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first list's copy (nothing younger is in flight)
+        __asm__ volatile("" ::: "memory");
+        e = s_plan[kPlan ? wv : 0][lane];
+      } else if (lane < L.n) {
+        e = a.plan_tiles[cb + lane];
+      }
+      if (lane < L.n) {
+        L.page = e.x;
+        vrow = e.y & ((1 << kPlanRowBits) - 1);
+        L.off = ((e.y >> kPlanRowBits) & ((1 << kPlanOffBits) - 1)) * kTile;
+        L.nvalid = (e.y >> (kPlanRowBits + kPlanOffBits)) & 31;
+        vflags = (e.y >> (kPlanRowBits + kPlanOffBits + 5)) & 15;
+      }
+    }
     // The rows of the list's first and last tiles, by the whole wave; each lane then searches only between them.
     // (Not in the norm/rope form: at its register limit the two bounds spilled.)
     int lo0 = 0, hi0 = B;
-    if constexpr (!kRope) {
+    if constexpr (!kRope && !kPlan) {
       lo0 = row_at_or_before(s_prefix, B, cb, lane);
       hi0 = row_at_or_before(s_prefix, B, cb + L.n - 1, lane) + 1;
     }
-    if (lane < L.n) {
+    if (!kPlan && lane < L.n) {
       const int t = cb + lane;
       int lo_r = lo0, hi_r = hi0;  // largest row with prefix[row] <= t
       while (hi_r - lo_r > 1) {
@@ -892,8 +1060,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       }
       // Slot 0 is the segment opened at the range's first tile (the row starts there or before), as the combine
       // expects; slot 1 one that runs past the range's end and started after its first tile.
-      const bool from_lo = s_prefix[mid_row] <= lo_w;
-      if (s_prefix[mid_row] >= lo_w && s_prefix[mid_row + 1] <= hi_w)
+      const bool from_lo = kPlan ? pwg[5] != 0 : s_prefix[mid_row] <= lo_w;
+      if (kPlan ? pwg[4] != 0 : (s_prefix[mid_row] >= lo_w && s_prefix[mid_row + 1] <= hi_w))
         write_output(a, mid_row, g, grp, dl, l, acc);
       else
         write_partial(part + ((from_lo ? 0 : 1) * a.hkv + g) * kPartFloats, lane, grp, dl, m, l, acc);
@@ -1395,7 +1563,8 @@ Path choose_path(int batch, int64_t max_ctx, int split_tokens) {
   switch (split_tokens) {
     case Q3A_DECODE_ROW: return row_ok ? Path::kRow : Path::kNone;
     case Q3A_DECODE_CHUNKS: return chunk_ok ? Path::kChunks : Path::kNone;
-    case Q3A_DECODE_STREAMK: return batch <= kSkMaxRows ? Path::kStreamK : Path::kNone;
+    case Q3A_DECODE_STREAMK:
+    case Q3A_DECODE_PLANNED: return batch <= kSkMaxRows ? Path::kStreamK : Path::kNone;
     case 0: break;
     default: return split_tokens > 0 ? Path::kFixed : Path::kNone;
   }
@@ -1429,10 +1598,121 @@ size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int spl
   return (size_t)batch * max_splits * hkv * kPartFloats * sizeof(float);
 }
 
+// Planned stream-K calls.  A plan is a stream-K workspace (prefix sums, slot pages, partial records) followed by the
+// plan proper: the decode workgroups' ranges, each wave's first tile list, and an entry for every tile.
+struct PlanLayout {
+  size_t slot_off, rec_off, wg_off, first_off, tiles_off, bytes;
+};
+
+PlanLayout plan_layout(int batch, int hkv, int max_pages, int page_size) {
+  const int64_t cap_tiles = ((int64_t)max_pages * page_size + kTile - 1) / kTile;
+  const int grid = sk_effective_grid_host(sk_grid(hkv), (int64_t)batch * cap_tiles);
+  PlanLayout L;
+  L.slot_off = align256((size_t)(batch + 1) * sizeof(int));
+  L.rec_off = L.slot_off + align256((size_t)batch * sizeof(int));
+  L.wg_off = L.rec_off + align256((size_t)grid * kSkSlots * hkv * kPartFloats * sizeof(float));
+  L.first_off = L.wg_off + align256((size_t)grid * kPlanWgInts * sizeof(int));
+  L.tiles_off = L.first_off + align256((size_t)grid * sk_halves(hkv) * 64 * sizeof(int2));
+  L.bytes = L.tiles_off + align256((size_t)batch * cap_tiles * sizeof(int2));
+  return L;
+}
+
+// What each plan was built for, keyed by its address: a planned call is checked against it on the host, so a plan
+// built for other lengths' pointer, table, shape or form is refused instead of read.
+struct PlanInfo {
+  int dev, batch, hkv, form, grid, max_pages, page_size;
+  const int32_t* seqlens;
+  const int32_t* bt;
+  int64_t bt_sb;
+  size_t bytes;
+};
+std::mutex g_plan_mu;
+std::unordered_map<const void*, PlanInfo> g_plans;
+
+bool find_plan(const void* plan, PlanInfo* out) {
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  const auto it = g_plans.find(plan);
+  if (it == g_plans.end()) return false;
+  *out = it->second;
+  return true;
+}
+
 }  // namespace
 }  // namespace q3a
 
 using namespace q3a;
+
+extern "C" size_t q3a_paged_decode_plan_bytes(int batch, int num_kv_heads, int max_pages_per_seq, int page_size) {
+  if (batch <= 0 || batch > kSkMaxRows || num_kv_heads != 8 || max_pages_per_seq <= 0 || page_size <= 0 ||
+      page_size % kTile != 0 || page_size > (kTile << kPlanOffBits) ||
+      (int64_t)max_pages_per_seq * page_size > ((int64_t)1 << 30))
+    return 0;
+  // Plans serve the shapes for which the library itself chooses stream-K (small batches take one-launch kernels).
+  if (choose_path(batch, (int64_t)max_pages_per_seq * page_size, 0) != Path::kStreamK) return 0;
+  return plan_layout(batch, num_kv_heads, max_pages_per_seq, page_size).bytes;
+}
+
+extern "C" int q3a_paged_decode_plan(const int32_t* cache_seqlens, const int32_t* block_table, int64_t bt_stride_b,
+                                     int64_t bt_stride_table, int num_tables, int max_pages_per_seq, int page_size,
+                                     int batch, int num_kv_heads, int form, void* plans, int64_t plan_stride,
+                                     size_t plans_bytes, void* stream) {
+  const char* who = "paged_decode_plan";
+  const size_t need = q3a_paged_decode_plan_bytes(batch, num_kv_heads, max_pages_per_seq, page_size);
+  if (need == 0)
+    return fail(Q3A_EINVAL,
+                "%s: no plan for batch %d, %d KV heads, %d pages of %d tokens (need a shape the library decodes "
+                "with stream-K, 1 <= batch <= %d, 8 KV heads, page_size a multiple of %d up to %d)",
+                who, batch, num_kv_heads, max_pages_per_seq, page_size, kSkMaxRows, kTile, kTile << kPlanOffBits);
+  if (form < Q3A_PLAN_PLAIN || form > Q3A_PLAN_APPEND_ROPE) return fail(Q3A_EINVAL, "%s: form %d unknown", who, form);
+  if (!cache_seqlens || !block_table || !plans) return fail(Q3A_EINVAL, "%s: null pointer argument", who);
+  if (num_tables < 1 || num_tables > 65535) return fail(Q3A_EINVAL, "%s: num_tables %d outside [1, 65535]", who, num_tables);
+  if (bt_stride_b < max_pages_per_seq || (num_tables > 1 && bt_stride_table < (int64_t)batch * bt_stride_b))
+    return fail(Q3A_EINVAL, "%s: table strides %lld / %lld overlap", who, (long long)bt_stride_b,
+                (long long)bt_stride_table);
+  if ((uintptr_t)plans % 256 != 0 || plan_stride % 256 != 0 || (num_tables > 1 && plan_stride < (int64_t)need))
+    return fail(Q3A_EINVAL, "%s: plans must be 256-byte aligned with a 256-byte multiple stride >= %zu", who, need);
+  if (plans_bytes < (size_t)(num_tables - 1) * (size_t)plan_stride + need)
+    return fail(Q3A_ESPACE, "%s: %zu bytes < %zu needed", who, plans_bytes,
+                (size_t)(num_tables - 1) * (size_t)plan_stride + need);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(Q3A_ELAUNCH, "%s: no current device", who);
+  const PlanLayout L = plan_layout(batch, num_kv_heads, max_pages_per_seq, page_size);
+  const int64_t cap_tiles = ((int64_t)max_pages_per_seq * page_size + kTile - 1) / kTile;
+  DecodeArgs a{};
+  a.seqlens = cache_seqlens;
+  a.bt = block_table;
+  a.bt_sb = bt_stride_b;
+  a.max_pages = max_pages_per_seq;
+  a.page_size = page_size;
+  a.batch = batch;
+  a.hkv = num_kv_heads;
+  // The grid the decode kernel of this form launches with (the same rule as launch_decode).
+  a.grid = sk_effective_grid_host(sk_grid_of(num_kv_heads, form), (int64_t)batch * cap_tiles);
+  PlanArgs p;
+  p.plans = static_cast<char*>(plans);
+  p.plan_stride = plan_stride;
+  p.bt_stable = bt_stride_table;
+  p.wg_off = (int64_t)L.wg_off;
+  p.first_off = (int64_t)L.first_off;
+  p.tiles_off = (int64_t)L.tiles_off;
+  p.halves = sk_halves(num_kv_heads);
+  const int64_t work = std::max<int64_t>((int64_t)batch * cap_tiles, a.grid);
+  const int gx = (int)std::min<int64_t>(16, std::max<int64_t>(1, (work + 4095) / 4096));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (form == Q3A_PLAN_PLAIN)
+    hipLaunchKernelGGL(paged_decode_plan_kernel<false>, dim3(gx, num_tables), dim3(1024), 0, st, a, p);
+  else
+    hipLaunchKernelGGL(paged_decode_plan_kernel<true>, dim3(gx, num_tables), dim3(1024), 0, st, a, p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  for (int t = 0; t < num_tables; ++t) {
+    const void* key = static_cast<char*>(plans) + (int64_t)t * plan_stride;
+    g_plans[key] = PlanInfo{dev, batch, num_kv_heads, form, a.grid, max_pages_per_seq, page_size, cache_seqlens,
+                            block_table + (int64_t)t * bt_stride_table, bt_stride_b, need};
+  }
+  return Q3A_OK;
+}
 
 extern "C" int q3a_paged_decode_default_split(int batch, int num_kv_heads, int max_pages_per_seq,
                                               int page_size) {
@@ -1492,8 +1772,9 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   if (q_stride_h <= 0 || ((int64_t)(kG - 1) * q_stride_h + head_dim) * 2 >= ((int64_t)1 << 31))
     return fail(Q3A_EINVAL, "%s: q head stride %lld unsupported (need > 0, head pair extent < 2 GiB)", who,
                 (long long)q_stride_h);
-  const bool path_code =
-      split_tokens == Q3A_DECODE_ROW || split_tokens == Q3A_DECODE_CHUNKS || split_tokens == Q3A_DECODE_STREAMK;
+  const bool planned = split_tokens == Q3A_DECODE_PLANNED;
+  const bool path_code = split_tokens == Q3A_DECODE_ROW || split_tokens == Q3A_DECODE_CHUNKS ||
+                         split_tokens == Q3A_DECODE_STREAMK || planned;
   if (!path_code && (split_tokens < 0 || split_tokens % kTile != 0))
     return fail(Q3A_EINVAL, "%s: split_tokens %d is not 0, a path code or a positive multiple of %d", who,
                 split_tokens, kTile);
@@ -1529,11 +1810,31 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
   const int max_splits = sk ? 0 : (chunks ? nchunks : ceil_div(max_ctx, split_tokens));
   if (path == Path::kFixed && max_splits > kMaxSplits)
     return fail(Q3A_EINVAL, "%s: %d splits exceed %d (raise split_tokens)", who, max_splits, kMaxSplits);
-  const size_t need = workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, workspace_split);
-  if (need > 0 && (workspace == nullptr || workspace_bytes_ < need))
-    return fail(Q3A_ESPACE, "%s: workspace %zu bytes < %zu needed", who, workspace_bytes_, need);
-  if (need > 0 && (uintptr_t)workspace % 16 != 0)
-    return fail(Q3A_EINVAL, "%s: workspace must be 16-byte aligned", who);
+  PlanInfo plan{};
+  if (planned) {
+    // The workspace is a plan: it must have been built (q3a_paged_decode_plan) for this call's lengths, table,
+    // shape and form on this device.
+    int dev = -1;
+    (void)hipGetDevice(&dev);
+    const int form = nr != nullptr ? Q3A_PLAN_APPEND_ROPE : (append ? Q3A_PLAN_APPEND : Q3A_PLAN_PLAIN);
+    if (workspace == nullptr || !find_plan(workspace, &plan))
+      return fail(Q3A_EINVAL, "%s: the workspace is not a decode plan (build it with q3a_paged_decode_plan)", who);
+    if (plan.dev != dev || plan.batch != batch || plan.hkv != num_kv_heads || plan.form != form ||
+        plan.max_pages != max_pages_per_seq || plan.page_size != page_size || plan.seqlens != cache_seqlens ||
+        plan.bt != block_table || plan.bt_sb != bt_stride_b)
+      return fail(Q3A_EINVAL,
+                  "%s: the plan was built for another call (device %d, batch %d, %d KV heads, form %d, %d pages of %d "
+                  "tokens, other cache_seqlens or block table)",
+                  who, plan.dev, plan.batch, plan.hkv, plan.form, plan.max_pages, plan.page_size);
+    if (workspace_bytes_ < plan.bytes)
+      return fail(Q3A_ESPACE, "%s: plan buffer %zu bytes < %zu", who, workspace_bytes_, plan.bytes);
+  } else {
+    const size_t need = workspace_bytes(batch, num_kv_heads, max_pages_per_seq, page_size, workspace_split);
+    if (need > 0 && (workspace == nullptr || workspace_bytes_ < need))
+      return fail(Q3A_ESPACE, "%s: workspace %zu bytes < %zu needed", who, workspace_bytes_, need);
+    if (need > 0 && (uintptr_t)workspace % 16 != 0)
+      return fail(Q3A_EINVAL, "%s: workspace must be 16-byte aligned", who);
+  }
   if (nr != nullptr) {
     if (!append) return fail(Q3A_EINVAL, "%s: the norm/rope form needs k_new/v_new", who);
     if (!row && !sk && !chunks)
@@ -1600,7 +1901,25 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     const size_t pb = align256((size_t)(batch + 1) * sizeof(int));
     a.slot_page = reinterpret_cast<int*>(static_cast<char*>(workspace) + pb);
     a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + pb + align256((size_t)batch * sizeof(int)));
-    if (sk_halves(num_kv_heads) == 2) {
+    a.plan_wg = nullptr;
+    a.plan_first = nullptr;
+    a.plan_tiles = nullptr;
+    if (planned) {
+      if (sk_halves(num_kv_heads) != 2 || a.grid != plan.grid)
+        return fail(Q3A_EINVAL, "%s: plan grid %d does not match this device's %d", who, plan.grid, a.grid);
+      const PlanLayout PL = plan_layout(batch, num_kv_heads, max_pages_per_seq, page_size);
+      char* const wsb = static_cast<char*>(workspace);
+      a.plan_wg = reinterpret_cast<const int*>(wsb + PL.wg_off);
+      a.plan_first = reinterpret_cast<const int2*>(wsb + PL.first_off);
+      a.plan_tiles = reinterpret_cast<const int2*>(wsb + PL.tiles_off);
+      const dim3 block2(2 * 64 * num_kv_heads);
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_sk_kernel<true, true, 2, true>), dim3(a.grid), block2, 0, st, a);
+      else if (append)
+        hipLaunchKernelGGL((paged_decode_sk_kernel<true, false, 2, true>), dim3(a.grid), block2, 0, st, a);
+      else
+        hipLaunchKernelGGL((paged_decode_sk_kernel<false, false, 2, true>), dim3(a.grid), block2, 0, st, a);
+    } else if (sk_halves(num_kv_heads) == 2) {
       const dim3 block2(2 * 64 * num_kv_heads);
       if (rope)
         hipLaunchKernelGGL((paged_decode_sk_kernel<true, true, 2>), dim3(a.grid), block2, 0, st, a);

@@ -19,7 +19,8 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 from ._lib import LIB_PATH, Q3AttnError, lib  # noqa: F401
 from .cp_attn import (cp_attn, cp_attn_append, cp_attn_append_op, cp_attn_append_rope,  # noqa: F401
                       cp_attn_append_rope_op, cp_attn_op)
-from .ops import (DECODE_CHUNKS, DECODE_ROW, DECODE_STREAMK, flash_attn_with_kvcache, paged_decode,  # noqa: F401
+from .ops import (DECODE_CHUNKS, DECODE_PLANNED, DECODE_ROW, DECODE_STREAMK, decode_plan,  # noqa: F401
+                  flash_attn_with_kvcache, paged_decode,  # noqa: F401
                   paged_decode_append, paged_decode_append_rope)
 from .pages import PagePool, PoolExhausted  # noqa: F401
 from .prefill import (flash_attn_func, flash_attn_varlen_func, prefill, prefill_append, prefill_dense,  # noqa: F401

@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (must precede the library load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libq3attn.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -68,6 +68,12 @@ SIGNATURES = {
         _c_float, _c_int, _c_vp,                    # softmax_scale, split_tokens, stream
     ]),
     "q3a_paged_decode_workspace_bytes": (_c_size, [_c_int] * 7),
+    "q3a_paged_decode_plan_bytes": (_c_size, [_c_int] * 4),
+    "q3a_paged_decode_plan": (_c_int, [
+        _c_vp, _c_vp, _c_i64, _c_i64, _c_int,       # cache_seqlens, block_table, bt strides (row, table), num_tables
+        _c_int, _c_int, _c_int, _c_int, _c_int,     # max_pages, page_size, batch, Hkv, form
+        _c_vp, _c_i64, _c_size, _c_vp,              # plans, plan_stride, plans_bytes, stream
+    ]),
     "q3a_paged_decode_default_split": (_c_int, [_c_int] * 4),
     "q3a_cp_attn": (_c_int, [
         _c_vp, _c_i64,                                         # q, q_stride_b

@@ -10,6 +10,7 @@ the GPU only: CPU tensors raise.
 from __future__ import annotations
 
 import math
+from typing import Optional
 
 import torch
 
@@ -25,6 +26,10 @@ _MAX_SPLITS = 64
 DECODE_ROW = -1        # one workgroup per (row, KV head), one launch (tables <= 2,048 tokens)
 DECODE_CHUNKS = -2     # chunks of each row over many workgroups, then a combine (small batches of long rows)
 DECODE_STREAMK = -3    # stream-K over all rows' tiles, then a combine (batch <= 4096)
+DECODE_PLANNED = -4    # stream-K read from a per-frame plan (decode_plan); the plan is the call's workspace
+
+# Plan forms (include/q3attn.h): which entry point a plan serves.
+_PLAN_FORMS = {"plain": 0, "append": 1, "append_rope": 2}
 
 
 def _req(cond: bool, msg: str) -> None:
@@ -60,16 +65,66 @@ def _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table):
     _req(block_table.stride(1) == 1, "q3attn.paged_decode: block_table rows must be contiguous")
 
 
+def decode_plan(cache_seqlens: torch.Tensor, block_table: torch.Tensor, page_size: int, num_kv_heads: int = 8,
+                form: str = "plain"):
+    """The stream-K decomposition of the decode calls that share ``cache_seqlens`` and ``block_table``, built once
+    (one launch on the current stream) and passed to each of them as ``plan=`` (``scheduler_metadata=`` in
+    ``flash_attn_with_kvcache``).  The talker's 28 calls of a frame all take the frame's ctx and block table
+    (engine/talker.py:77, 107-112), so one plan per frame serves them all: a planned call's waves read their tile
+    lists and page ids in one memory round trip instead of scanning cache_seqlens and looking pages up in the table.
+
+    ``block_table`` is [batch, max_pages] (one plan, a uint8 tensor) or [tables, batch, max_pages] (one plan per
+    table, stacked: plan t serves table t).  ``form``: "plain" (paged_decode), "append" (paged_decode_append) or
+    "append_rope" (paged_decode_append_rope); ``cache_seqlens`` as those calls take it.  Returns None for shapes the
+    library does not decode with stream-K (small batches, narrow tables): pass the None on, the calls then take their
+    usual path.  The plan holds the lengths and table entries of the moment the plan kernel runs: build it again
+    after either changes.  Calls that share a plan must not run concurrently (each uses the buffer behind the plan
+    as scratch for its partial records); calls on one stream never do.  Build it outside a torch.compile'd region
+    (it is a host call that allocates its result), as flash-attn 3's get_scheduler_metadata is used."""
+    _req(cache_seqlens.is_cuda, "q3attn.decode_plan: tensors must be on a GPU")
+    _req(form in _PLAN_FORMS, f"q3attn.decode_plan: form must be one of {sorted(_PLAN_FORMS)}, got {form!r}")
+    _req(cache_seqlens.dtype == torch.int32 and cache_seqlens.dim() == 1 and cache_seqlens.is_contiguous(),
+         "q3attn.decode_plan: cache_seqlens must be a contiguous int32 [batch] tensor")
+    _req(block_table.device == cache_seqlens.device and block_table.dtype == torch.int32,
+         "q3attn.decode_plan: block_table must be int32 on cache_seqlens' device")
+    stacked = block_table.dim() == 3
+    bt = block_table if stacked else block_table.unsqueeze(0)
+    _req(bt.dim() == 3 and bt.shape[1] == cache_seqlens.shape[0] and bt.stride(2) == 1,
+         "q3attn.decode_plan: block_table must be [batch, max_pages] or [tables, batch, max_pages] with contiguous rows")
+    T, B, max_pages = bt.shape
+    L = lib()
+    nbytes = L.q3a_paged_decode_plan_bytes(B, int(num_kv_heads), max_pages, int(page_size))
+    if nbytes == 0 or T == 0:
+        return None
+    stride = (nbytes + 255) // 256 * 256
+    plans = torch.empty((T, stride), dtype=torch.uint8, device=cache_seqlens.device)
+    rc = L.q3a_paged_decode_plan(cache_seqlens.data_ptr(), bt.data_ptr(), bt.stride(1), bt.stride(0), T, max_pages,
+                                 int(page_size), B, int(num_kv_heads), _PLAN_FORMS[form], plans.data_ptr(), stride,
+                                 plans.numel(), _stream(cache_seqlens.device))
+    check(rc, "q3a_paged_decode_plan")
+    return plans if stacked else plans[0]
+
+
+def _plan_ws(plan, q, what):
+    """(workspace, bytes, split code) of a planned call."""
+    _req(plan.device == q.device and plan.dtype == torch.uint8 and plan.dim() == 1 and plan.is_contiguous(),
+         f"q3attn.{what}: plan must be a uint8 plan from q3attn.decode_plan on q's device")
+    return plan, plan.numel(), DECODE_PLANNED
+
+
 @torch.library.custom_op("q3attn::paged_decode", mutates_args=())
 def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                  cache_seqlens: torch.Tensor, block_table: torch.Tensor, softmax_scale: float,
-                 split_tokens: int = 0) -> torch.Tensor:
+                 split_tokens: int = 0, plan: Optional[torch.Tensor] = None) -> torch.Tensor:
     """o[b, h] = softmax(q[b, h] . K_b^T * scale) . V_b over the ctx = cache_seqlens[b] tokens of
     row b, gathered through ``block_table``; query head h reads KV head h // (Hq / Hkv).
 
     q [B, Hq, D] bf16; k_cache, v_cache [num_pages, page_size, Hkv, D] bf16; cache_seqlens [B]
     int32; block_table [B, max_pages] int32.  Returns [B, Hq, D] bf16.  fp32 semantics:
-    engine/talker.py:82-88; the call it replaces: engine/talker.py:77.
+    engine/talker.py:82-88; the call it replaces: engine/talker.py:77.  ``plan``: a decode_plan(form="plain") of
+    these cache_seqlens and block_table (the call then ignores split_tokens).  The plan buffer is also the call's
+    scratch for its partial records, which it writes and reads within the call; the plan itself is left as it was,
+    so the op is declared free of mutation and calls in one stream may share a plan.
     """
     _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table)
     B, Hq, D = q.shape
@@ -79,9 +134,12 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     if B == 0:
         return out
     L = lib()
-    split = int(split_tokens)            # 0: the library's default decomposition (stream-K)
-    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    if plan is not None:
+        ws, ws_bytes, split = _plan_ws(plan, q, "paged_decode")
+    else:
+        split = int(split_tokens)            # 0: the library's default decomposition (stream-K)
+        ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
     rc = L.q3a_paged_decode(
         q.data_ptr(), q.stride(0), q.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
@@ -95,7 +153,7 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
 
 
 @paged_decode.register_fake
-def _paged_decode_fake(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, split_tokens=0):
+def _paged_decode_fake(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, split_tokens=0, plan=None):
     return q.new_empty(q.shape)
 
 
@@ -116,10 +174,12 @@ def _new_rows(x, B, Hkv, D, name):
 @torch.library.custom_op("q3attn::paged_decode_append", mutates_args=("k_cache", "v_cache"))
 def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
                         v_cache: torch.Tensor, cache_seqlens: torch.Tensor, block_table: torch.Tensor,
-                        softmax_scale: float, split_tokens: int = 0) -> torch.Tensor:
+                        softmax_scale: float, split_tokens: int = 0,
+                        plan: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Append + attend in one pass: writes k[b], v[b] at position p = cache_seqlens[b] of row b (page
     block_table[b][p // page], offset p % page) and returns the attention of q[b] over tokens 0..p
-    (engine/talker.py:72-73 then :77).  Rows with cache_seqlens < 0 give zeros and write nothing."""
+    (engine/talker.py:72-73 then :77).  Rows with cache_seqlens < 0 give zeros and write nothing.  ``plan``: a
+    decode_plan(form="append") of these cache_seqlens and block_table."""
     _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table)
     B, Hq, D = q.shape
     num_pages, page, Hkv, _ = k_cache.shape
@@ -131,9 +191,12 @@ def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cac
     if B == 0:
         return out
     L = lib()
-    split = int(split_tokens)
-    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    if plan is not None:
+        ws, ws_bytes, split = _plan_ws(plan, q, "paged_decode_append")
+    else:
+        split = int(split_tokens)
+        ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
     rc = L.q3a_paged_decode_append(
         q.data_ptr(), q.stride(0), q.stride(1),
         k3.data_ptr(), k3.stride(0), v3.data_ptr(), v3.stride(0),
@@ -149,7 +212,7 @@ def paged_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cac
 
 @paged_decode_append.register_fake
 def _paged_decode_append_fake(q, k, v, k_cache, v_cache, cache_seqlens, block_table, softmax_scale,
-                              split_tokens=0):
+                              split_tokens=0, plan=None):
     return q.new_empty(q.shape)
 
 
@@ -171,12 +234,14 @@ def _rope_rows(x: torch.Tensor, B: int, D: int, dev, name: str) -> torch.Tensor:
 def paged_decode_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
                              k_norm_w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
                              v_cache: torch.Tensor, cache_seqlens: torch.Tensor, block_table: torch.Tensor,
-                             softmax_scale: float, eps: float = 1e-6, split_tokens: int = 0) -> torch.Tensor:
+                             softmax_scale: float, eps: float = 1e-6, split_tokens: int = 0,
+                             plan: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The talker's per-layer attention block in one launch (engine/talker.py:69-77): q and k arrive as the raw
     projections (views of the qkv output), are RMS-normalised with q_norm_w / k_norm_w and rotated with each row's
     cos/sin (engine/ops.py:51-60), k and v are written at position p = cache_seqlens[b] of row b, and the attention of
     q[b] over tokens 0..p is returned, as paged_decode_append does for already-normalised q and k.  split_tokens: 0
-    (the library's choice) or one of the DECODE_* codes; fixed splits do not take this form."""
+    (the library's choice) or one of the DECODE_* codes; fixed splits do not take this form.  ``plan``: a
+    decode_plan(form="append_rope") of these cache_seqlens and block_table."""
     _check_decode_inputs(q, k_cache, v_cache, cache_seqlens, block_table)
     B, Hq, D = q.shape
     num_pages, page, Hkv, _ = k_cache.shape
@@ -196,9 +261,12 @@ def paged_decode_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     if B == 0:
         return out
     L = lib()
-    split = int(split_tokens)
-    ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    if plan is not None:
+        ws, ws_bytes, split = _plan_ws(plan, q, "paged_decode_append_rope")
+    else:
+        split = int(split_tokens)
+        ws_bytes = L.q3a_paged_decode_workspace_bytes(B, Hq, Hkv, D, max_pages, page, split)
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     rc = L.q3a_paged_decode_append_rope(
         q.data_ptr(), q.stride(0), q.stride(1),
         k3.data_ptr(), k3.stride(0), v3.data_ptr(), v3.stride(0),
@@ -215,7 +283,7 @@ def paged_decode_append_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
 
 @paged_decode_append_rope.register_fake
 def _paged_decode_append_rope_fake(q, k, v, q_norm_w, k_norm_w, cos, sin, k_cache, v_cache, cache_seqlens,
-                                   block_table, softmax_scale, eps=1e-6, split_tokens=0):
+                                   block_table, softmax_scale, eps=1e-6, split_tokens=0, plan=None):
     return q.new_empty(q.shape)
 
 
@@ -223,7 +291,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
                             cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None,
                             block_table=None, softmax_scale=None, causal=False, window_size=(-1, -1),
                             softcap=0.0, rotary_interleaved=True, alibi_slopes=None, num_splits=0,
-                            return_softmax_lse=False):
+                            return_softmax_lse=False, scheduler_metadata=None):
     """Drop-in for the paged-decode subset of ``flash_attn.flash_attn_with_kvcache`` that the talker
     calls (engine/talker.py:77): q [B, 1, Hq, D], paged caches, int32 ``cache_seqlens`` and
     ``block_table``, ``softmax_scale``, ``causal`` (a no-op for one query token).  Returns
@@ -232,8 +300,9 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
     With ``k``/``v`` ([B, 1, Hkv, D], one new token per row) the flash-attn append semantics apply:
     the new token is written into the caches at position ``cache_seqlens[b]`` and attention runs over
     ``cache_seqlens[b] + 1`` tokens, in one pass (replacing engine/talker.py:72-73 + :77);
-    ``cache_seqlens`` itself is not updated.  Arguments the talker does not use raise
-    NotImplementedError."""
+    ``cache_seqlens`` itself is not updated.  ``scheduler_metadata``: a plan from q3attn.decode_plan for these
+    cache_seqlens and block_table (form "append" with k/v, else "plain"), built once for the calls that share them;
+    None decodes without one.  Arguments the talker does not use raise NotImplementedError."""
     _req((k is None) == (v is None), "q3attn.flash_attn_with_kvcache: pass both k and v, or neither")
     unsupported = {"rotary_cos": rotary_cos, "rotary_sin": rotary_sin,
                    "cache_batch_idx": cache_batch_idx, "cache_leftpad": cache_leftpad,
@@ -265,7 +334,8 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
         if k.shape[1] != 1 or v.shape[1] != 1:
             raise NotImplementedError("q3attn.flash_attn_with_kvcache: one new token per row is supported")
         o = paged_decode_append(q[:, 0], k[:, 0], v[:, 0], k_cache, v_cache, cache_seqlens, block_table,
-                                float(scale), split)
+                                float(scale), split, scheduler_metadata)
     else:
-        o = paged_decode(q[:, 0], k_cache, v_cache, cache_seqlens, block_table, float(scale), split)
+        o = paged_decode(q[:, 0], k_cache, v_cache, cache_seqlens, block_table, float(scale), split,
+                         scheduler_metadata)
     return o.unsqueeze(1)

@@ -60,7 +60,8 @@ def _decode(**kw):
     (dict(ws_bytes=10, max_pages=16, B=65), "workspace"),  # 65 rows of a 256-token table: stream-K, with workspace
     (dict(ws_bytes=10, max_pages=16, B=4), "workspace"),   # 4 rows of a 256-token table: chunks, with workspace
     (dict(B=-1), "batch"),
-    (dict(split=-4), "split_tokens"),                      # not a path code
+    (dict(split=-5), "split_tokens"),                      # not a path code
+    (dict(split=-4, B=65, max_pages=16), "not a decode plan"),  # planned, with a workspace no plan was built in
     (dict(split=-1, max_pages=129), "decode path"),        # the row kernel takes tables of at most 2,048 tokens
     (dict(split=-3, B=4097), "decode path"),               # stream-K takes at most 4,096 rows
     (dict(split=-2, max_pages=8193), "decode path"),       # chunks: at most 64 tiles per wave
@@ -114,6 +115,45 @@ def test_workspace_of_the_decode_paths():
     assert ws(4, 15, 0) == 0                                      # 240-token tables: the row-parallel kernel
     assert ws(4, 128, -3) > 0 and ws(4, 128, -3) != ws(4, 128, 0)  # forced stream-K
     assert ws(4, 129, -1) == 0                                    # a code that does not take the shape: nothing
+
+
+def _plan(**kw):
+    a = dict(seqlens=256, bt=256, bt_sb=16, bt_st=65 * 16, tables=1, max_pages=16, page=16, B=65, Hkv=8,
+             form=0, plans=256, stride=1 << 24, plans_bytes=1 << 30)
+    a.update(kw)
+    return _lib.lib().q3a_paged_decode_plan(a["seqlens"], a["bt"], a["bt_sb"], a["bt_st"], a["tables"],
+                                            a["max_pages"], a["page"], a["B"], a["Hkv"], a["form"], a["plans"],
+                                            a["stride"], a["plans_bytes"], None)
+
+
+@pytest.mark.parametrize("kw,frag", [
+    (dict(form=3), "form"), (dict(form=-1), "form"), (dict(seqlens=None), "null"), (dict(plans=None), "null"),
+    (dict(tables=0), "num_tables"), (dict(plans=264), "256-byte"), (dict(tables=2, stride=1000), "256-byte"),
+    (dict(tables=2, stride=256), "256-byte"), (dict(plans_bytes=100), "bytes"),
+    (dict(bt_sb=8), "overlap"), (dict(tables=2, bt_st=16), "overlap"),
+    (dict(B=8), "no plan"),                  # 8 rows of a 256-token table: the chunked kernel, no plan
+    (dict(B=65, max_pages=8), "no plan"),    # 128-token tables: the row-parallel kernel
+    (dict(Hkv=4), "no plan"), (dict(B=4097), "no plan"), (dict(page=24), "no plan"), (dict(page=8192), "no plan"),
+])
+def test_decode_plan_rejects_bad_arguments(kw, frag):
+    rc = _plan(**kw)
+    assert rc < 0
+    assert frag in _lib.lib().q3a_last_error().decode()
+
+
+def test_decode_plan_bytes_follow_the_library_choice():
+    """Plans exist exactly for the shapes the library decodes with stream-K; a plan is a stream-K workspace (prefix
+    sums, slot pages, partial records of the grid the call launches) plus the ranges, the first tile lists and 8 B
+    per tile of the table capacity."""
+    L = _lib.lib()
+    pb = lambda B, pages, page=16, hkv=8: L.q3a_paged_decode_plan_bytes(B, hkv, pages, page)
+    assert pb(8, 16) == 0 and pb(16, 129) == 0        # chunks
+    assert pb(64, 128) == 0 and pb(4096, 8) == 0       # row-parallel
+    assert pb(4097, 16) == 0 and pb(576, 129, hkv=4) == 0
+    for B, pages in ((65, 16), (17, 129), (576, 129), (4096, 64)):
+        assert pb(B, pages) >= 4 * (2 * B + 1) + B * pages * 8, (B, pages)
+        assert pb(B, pages) % 256 == 0
+    assert pb(576, 258, page=8 * 16) == pb(576, 258 * 8)  # only the capacity in tokens matters
 
 
 @pytest.mark.parametrize("kw,frag", [
