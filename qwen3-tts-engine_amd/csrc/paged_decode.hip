@@ -82,6 +82,8 @@ struct DecodeArgs {
   const int* plan_wg;
   const int2* plan_first;
   const int2* plan_tiles;
+  const int4* plan_cut;  // the planned combine: cut-row descriptors (row, pieces, overflow base, 0)
+  int plan_rec_cap;
   int batch, hkv, split_tokens, max_splits, grid;
   int row_per;          // row-parallel path: tiles per wave of the table capacity (the host picks the kernel)
   float scale_log2;
@@ -441,6 +443,34 @@ __device__ __forceinline__ void write_partial(float* P, int lane, int grp, int d
     st16(P + kPartML, __builtin_bit_cast(uint4, make_float4(m[0], m[1], wide ? -l[0] : l[0], wide ? -l[1] : l[1])));
 }
 
+// Folds a group of up to 8 records (unused entries: m = kMaxSeed, l = 0) into the running (M, L, A): one rescale to
+// the group's max, then each record's weight |l| 2^(m - M) (a negative l flags bf16 o values, else fp16).
+__device__ __forceinline__ void merge_fold8(const uint2 (&raw)[8], const float (&mr)[8], const float (&lr)[8],
+                                            float& M, float& L, float4& A) {
+  float mc = M;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) mc = fmaxf(mc, mr[u]);
+  const float alpha = fast_exp2(M - mc);
+  L *= alpha;
+  A.x *= alpha;
+  A.y *= alpha;
+  A.z *= alpha;
+  A.w *= alpha;
+  M = mc;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const bool wide = __builtin_signbit(lr[u]);
+    const float w = fabsf(lr[u]) * fast_exp2(mr[u] - M);
+    const float4 v = wide ? make_float4(bf16_lo(raw[u].x), bf16_hi(raw[u].x), bf16_lo(raw[u].y), bf16_hi(raw[u].y))
+                          : make_float4(f16_lo(raw[u].x), f16_hi(raw[u].x), f16_lo(raw[u].y), f16_hi(raw[u].y));
+    L += w;
+    A.x = fmaf(v.x, w, A.x);
+    A.y = fmaf(v.y, w, A.y);
+    A.z = fmaf(v.z, w, A.z);
+    A.w = fmaf(v.w, w, A.w);
+  }
+}
+
 // Merges `count` partial records (rec(i) -> record i) of one (row, KV head) into the output row.
 // The whole wave participates; lane l owns query head l/32 and dims 4*(l%32)..+4.  Each lane reads every
 // record's (m, l) of its head itself (the 32 lanes of a head read the same words), so the merge needs no
@@ -468,28 +498,7 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int b, int g,
         lr[u] = P[kPartML + kG + h];
       }
     }
-    float mc = M;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) mc = fmaxf(mc, mr[u]);
-    const float alpha = fast_exp2(M - mc);
-    L *= alpha;
-    A.x *= alpha;
-    A.y *= alpha;
-    A.z *= alpha;
-    A.w *= alpha;
-    M = mc;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const bool wide = __builtin_signbit(lr[u]);
-      const float w = fabsf(lr[u]) * fast_exp2(mr[u] - M);
-      const float4 v = wide ? make_float4(bf16_lo(raw[u].x), bf16_hi(raw[u].x), bf16_lo(raw[u].y), bf16_hi(raw[u].y))
-                            : make_float4(f16_lo(raw[u].x), f16_hi(raw[u].x), f16_lo(raw[u].y), f16_hi(raw[u].y));
-      L += w;
-      A.x = fmaf(v.x, w, A.x);
-      A.y = fmaf(v.y, w, A.y);
-      A.z = fmaf(v.z, w, A.z);
-      A.w = fmaf(v.w, w, A.w);
-    }
+    merge_fold8(raw, mr, lr, M, L, A);
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   // Non-temporal: with the slot stores below, 200.5 -> 198.9 us per append call at 576 rows (the plain form
@@ -599,11 +608,14 @@ __device__ __forceinline__ int sk_tile_scan(const DecodeArgs& a, int* s_ctx, int
 // The 28 decode calls of a talker frame share cache_seqlens (and, in the engine, the block table), so the stream-K
 // partition, each wave's tile list and the tiles' page ids can be computed once per frame and read by every call:
 // a planned call's waves load their first tile list (page ids included) in one round trip, where the unplanned
-// prologue waits for cache_seqlens, a block-wide scan, row searches in LDS and then the table.
+// prologue waits for cache_seqlens, a block-wide scan, row searches in LDS and then the table.  The plan also says
+// where each partial record goes: the records of the c-th cut row (a row whose tiles span several workgroups) start
+// at positions 2c and 2c + 1 (its first two pieces; every cut row has at least two), further pieces at an overflow
+// position, so the planned combine loads a cut row's first two records beside its descriptor, one round trip.
 //
 // A tile's entry (int2): x = its page id (as the table holds it), y = row | (offset in page / 16) << 13 |
 // valid tokens << 21 | segment flags << 26, with the flags of the wave range that holds the tile.
-constexpr int kPlanWgInts = 8;  // per decode workgroup: lo, hi, mid, mid_row, mid_whole, mid_from_lo, 0, 0
+constexpr int kPlanWgInts = 8;  // per decode workgroup: lo, hi, mid, mid_row, mid_whole, mid_from_lo, rec0, rec1
 constexpr int kPlanRowBits = 13;
 constexpr int kPlanOffBits = 8;
 
@@ -612,37 +624,69 @@ __device__ __forceinline__ int plan_pack(int row, int off_tiles, int nvalid, int
          (flags << (kPlanRowBits + kPlanOffBits + 5));
 }
 
-// One launch per frame: grid (x, tables), 1,024 threads.  Every workgroup scans the rows itself (at most 4,096
-// ints); workgroup (0, t) writes table t's prefix sums (the combine kernel's input), and the tiles and decode
-// workgroups are spread over x.  Plan t lives at plans + t * plan_stride with the layout of the host's plan_layout.
+// Record position of piece j of the cut row with index c (ob: its overflow base) among rec_cap cut-row slots.
+__device__ __forceinline__ int plan_rec_pos(int c, int j, int ob, int rec_cap) {
+  return j < 2 ? 2 * c + j : 2 * rec_cap + ob + (j - 2);
+}
+
+// Plan t lives at plans + t * plan_stride with the layout of the host's plan_layout.
 struct PlanArgs {
   char* plans;
   int64_t plan_stride;
   int64_t bt_stable;  // element stride between the tables
-  int64_t wg_off, first_off, tiles_off;  // byte offsets inside one plan
+  int64_t wg_off, cut_off, first_off, tiles_off;  // byte offsets inside one plan
+  int num_tables;
   int halves;
+  int rec_cap;        // cut-row descriptors (and pairs of leading record slots) per plan: the decode grid
 };
 
+// One launch per frame, 256 threads per workgroup.  Every workgroup scans the rows itself (at most 4,096 ints); the
+// tiles, the decode workgroups and the cut rows are spread over the grid.  A tile's thread writes it into every
+// table's plan (only the page ids differ between the tables).
 template <bool kAppend>
-__global__ __launch_bounds__(1024) void paged_decode_plan_kernel(const DecodeArgs a, const PlanArgs p) {
+__global__ __launch_bounds__(256) void paged_decode_plan_kernel(const DecodeArgs a, const PlanArgs p) {
   __shared__ int s_ctx[kSkMaxRows];
   __shared__ int s_prefix[kSkMaxRows + 1];
+  __shared__ int s_cut[kSkMaxRows + 1];  // per row: cut rows before it | overflow records before it << 16
   __shared__ int s_wsum[16];
   const int NT = sk_tile_scan<kAppend>(a, s_ctx, s_prefix, s_wsum);
   const int ge = sk_effective_grid(a.grid, NT);
   const int B = a.batch;
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
-  const int64_t tbl = blockIdx.y;
-  const int32_t* bt = a.bt + tbl * p.bt_stable;
-  char* base = p.plans + tbl * p.plan_stride;
-  int* wg = reinterpret_cast<int*>(base + p.wg_off);
-  int2* first = reinterpret_cast<int2*>(base + p.first_off);
-  int2* tiles = reinterpret_cast<int2*>(base + p.tiles_off);
-  if (blockIdx.x == 0) {
-    int* prefix = reinterpret_cast<int*>(base);
-    for (int r = tid; r <= B; r += nthr) prefix[r] = s_prefix[r];
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  // The workgroups holding a row's first and last tile: kf = ((p0 + 1) ge - 1) / NT, kl = (p1 ge - 1) / NT.
+  auto wg_of = [&](int t) { return (int)udiv_fit((uint64_t)(t + 1) * (uint64_t)ge - 1, (uint32_t)NT); };
+  auto row_cut = [&](int r, int& kf, int& nseg) {
+    const int p0 = s_prefix[r], p1 = s_prefix[r + 1];
+    kf = p1 > p0 ? wg_of(p0) : 0;
+    nseg = p1 > p0 ? wg_of(p1 - 1) - kf + 1 : 0;
+    return nseg > 1;
+  };
+  // Second scan: cut rows (low 16 bits) and overflow pieces (high 16 bits) before each row.
+  {
+    const int per = (B + nthr - 1) / nthr;
+    const int r0 = min(B, tid * per), r1 = min(B, r0 + per);
+    int sum = 0;
+    for (int r = r0; r < r1; ++r) {
+      int kf, nseg;
+      if (row_cut(r, kf, nseg)) sum += 1 + ((nseg - 2) << 16);
+    }
+    const int x = wave_scan_incl(sum);
+    if (lane == 63) s_wsum[wv] = x;  // (sk_tile_scan's last reads of s_wsum precede its closing barrier)
+    __syncthreads();
+    const int wt = wave_scan_incl(lane < (nthr >> 6) ? s_wsum[lane] : 0);
+    int run = (wv == 0 ? 0 : __builtin_amdgcn_readlane(wt, wv - 1)) + x - sum;
+    for (int r = r0; r < r1; ++r) {
+      s_cut[r] = run;
+      int kf, nseg;
+      if (row_cut(r, kf, nseg)) run += 1 + ((nseg - 2) << 16);
+    }
+    if (tid == nthr - 1) s_cut[B] = run;
+    __syncthreads();
   }
+  const int ncut = s_cut[B] & 0xFFFF;
   // The largest row r with s_prefix[r] <= t (t < NT; an empty row shares its successor's prefix).
   auto row_of = [&](int t) {
     int lo = 0, hi = B;
@@ -652,11 +696,19 @@ __global__ __launch_bounds__(1024) void paged_decode_plan_kernel(const DecodeArg
     }
     return lo;
   };
+  auto rec_of = [&](int r, int j) {
+    const int c = s_cut[r];
+    return plan_rec_pos(c & 0xFFFF, j, c >> 16, p.rec_cap);
+  };
   const int stride = gridDim.x * nthr;
-  // Decode workgroup ranges, exactly as the unplanned kernel computes them; workgroups past the effective grid get
-  // an empty range and exit.
-  for (int w = blockIdx.x * nthr + tid; w < a.grid; w += stride) {
-    int v[kPlanWgInts] = {0, 0, 0, -1, 0, 0, 0, 0};
+  // The three kinds of items start on different workgroups (tiles from the first, workgroup ranges from the last,
+  // cut rows from the middle), so that no workgroup's chain holds two kinds; the last two have one item per table.
+  const int gx = gridDim.x;
+  // Decode workgroup ranges, exactly as the unplanned kernel computes them, and where its two records go; workgroups
+  // past the effective grid get an empty range and exit.
+  for (int it = (gx - 1 - (int)blockIdx.x) * nthr + tid; it < a.grid * p.num_tables; it += stride) {
+    const int w = it % a.grid, tb = it / a.grid;
+    int v[kPlanWgInts] = {0, 0, 0, -1, 0, 0, -1, -1};
     if (w < ge) {
       const int lo_w = (int)sk_lo(w, NT, ge), hi_w = (int)sk_lo(w + 1, NT, ge);
       const int mid = p.halves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
@@ -673,14 +725,40 @@ __global__ __launch_bounds__(1024) void paged_decode_plan_kernel(const DecodeArg
         v[4] = s_prefix[mid_row] >= lo_w && s_prefix[mid_row + 1] <= hi_w;
         v[5] = s_prefix[mid_row] <= lo_w;
       }
+      int kf, nseg;
+      // Slot 0: the row holding the range's first tile, when cut (piece w - kf); slot 1: the row holding its last
+      // tile, when cut and starting after the first tile (its first piece).
+      const int r0 = row_of(lo_w);
+      if (row_cut(r0, kf, nseg)) v[6] = rec_of(r0, w - kf);
+      const int r1 = row_of(hi_w - 1);
+      if (s_prefix[r1] > lo_w && row_cut(r1, kf, nseg)) v[7] = rec_of(r1, 0);
     }
-    int4* d = reinterpret_cast<int4*>(wg + (int64_t)w * kPlanWgInts);
+    int4* d = reinterpret_cast<int4*>(p.plans + tb * p.plan_stride + p.wg_off) + 2 * (int64_t)w;
     d[0] = make_int4(v[0], v[1], v[2], v[3]);
     d[1] = make_int4(v[4], v[5], v[6], v[7]);
   }
-  // Tiles: the workgroup that holds tile t is the largest k with sk_lo(k) <= t, i.e. ((t + 1) ge - 1) / NT.
+  // Cut-row descriptors (row, pieces, overflow base, 0), in row order; the slots past the last cut row get row -1.
+  const int ncr = B + p.rec_cap;
+  for (int it = (((int)blockIdx.x + gx / 2) % gx) * nthr + tid; it < ncr * p.num_tables; it += stride) {
+    const int r = it % ncr, tb = it / ncr;
+    int4 e;
+    int idx;
+    if (r < B) {
+      int kf, nseg;
+      if (!row_cut(r, kf, nseg)) continue;
+      idx = s_cut[r] & 0xFFFF;
+      e = make_int4(r, nseg, s_cut[r] >> 16, 0);
+    } else {
+      idx = ncut + (r - B);
+      if (idx >= p.rec_cap) continue;
+      e = make_int4(-1, 0, 0, 0);
+    }
+    reinterpret_cast<int4*>(p.plans + tb * p.plan_stride + p.cut_off)[idx] = e;
+  }
+  // Tiles: the workgroup that holds tile t is wg_of(t).  A tile among the first 64 of its wave's range goes into the
+  // wave's first list, a later one into the per-tile entries.
   for (int t = blockIdx.x * nthr + tid; t < NT; t += stride) {
-    const int k = (int)udiv_fit((uint64_t)(t + 1) * (uint64_t)ge - 1, (uint32_t)NT);
+    const int k = wg_of(t);
     const int lo_w = (int)sk_lo(k, NT, ge), hi_w = (int)sk_lo(k + 1, NT, ge);
     const int mid = p.halves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
     const int half = t >= mid ? 1 : 0;
@@ -690,14 +768,26 @@ __global__ __launch_bounds__(1024) void paged_decode_plan_kernel(const DecodeArg
     const int ntr = s_prefix[row + 1] - s_prefix[row];
     const int tok = mt * kTile;
     const int pidx = tok / a.page_size;
-    const int page = bt[(int64_t)row * a.bt_sb + pidx];
     const int off = tok - pidx * a.page_size;
     const int nvalid = min(kTile, s_ctx[row] - tok);
     const int flags = ((mt == 0 || t == lo) ? kFirst : 0) | ((mt == ntr - 1 || t == hi - 1) ? kLast : 0) |
                       (mt == 0 ? kRowStart : 0) | (mt == ntr - 1 ? kRowEnd : 0);
-    const int2 e = make_int2(page, plan_pack(row, off / kTile, nvalid, flags));
-    tiles[t] = e;
-    if (t - lo < 64) first[((int64_t)k * p.halves + half) * 64 + (t - lo)] = e;
+    const int y = plan_pack(row, off / kTile, nvalid, flags);
+    const int32_t* bt = a.bt + (int64_t)row * a.bt_sb + pidx;
+    const int64_t dst = t - lo < 64 ? p.first_off + (((int64_t)k * p.halves + half) * 64 + (t - lo)) * 8
+                                    : p.tiles_off + (int64_t)t * 8;
+    // All tables' page ids of a pass are loaded before the first store (the compiler cannot move a load above a
+    // store that may alias it), unconditionally (a table index past the last reads the last table again: a load
+    // under a branch would be waited for at the branch's end): one round trip per 32 tables instead of one per table.
+    for (int tb0 = 0; tb0 < p.num_tables; tb0 += 32) {
+      int pg[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) pg[u] = bt[(int64_t)min(tb0 + u, p.num_tables - 1) * p.bt_stable];
+#pragma unroll
+      for (int u = 0; u < 32; ++u)
+        if (tb0 + u < p.num_tables)
+          *reinterpret_cast<int2*>(p.plans + (tb0 + u) * p.plan_stride + dst) = make_int2(pg[u], y);
+    }
   }
 }
 
@@ -809,6 +899,16 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
 
   const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + dl) * 2);
   float* part = a.ws + (int64_t)blockIdx.x * kSkSlots * a.hkv * kPartFloats;
+  // This KV head's record of slot s (0: the piece opened at the range's first tile, 1: the piece cut at its end).
+  // A planned call writes it where the plan puts it (the planned combine finds a cut row's records by the row's
+  // index among the cut rows); the plan marks a slot the workgroup does not fill with -1.
+  auto rec_ptr = [&](int slot) -> float* {
+    if constexpr (kPlan) {
+      const int pos = pwg[6 + slot];
+      return pos >= 0 ? a.ws + ((int64_t)pos * a.hkv + g) * kPartFloats : nullptr;
+    }
+    return part + (slot * a.hkv + g) * kPartFloats;
+  };
 
   uint8_t* const st0 = s_stage0 + wv * kSt;
   uint8_t* const st1 = s_stage1 + wv * kSt;
@@ -945,8 +1045,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
           if (seg_slot == 0) {
             write_partial(&s_first[wv][0], lane, grp, dl, m, l, acc);
             first_deferred = true;
-          } else {
-            write_partial(part + (a.hkv + g) * kPartFloats, lane, grp, dl, m, l, acc);
+          } else if (float* const P = rec_ptr(1)) {
+            write_partial(P, lane, grp, dl, m, l, acc);
           }
         }
       }
@@ -1018,7 +1118,9 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       prep(j + 2, st0);
     }
   }
-  if (first_deferred && lane < kPartFloats / 4) st16(part + g * kPartFloats + lane * 4, ld16(&s_first[wv][lane * 4]));
+  if (first_deferred && lane < kPartFloats / 4) {
+    if (float* const P = rec_ptr(0)) st16(P + lane * 4, ld16(&s_first[wv][lane * 4]));
+  }
   if constexpr (kStageOut) {
     if (grp == 0) {
       for (int i = 0; i < n_out; ++i) {
@@ -1063,8 +1165,8 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
       const bool from_lo = kPlan ? pwg[5] != 0 : s_prefix[mid_row] <= lo_w;
       if (kPlan ? pwg[4] != 0 : (s_prefix[mid_row] >= lo_w && s_prefix[mid_row + 1] <= hi_w))
         write_output(a, mid_row, g, grp, dl, l, acc);
-      else
-        write_partial(part + ((from_lo ? 0 : 1) * a.hkv + g) * kPartFloats, lane, grp, dl, m, l, acc);
+      else if (float* const P = rec_ptr(from_lo ? 0 : 1))
+        write_partial(P, lane, grp, dl, m, l, acc);
     }
   }
 }
@@ -1130,6 +1232,83 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const Dec
     });
   }
   store_slot();
+}
+
+// Planned calls: one workgroup per row (zero rows, and in the append forms the new rows' slot stores, as in the
+// combine above) and then one per possible cut row.  A cut row's first two records sit at positions 2c and 2c + 1
+// (c: its index among the cut rows), so they are loaded beside its descriptor, before the row is known: the merge
+// waits for one memory round trip (a second only for rows cut into more than two pieces), where the unplanned
+// combine first loads the prefix sums and then the records.  The merge itself is merge_records' arithmetic over the
+// same records in the same order, so the output equals the unplanned call's bit for bit.
+template <bool kAppend, bool kRope = false>
+__global__ __launch_bounds__(1024) void paged_decode_plan_combine_kernel(const DecodeArgs a) {
+  const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
+  const int lane = threadIdx.x & 63;
+  if ((int)blockIdx.x < a.batch) {
+    const int b = blockIdx.x;
+    const int cap = a.max_pages * a.page_size;
+    const int c = a.seqlens[b];
+    if constexpr (kAppend) {
+      uint32_t kw = reinterpret_cast<const uint32_t*>(a.k_new + (int64_t)b * a.kn_sb + g * kD)[lane];
+      const uint32_t vw = reinterpret_cast<const uint32_t*>(a.v_new + (int64_t)b * a.vn_sb + g * kD)[lane];
+      if constexpr (kRope)
+        kw = qk_norm_rope64(kw, reinterpret_cast<const uint32_t*>(a.kn_w)[lane],
+                            reinterpret_cast<const uint32_t*>(a.rcos + (int64_t)b * a.rs_sb)[lane],
+                            reinterpret_cast<const uint32_t*>(a.rsin + (int64_t)b * a.rs_sb)[lane], a.eps);
+      if (c < 0 || c >= cap) {
+        write_zero_row(a, b, g, lane);
+        return;
+      }
+      const int page = a.slot_page[b];
+      if ((unsigned)page < (unsigned)a.num_pages) {
+        const int pidx = c / a.page_size;
+        const int64_t dst = (int64_t)page * a.kv_sp + (int64_t)(c - pidx * a.page_size) * a.kv_st + (int64_t)g * a.kv_sh;
+        __builtin_nontemporal_store(kw, reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.kc) + dst) + lane);
+        __builtin_nontemporal_store(vw, reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.vc) + dst) + lane);
+      }
+    } else {
+      if (ctx_of<false>(c, cap) == 0) write_zero_row(a, b, g, lane);
+    }
+    return;
+  }
+  const int ci = blockIdx.x - a.batch;
+  const int4 d = a.plan_cut[ci];
+  const int h = lane >> 5;
+  const int d0 = (lane & 31) * 4;
+  uint2 raw[8];
+  float mr[8], lr[8];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const float* P = a.ws + ((int64_t)(2 * ci + u) * a.hkv + g) * kPartFloats;
+    raw[u] = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(P) + (h * kD + d0) * 2);
+    mr[u] = P[kPartML + h];
+    lr[u] = P[kPartML + kG + h];
+  }
+  const int b = d.x, count = d.y, ob = d.z;
+  if (b < 0) return;
+  float M = kMaxSeed, L = 0.f;
+  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < count; s0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s0 == 0 && u < 2) continue;  // loaded above
+      raw[u] = make_uint2(0u, 0u);
+      mr[u] = kMaxSeed;
+      lr[u] = 0.f;
+      if (s0 + u < count) {
+        const float* P = a.ws + ((int64_t)plan_rec_pos(ci, s0 + u, ob, a.plan_rec_cap) * a.hkv + g) * kPartFloats;
+        raw[u] = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(P) + (h * kD + d0) * 2);
+        mr[u] = P[kPartML + h];
+        lr[u] = P[kPartML + kG + h];
+      }
+    }
+    merge_fold8(raw, mr, lr, M, L, A);
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  u32x2 o;
+  o.x = pack_bf16x2(A.x * inv, A.y * inv);
+  o.y = pack_bf16x2(A.z * inv, A.w * inv);
+  __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(a.out + b * a.o_sb + (kG * g + h) * a.o_sh + d0));
 }
 
 // ------------------------------------------------------------------------------ fixed-split path
@@ -1598,21 +1777,25 @@ size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int spl
   return (size_t)batch * max_splits * hkv * kPartFloats * sizeof(float);
 }
 
-// Planned stream-K calls.  A plan is a stream-K workspace (prefix sums, slot pages, partial records) followed by the
-// plan proper: the decode workgroups' ranges, each wave's first tile list, and an entry for every tile.
+// Planned stream-K calls.  A plan holds the call's scratch (the new tokens' slot pages, the partial records: two
+// leading slots per possible cut row and as many overflow slots) and the plan proper: the decode workgroups' ranges
+// and record positions, the cut-row descriptors, each wave's first tile list, and entries for the tiles past them.
+// At most grid - 1 rows are cut (each crosses a range boundary), and the records number at most 2 per workgroup.
 struct PlanLayout {
-  size_t slot_off, rec_off, wg_off, first_off, tiles_off, bytes;
+  int grid;
+  size_t slot_off, rec_off, wg_off, cut_off, first_off, tiles_off, bytes;
 };
 
 PlanLayout plan_layout(int batch, int hkv, int max_pages, int page_size) {
   const int64_t cap_tiles = ((int64_t)max_pages * page_size + kTile - 1) / kTile;
-  const int grid = sk_effective_grid_host(sk_grid(hkv), (int64_t)batch * cap_tiles);
   PlanLayout L;
-  L.slot_off = align256((size_t)(batch + 1) * sizeof(int));
+  L.grid = sk_effective_grid_host(sk_grid(hkv), (int64_t)batch * cap_tiles);
+  L.slot_off = 0;
   L.rec_off = L.slot_off + align256((size_t)batch * sizeof(int));
-  L.wg_off = L.rec_off + align256((size_t)grid * kSkSlots * hkv * kPartFloats * sizeof(float));
-  L.first_off = L.wg_off + align256((size_t)grid * kPlanWgInts * sizeof(int));
-  L.tiles_off = L.first_off + align256((size_t)grid * sk_halves(hkv) * 64 * sizeof(int2));
+  L.wg_off = L.rec_off + align256((size_t)4 * L.grid * hkv * kPartFloats * sizeof(float));
+  L.cut_off = L.wg_off + align256((size_t)L.grid * kPlanWgInts * sizeof(int));
+  L.first_off = L.cut_off + align256((size_t)L.grid * sizeof(int4));
+  L.tiles_off = L.first_off + align256((size_t)L.grid * sk_halves(hkv) * 64 * sizeof(int2));
   L.bytes = L.tiles_off + align256((size_t)batch * cap_tiles * sizeof(int2));
   return L;
 }
@@ -1693,16 +1876,23 @@ extern "C" int q3a_paged_decode_plan(const int32_t* cache_seqlens, const int32_t
   p.plan_stride = plan_stride;
   p.bt_stable = bt_stride_table;
   p.wg_off = (int64_t)L.wg_off;
+  p.cut_off = (int64_t)L.cut_off;
   p.first_off = (int64_t)L.first_off;
   p.tiles_off = (int64_t)L.tiles_off;
+  p.num_tables = num_tables;
   p.halves = sk_halves(num_kv_heads);
-  const int64_t work = std::max<int64_t>((int64_t)batch * cap_tiles, a.grid);
-  const int gx = (int)std::min<int64_t>(16, std::max<int64_t>(1, (work + 4095) / 4096));
+  p.rec_cap = L.grid;
+  // One thread per tile of the table capacity (at most 64 workgroups; each scans the rows itself).
+  // Workgroups of 256 threads, one thread per tile of the table capacity, at most 256 of them (each scans the rows
+  // itself): the page-id loads of every table spread over that many CUs (with 28 tables of 576 rows they read 8 MB of
+  // table lines, which a few CUs pull far more slowly).
+  const int64_t work = std::max<int64_t>((int64_t)batch * cap_tiles, (int64_t)batch + L.grid);
+  const int gx = (int)std::min<int64_t>(256, std::max<int64_t>(1, (work + 255) / 256));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (form == Q3A_PLAN_PLAIN)
-    hipLaunchKernelGGL(paged_decode_plan_kernel<false>, dim3(gx, num_tables), dim3(1024), 0, st, a, p);
+    hipLaunchKernelGGL(paged_decode_plan_kernel<false>, dim3(gx), dim3(256), 0, st, a, p);
   else
-    hipLaunchKernelGGL(paged_decode_plan_kernel<true>, dim3(gx, num_tables), dim3(1024), 0, st, a, p);
+    hipLaunchKernelGGL(paged_decode_plan_kernel<true>, dim3(gx), dim3(256), 0, st, a, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   std::lock_guard<std::mutex> lk(g_plan_mu);
@@ -1904,14 +2094,21 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     a.plan_wg = nullptr;
     a.plan_first = nullptr;
     a.plan_tiles = nullptr;
+    a.plan_cut = nullptr;
+    a.plan_rec_cap = 0;
     if (planned) {
       if (sk_halves(num_kv_heads) != 2 || a.grid != plan.grid)
         return fail(Q3A_EINVAL, "%s: plan grid %d does not match this device's %d", who, plan.grid, a.grid);
       const PlanLayout PL = plan_layout(batch, num_kv_heads, max_pages_per_seq, page_size);
       char* const wsb = static_cast<char*>(workspace);
+      a.prefix = nullptr;
+      a.slot_page = reinterpret_cast<int*>(wsb + PL.slot_off);
+      a.ws = reinterpret_cast<float*>(wsb + PL.rec_off);
       a.plan_wg = reinterpret_cast<const int*>(wsb + PL.wg_off);
+      a.plan_cut = reinterpret_cast<const int4*>(wsb + PL.cut_off);
       a.plan_first = reinterpret_cast<const int2*>(wsb + PL.first_off);
       a.plan_tiles = reinterpret_cast<const int2*>(wsb + PL.tiles_off);
+      a.plan_rec_cap = PL.grid;
       const dim3 block2(2 * 64 * num_kv_heads);
       if (rope)
         hipLaunchKernelGGL((paged_decode_sk_kernel<true, true, 2, true>), dim3(a.grid), block2, 0, st, a);
@@ -1919,6 +2116,18 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
         hipLaunchKernelGGL((paged_decode_sk_kernel<true, false, 2, true>), dim3(a.grid), block2, 0, st, a);
       else
         hipLaunchKernelGGL((paged_decode_sk_kernel<false, false, 2, true>), dim3(a.grid), block2, 0, st, a);
+      e = hipGetLastError();
+      if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: planned launch failed: %s", who, hipGetErrorString(e));
+      const dim3 cgrid(batch + PL.grid);
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_plan_combine_kernel<true, true>), cgrid, block, 0, st, a);
+      else if (append)
+        hipLaunchKernelGGL(paged_decode_plan_combine_kernel<true>, cgrid, block, 0, st, a);
+      else
+        hipLaunchKernelGGL(paged_decode_plan_combine_kernel<false>, cgrid, block, 0, st, a);
+      e = hipGetLastError();
+      if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: planned combine launch failed: %s", who, hipGetErrorString(e));
+      return Q3A_OK;
     } else if (sk_halves(num_kv_heads) == 2) {
       const dim3 block2(2 * 64 * num_kv_heads);
       if (rope)

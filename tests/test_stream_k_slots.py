@@ -138,3 +138,80 @@ def test_planted_slot_rule_mistake_is_caught():
             except AssertionError:
                 failed += 1
     assert failed > 0
+
+
+def _plan_positions(tiles, grid, halves, rec_cap, running_ob=True):
+    """The per-frame plan's record placement (csrc/paged_decode.hip, paged_decode_plan_kernel): workgroup w's slot 0
+    goes to the cut row holding its first tile (piece w - kf), slot 1 to the cut row holding its last tile when that
+    row starts after the first tile (piece 0); piece j of the c-th cut row sits at 2c + j for j < 2, else at
+    2 rec_cap + ob + j - 2 (ob: the overflow pieces of the cut rows before it).  Returns {(w, slot): position} and the
+    descriptors [(row, pieces, ob)] in cut-row order."""
+    B = len(tiles)
+    pre = np.concatenate([[0], np.cumsum(tiles)]).astype(np.int64)
+    NT = int(pre[-1])
+    if NT == 0:
+        return {}, []
+    ge = _effective_grid(grid, NT)
+    wg_of = lambda t: ((t + 1) * ge - 1) // NT
+    desc, where = [], {}
+    ob = 0
+    for r in range(B):
+        p0, p1 = int(pre[r]), int(pre[r + 1])
+        if p1 > p0 and wg_of(p0) != wg_of(p1 - 1):
+            n = wg_of(p1 - 1) - wg_of(p0) + 1
+            where[r] = (len(desc), ob)
+            desc.append((r, n, ob))
+            ob += (n - 2) if running_ob else 0
+
+    def row_of(t):
+        return min(int(np.searchsorted(pre, t, side="right") - 1), B - 1)
+
+    def pos(r, j):
+        c, o = where[r]
+        return 2 * c + j if j < 2 else 2 * rec_cap + o + j - 2
+
+    out = {}
+    for w in range(ge):
+        lo_w, hi_w = w * NT // ge, (w + 1) * NT // ge
+        r0 = row_of(lo_w)
+        if r0 in where:
+            out[(w, 0)] = pos(r0, w - wg_of(int(pre[r0])))
+        r1 = row_of(hi_w - 1)
+        if pre[r1] > lo_w and r1 in where:
+            out[(w, 1)] = pos(r1, 0)
+    return out, desc
+
+
+@pytest.mark.parametrize("halves", [1, 2])
+def test_plan_places_every_record_where_the_planned_combine_reads_it(halves):
+    """Every record the decode writes has a plan position, no two records share one, every position lies inside the
+    4 rec_cap slots, and the planned combine's reads (descriptor c: positions of pieces 0 .. n-1) hit exactly the
+    records of that row, in the order the unplanned combine merges them."""
+    for tiles in _batches(5, 400):
+        for grid in (1, 2, 7, 8, 64, 256):
+            _, NT, ge, writes, _ = _decode_writes(tiles, grid, halves)
+            pos, desc = _plan_positions(tiles, grid, halves, rec_cap=grid)
+            assert set(pos) == set(writes), (sorted(set(writes) ^ set(pos)))
+            assert len(set(pos.values())) == len(pos)
+            assert all(0 <= p < 4 * grid for p in pos.values())
+            assert len(desc) <= max(ge - 1, 0)
+            inv = {p: k for k, p in pos.items()}
+            pre = np.concatenate([[0], np.cumsum(tiles)]).astype(np.int64)
+            for c, (r, n, ob) in enumerate(desc):
+                kf = ((int(pre[r]) + 1) * ge - 1) // NT
+                first_slot = 1 if kf * NT // ge < pre[r] else 0
+                for j in range(n):
+                    p = 2 * c + j if j < 2 else 2 * grid + ob + j - 2
+                    assert inv[p] == (kf + j, first_slot if j == 0 else 0), (r, j)
+                    assert writes[inv[p]] == r
+
+
+def test_planted_plan_position_mistake_is_caught():
+    """Numbering every cut row's overflow pieces from 0 (no running base) makes two records share a position as soon
+    as two rows are cut into three pieces or more."""
+    clashes = 0
+    for tiles in _batches(6, 200):
+        for grid in (8, 64):
+            pos, _ = _plan_positions(tiles, grid, 2, rec_cap=grid, running_ob=False)
+            clashes += len(set(pos.values())) < len(pos)
+    assert clashes > 0
