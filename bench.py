@@ -458,18 +458,33 @@ def bench_decode_append(args, dev, wl):
                                            args.split))
         return out
 
+    # The frame's plan (one per layer table, built in the frame) for the planned forms.
+    bts = torch.stack([L.block_table for (L, _, _, _) in steps])
+    planned = args.split == 0 and not args.no_plan and q3attn.decode_plan(old, bts, page, form="append") is not None
+
+    def fused_planned():
+        plans = q3attn.decode_plan(old, bts, page, form="append")
+        return [q3attn.paged_decode_append(L.q, k, v, wl.k_cache, wl.v_cache, old, bts[i], wl.scale, plan=plans[i])
+                for i, (L, _, k, v) in enumerate(steps)]
+
     _, fr_split, _ = time_graph(dev, scatter_then_decode, args.steps, args.warmup)
     _, fr_fused, _ = time_graph(dev, fused, args.steps, args.warmup)
     a = statistics.mean(fr_fused) * 1e3 / LAYERS
     b = statistics.mean(fr_split) * 1e3 / LAYERS
-    log(f"[bench] append form: fused {a:.1f} us/layer call; index_copy_ x2 + decode {b:.1f} us/layer call")
     rec = {"fused_us_per_layer_call": round(a, 2), "index_copy_then_decode_us_per_layer_call": round(b, 2),
            "fused_us_per_step": round(a * LAYERS, 1), "index_copy_then_decode_us_per_step": round(b * LAYERS, 1)}
-    rec["norm_rope_form"] = bench_decode_rope(args, dev, wl, steps, old)
+    msg = ""
+    if planned:
+        _, fr_plan, _ = time_graph(dev, fused_planned, args.steps, args.warmup)
+        c = statistics.mean(fr_plan) * 1e3 / LAYERS
+        rec["fused_planned_us_per_layer_call"] = round(c, 2)
+        msg = f"; fused with the frame's plan {c:.1f}"
+    log(f"[bench] append form: fused {a:.1f} us/layer call; index_copy_ x2 + decode {b:.1f} us/layer call{msg}")
+    rec["norm_rope_form"] = bench_decode_rope(args, dev, wl, steps, old, bts if planned else None)
     return rec
 
 
-def bench_decode_rope(args, dev, wl, steps, old):
+def bench_decode_rope(args, dev, wl, steps, old, bts=None):
     """The talker's whole attention block per layer (engine/talker.py:69-77): q/k RMSNorm + RoPE, the K/V append and
     the decode, three ways over the same frame: paged_decode_append_rope (one launch); paged_decode_append on q and k
     normalised beforehand (the attention and append alone, what the producers cost nothing in); and the producers as
@@ -509,13 +524,20 @@ def bench_decode_rope(args, dev, wl, steps, old):
         return [q3attn.paged_decode_append(L.q, k, v, wl.k_cache, wl.v_cache, old, L.block_table, wl.scale)
                 for (L, _, k, v) in steps]
 
+    def fused_planned():
+        plans = q3attn.decode_plan(old, bts, wl.page_size, form="append_rope")
+        return [q3attn.paged_decode_append_rope(L.q, k, v, qn, kn, cos, sin, wl.k_cache, wl.v_cache, old, bts[i],
+                                                wl.scale, plan=plans[i]) for i, (L, _, k, v) in enumerate(steps)]
+
     def eager_producers():
         return [q3attn.paged_decode_append(rope(rms(L.q, qn)), rope(rms(k, kn)), v, wl.k_cache, wl.v_cache, old,
                                            L.block_table, wl.scale) for (L, _, k, v) in steps]
 
     res = {}
-    for name, fn in (("append_on_normalised", append_only), ("fused", fused), ("torch_producers_then_append",
-                                                                                eager_producers)):
+    forms = [("append_on_normalised", append_only), ("fused", fused), ("torch_producers_then_append", eager_producers)]
+    if bts is not None:
+        forms.append(("fused_planned", fused_planned))
+    for name, fn in forms:
         # The layers share one pool, so a layer can read a slot another layer rewrites: one untimed frame first
         # leaves every slot at the value the frame writes, and the replays then see the state the eager frame saw.
         fn()
@@ -528,7 +550,8 @@ def bench_decode_rope(args, dev, wl, steps, old):
     torch.cuda.synchronize()
     log(f"[bench] norm/rope form: fused {res['fused_us_per_layer_call']:.1f} us/layer call; append on normalised "
         f"q/k {res['append_on_normalised_us_per_layer_call']:.1f}; torch producers + append "
-        f"{res['torch_producers_then_append_us_per_layer_call']:.1f}")
+        f"{res['torch_producers_then_append_us_per_layer_call']:.1f}" +
+        (f"; fused with the frame's plan {res['fused_planned_us_per_layer_call']:.1f}" if bts is not None else ""))
     return res
 
 
