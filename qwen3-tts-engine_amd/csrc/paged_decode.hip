@@ -84,6 +84,7 @@ struct DecodeArgs {
   const int2* plan_tiles;
   const int4* plan_cut;  // the planned combine: cut-row descriptors (row, pieces, overflow base, 0)
   int plan_rec_cap;
+  int* plan_claim;       // planned calls: one flag per range, set by the workgroup that takes it (zero between calls)
   int batch, hkv, split_tokens, max_splits, grid;
   int row_per;          // row-parallel path: tiles per wave of the table capacity (the host picks the kernel)
   float scale_log2;
@@ -629,12 +630,31 @@ __device__ __forceinline__ int plan_rec_pos(int c, int j, int ob, int rec_cap) {
   return j < 2 ? 2 * c + j : 2 * rec_cap + ob + (j - 2);
 }
 
+// Planned calls take their ranges by XCD (see paged_decode_sk_kernel's claim): range j is one of XCD (j mod 8)'s
+// ranges, and with enough tiles per range (NT >= 32 ranges) the ranges of even XCDs are 67/64 and those of odd XCDs
+// 61/64 of the mean: at equal work the odd XCDs' workgroups finished ~15 us after the even ones' at 576 rows (per-
+// wave XCC_ID stamps).  Measured at 576 rows, us per call against the unplanned call on the same box (191.6-192.3):
+// equal ranges claimed the same way -1.0, weights +-1/32 -3.7, +-3/64 -4.5, +-1/16 -2.9 to -4.2, +-5/64 -3.2,
+// +-3/32 -1.8, +-1/8 +0.5 (two passes each).  Range k starts at floor(NT W(k) / W(ge)),
+// W(k) = 64 k + 3 (k & 1) the summed weights of ranges 0 .. k-1; every range keeps at least 30 tiles, and the ranges
+// still cut the tile sequence in order, as the combine's record layout requires.
+constexpr int kPlanWScale = 64;  // range weights kPlanWScale +- kPlanWDelta: 67/64 on even XCDs, 61/64 on odd ones
+constexpr int kPlanWDelta = 3;
+__device__ __forceinline__ bool plan_weighted(int NT, int ge) { return NT >= 32 * ge; }
+__device__ __forceinline__ uint64_t plan_w(int k) {
+  return (uint64_t)kPlanWScale * (uint64_t)k + (uint64_t)(kPlanWDelta * (k & 1));
+}
+__device__ __forceinline__ int plan_lo(int k, int NT, int ge) {
+  if (!plan_weighted(NT, ge)) return (int)sk_lo(k, NT, ge);
+  return (int)((uint64_t)NT * plan_w(k) / plan_w(ge));
+}
+
 // Plan t lives at plans + t * plan_stride with the layout of the host's plan_layout.
 struct PlanArgs {
   char* plans;
   int64_t plan_stride;
   int64_t bt_stable;  // element stride between the tables
-  int64_t wg_off, cut_off, first_off, tiles_off;  // byte offsets inside one plan
+  int64_t wg_off, cut_off, first_off, tiles_off, claim_off;  // byte offsets inside one plan
   int num_tables;
   int halves;
   int rec_cap;        // cut-row descriptors (and pairs of leading record slots) per plan: the decode grid
@@ -656,8 +676,17 @@ __global__ __launch_bounds__(256) void paged_decode_plan_kernel(const DecodeArgs
   const int nthr = blockDim.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  // The workgroups holding a row's first and last tile: kf = ((p0 + 1) ge - 1) / NT, kl = (p1 ge - 1) / NT.
-  auto wg_of = [&](int t) { return (int)udiv_fit((uint64_t)(t + 1) * (uint64_t)ge - 1, (uint32_t)NT); };
+  // The range holding tile t: the largest k with plan_lo(k) <= t (equal ranges: ((t + 1) ge - 1) / NT).
+  const bool weighted = plan_weighted(NT, ge);
+  // Weighted: plan_lo(k) <= t iff W(k) <= M = floor(((t + 1) W(ge) - 1) / NT), and W(k) = 16 k + (k & 1) is increasing
+  // with W(M / 16 + 1) > M, so k is M / 16 or one less.
+  auto wg_of = [&](int t) {
+    if (!weighted) return (int)udiv_fit((uint64_t)(t + 1) * (uint64_t)ge - 1, (uint32_t)NT);
+    const int64_t M = (int64_t)(((uint64_t)(t + 1) * plan_w(ge) - 1) / (uint64_t)NT);
+    int k = (int)(M / kPlanWScale);
+    if ((int64_t)plan_w(k) > M) --k;
+    return min(max(k, 0), ge - 1);
+  };
   auto row_cut = [&](int r, int& kf, int& nseg) {
     const int p0 = s_prefix[r], p1 = s_prefix[r + 1];
     kf = p1 > p0 ? wg_of(p0) : 0;
@@ -710,7 +739,7 @@ __global__ __launch_bounds__(256) void paged_decode_plan_kernel(const DecodeArgs
     const int w = it % a.grid, tb = it / a.grid;
     int v[kPlanWgInts] = {0, 0, 0, -1, 0, 0, -1, -1};
     if (w < ge) {
-      const int lo_w = (int)sk_lo(w, NT, ge), hi_w = (int)sk_lo(w + 1, NT, ge);
+      const int lo_w = plan_lo(w, NT, ge), hi_w = plan_lo(w + 1, NT, ge);
       const int mid = p.halves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
       int mid_row = -1;
       if (p.halves == 2 && lo_w < mid && mid < hi_w) {
@@ -737,6 +766,11 @@ __global__ __launch_bounds__(256) void paged_decode_plan_kernel(const DecodeArgs
     d[0] = make_int4(v[0], v[1], v[2], v[3]);
     d[1] = make_int4(v[4], v[5], v[6], v[7]);
   }
+  // The range flags start at zero; every planned call's combine clears them again.
+  if (blockIdx.x == 0) {
+    for (int i = tid; i < p.rec_cap * p.num_tables; i += nthr)
+      reinterpret_cast<int*>(p.plans + (i / p.rec_cap) * p.plan_stride + p.claim_off)[i % p.rec_cap] = 0;
+  }
   // Cut-row descriptors (row, pieces, overflow base, 0), in row order; the slots past the last cut row get row -1.
   const int ncr = B + p.rec_cap;
   for (int it = (((int)blockIdx.x + gx / 2) % gx) * nthr + tid; it < ncr * p.num_tables; it += stride) {
@@ -759,7 +793,7 @@ __global__ __launch_bounds__(256) void paged_decode_plan_kernel(const DecodeArgs
   // wave's first list, a later one into the per-tile entries.
   for (int t = blockIdx.x * nthr + tid; t < NT; t += stride) {
     const int k = wg_of(t);
-    const int lo_w = (int)sk_lo(k, NT, ge), hi_w = (int)sk_lo(k + 1, NT, ge);
+    const int lo_w = plan_lo(k, NT, ge), hi_w = plan_lo(k + 1, NT, ge);
     const int mid = p.halves == 2 ? lo_w + (hi_w - lo_w) / 2 : hi_w;
     const int half = t >= mid ? 1 : 0;
     const int lo = half ? mid : lo_w, hi = half ? hi_w : mid;
@@ -860,13 +894,43 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
     ge = sk_effective_grid(a.grid, NT);
     if ((int)blockIdx.x >= ge) return;
   }
-  const int* const pwg = kPlan ? a.plan_wg + (int64_t)blockIdx.x * kPlanWgInts : nullptr;
+  // Planned calls: a workgroup takes the range its XCD's share of the plan holds for it (range j belongs to XCD
+  // j mod 8, and the plan weights the ranges by XCD), wherever the dispatcher put it: it reads its XCD id, guesses
+  // the range a round-robin placement gives it (workgroup 8i + c on XCD x: range 8i + x) and claims that range's flag
+  // with one exchange; on a collision (the placement was not round robin) it takes the next free range.  Every range
+  // is taken exactly once (one flag per range, as many workgroups as ranges) and is the same range whoever takes it,
+  // so the output does not depend on the placement.  The exchange goes out with the loads of the guessed range and its
+  // first tile list, on a flag no other workgroup touches, so it costs no round trip of its own; the planned combine
+  // clears the flags for the next call.
+  __shared__ int s_claim;
+  [[maybe_unused]] int krange = blockIdx.x;
+  const int* pwg = nullptr;
   if constexpr (kPlan) {
-    // The wave's first tile list goes straight into LDS (lanes 0-31 copy 16 B each; the other lanes' out-of-range
-    // copies write zeros over the next 512 B), issued beside the scalar loads of the range: no register holds it
-    // through the tile loop.
-    lds_copy16(make_rsrc(a.plan_first + ((int64_t)blockIdx.x * kHalves + half) * 64, 64 * sizeof(int2)),
-               &s_plan[kPlan ? wv : 0][0], lane < 32 ? (uint32_t)lane * 16 : kOutOfRange);
+    const int xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 7;  // HW_REG_XCC_ID, bits 0-3
+    const int kspec = min((int)(blockIdx.x & ~7u) + xcc, a.grid - 1);
+    auto load_range = [&](int k) {
+      pwg = a.plan_wg + (int64_t)k * kPlanWgInts;
+      // The wave's first tile list goes straight into LDS (lanes 0-31 copy 16 B each; the other lanes' out-of-range
+      // copies write zeros over the next 512 B): no register holds it through the tile loop.
+      lds_copy16(make_rsrc(a.plan_first + ((int64_t)k * kHalves + half) * 64, 64 * sizeof(int2)),
+                 &s_plan[kPlan ? wv : 0][0], lane < 32 ? (uint32_t)lane * 16 : kOutOfRange);
+    };
+    load_range(kspec);
+    if (tid == 0) {
+      int got = -1;
+      for (int d = 0; d < a.grid && got < 0; ++d) {
+        const int k = kspec + d < a.grid ? kspec + d : kspec + d - a.grid;
+        if (__hip_atomic_exchange(a.plan_claim + k, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) got = k;
+      }
+      s_claim = got;
+    }
+    __syncthreads();
+    krange = s_claim;
+    if (krange != kspec) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the guessed list's copy has landed before it is replaced
+      if (krange >= 0) load_range(krange);
+    }
+    if (krange < 0) return;  // no free range (one flag per launched workgroup: does not happen)
   }
   // The workgroup's tile range [lo_w, hi_w) and, with two halves, its midpoint; the row that runs across the
   // midpoint (tiles mid - 1 and mid in the same row), if any.  Only two values stay live through the tile loop (the
@@ -1272,6 +1336,8 @@ __global__ __launch_bounds__(1024) void paged_decode_plan_combine_kernel(const D
     return;
   }
   const int ci = blockIdx.x - a.batch;
+  // The decode kernel's range flags, cleared for the next call on the plan (one per possible range).
+  if (threadIdx.x == 0) __hip_atomic_store(a.plan_claim + ci, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int4 d = a.plan_cut[ci];
   const int h = lane >> 5;
   const int d0 = (lane & 31) * 4;
@@ -1783,7 +1849,7 @@ size_t workspace_bytes(int batch, int hkv, int max_pages, int page_size, int spl
 // At most grid - 1 rows are cut (each crosses a range boundary), and the records number at most 2 per workgroup.
 struct PlanLayout {
   int grid;
-  size_t slot_off, rec_off, wg_off, cut_off, first_off, tiles_off, bytes;
+  size_t slot_off, rec_off, wg_off, cut_off, claim_off, first_off, tiles_off, bytes;
 };
 
 PlanLayout plan_layout(int batch, int hkv, int max_pages, int page_size) {
@@ -1794,7 +1860,8 @@ PlanLayout plan_layout(int batch, int hkv, int max_pages, int page_size) {
   L.rec_off = L.slot_off + align256((size_t)batch * sizeof(int));
   L.wg_off = L.rec_off + align256((size_t)4 * L.grid * hkv * kPartFloats * sizeof(float));
   L.cut_off = L.wg_off + align256((size_t)L.grid * kPlanWgInts * sizeof(int));
-  L.first_off = L.cut_off + align256((size_t)L.grid * sizeof(int4));
+  L.claim_off = L.cut_off + align256((size_t)L.grid * sizeof(int4));
+  L.first_off = L.claim_off + align256((size_t)L.grid * sizeof(int));
   L.tiles_off = L.first_off + align256((size_t)L.grid * sk_halves(hkv) * 64 * sizeof(int2));
   L.bytes = L.tiles_off + align256((size_t)batch * cap_tiles * sizeof(int2));
   return L;
@@ -1879,6 +1946,7 @@ extern "C" int q3a_paged_decode_plan(const int32_t* cache_seqlens, const int32_t
   p.cut_off = (int64_t)L.cut_off;
   p.first_off = (int64_t)L.first_off;
   p.tiles_off = (int64_t)L.tiles_off;
+  p.claim_off = (int64_t)L.claim_off;
   p.num_tables = num_tables;
   p.halves = sk_halves(num_kv_heads);
   p.rec_cap = L.grid;
@@ -2096,6 +2164,7 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
     a.plan_tiles = nullptr;
     a.plan_cut = nullptr;
     a.plan_rec_cap = 0;
+    a.plan_claim = nullptr;
     if (planned) {
       if (sk_halves(num_kv_heads) != 2 || a.grid != plan.grid)
         return fail(Q3A_EINVAL, "%s: plan grid %d does not match this device's %d", who, plan.grid, a.grid);
@@ -2109,6 +2178,7 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
       a.plan_first = reinterpret_cast<const int2*>(wsb + PL.first_off);
       a.plan_tiles = reinterpret_cast<const int2*>(wsb + PL.tiles_off);
       a.plan_rec_cap = PL.grid;
+      a.plan_claim = reinterpret_cast<int*>(wsb + PL.claim_off);
       const dim3 block2(2 * 64 * num_kv_heads);
       if (rope)
         hipLaunchKernelGGL((paged_decode_sk_kernel<true, true, 2, true>), dim3(a.grid), block2, 0, st, a);

@@ -1,11 +1,14 @@
 """GPU parity of planned decode calls (q3attn.decode_plan + Q3A_DECODE_PLANNED through the C ABI).
 
 A plan holds the stream-K decomposition of the calls that share cache_seqlens and a block table (the 28 calls of a
-talker frame, engine/talker.py:77 with ctx and bt of engine/talker.py:107-112): the workgroup ranges, each wave's
-first tile list and every tile's row, offset, valid tokens and page id.  A planned call runs the same tile
-arithmetic over the same partition as the unplanned stream-K call, so its output must be bit-identical to it (and the
-append forms' slot rows too); the unplanned stream-K kernel is itself checked against the oracle elsewhere, and the
-outputs here are checked against the oracle as well (max-abs 2e-2, mean-abs 2e-3)."""
+talker frame, engine/talker.py:77 with ctx and bt of engine/talker.py:107-112): the tile ranges, each wave's first
+tile list and every tile's row, offset, valid tokens and page id.  Each workgroup of a planned call claims one of
+the plan's ranges from its XCD's queue, and with enough tiles per range the plan weights the ranges by XCD, so the
+partition differs from the unplanned call's equal ranges: the outputs are checked against the oracle (max-abs 2e-2,
+mean-abs 2e-3) and against the unplanned call within the spread of fp32 reduction orders (one bf16 step), the slot
+rows of the append forms bit for bit, and repeated planned calls against each other bit for bit (the ranges are
+fixed by the plan; which workgroup claims which does not change the output).  With few tiles per range the plan
+keeps equal ranges and the planned call is bit-identical to the unplanned one."""
 import numpy as np
 import pytest
 import torch
@@ -26,6 +29,15 @@ def _eq(a, b, what):
         d = (a.float() - b.float()).abs()
         print(f"[plan] {what}: {int((d > 0).sum())} elements differ, max {float(d.max())}", flush=True)
     assert same, what
+
+
+def _near(a, b, what, tol=1.6e-2):
+    """Two decompositions of the same attention: equal up to the order of the fp32 reductions and the rounding of
+    the bf16 output (a bf16 step at |o| ~ 1 is 2^-8)."""
+    d = (a.float() - b.float()).abs()
+    print(f"[plan] {what}: max |planned - unplanned| {float(d.max()):.3g}, {int((d > 0).sum())} of {d.numel()} differ",
+          flush=True)
+    assert float(d.max()) <= tol, what
 
 
 def _parity(out, ref, what):
@@ -51,14 +63,16 @@ def test_planned_576_rows_two_tables(cuda_device):
         out = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, bts[li], wl.scale,
                                   plan=plans[li])
         torch.cuda.synchronize()
-        _eq(out, ref, f"layer {li}")
+        _near(out, ref, f"layer {li}")
         if li == 0:
             _parity(out, decode_oracle(wl), "decode576 planned layer 0")
-    # The same plan serves repeated calls (the partial records it holds are rewritten by each).
-    again = q3attn.paged_decode(wl.layers[1].q, wl.k_cache, wl.v_cache, wl.cache_seqlens, bts[1], wl.scale,
-                                plan=plans[1])
-    torch.cuda.synchronize()
-    _eq(again, out, "repeated call")
+    # The same plan serves repeated calls (the partial records it holds are rewritten by each, the claim counters are
+    # left at zero), with the same output bits whatever workgroup claims which range.
+    for rep in range(4):
+        again = q3attn.paged_decode(wl.layers[1].q, wl.k_cache, wl.v_cache, wl.cache_seqlens, bts[1], wl.scale,
+                                    plan=plans[1])
+        torch.cuda.synchronize()
+        _eq(again, out, f"repeated call {rep}")
 
 
 @pytest.mark.parametrize("seed,B,max_ctx,page", [(1, 65, 2064, 16), (2, 200, 1800, 16), (3, 700, 600, 32),
@@ -78,10 +92,24 @@ def test_planned_random_shapes(cuda_device, seed, B, max_ctx, page):
     assert plan is not None
     ref = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale, SK)
     out = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale, plan=plan)
+    again = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale, plan=plan)
     torch.cuda.synchronize()
-    _eq(out, ref, f"seed {seed}")
+    _near(out, ref, f"seed {seed}")
+    _eq(again, out, f"seed {seed} repeated")
     rows = sorted(set(rng.choice(B, min(B, 48), replace=False).tolist()) | {0, 1, 2, 3})
     _parity(out[rows], decode_oracle(wl, rows=rows), f"planned seed {seed}")
+
+
+def test_planned_equal_ranges_are_bit_identical(cuda_device):
+    """With fewer than 32 tiles per range (70 rows of 400 tokens: 1,750 tiles over 256 ranges) the plan keeps the
+    unplanned call's equal ranges, and the planned call equals the unplanned one bit for bit."""
+    wl = W.make_decode("plan", cuda_device, ctx=np.full(70, 400), num_pages=70 * 26, max_ctx=416, seed=8)
+    L = wl.layers[0]
+    plan = q3attn.decode_plan(wl.cache_seqlens, L.block_table, wl.page_size)
+    ref = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale, SK)
+    out = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale, plan=plan)
+    torch.cuda.synchronize()
+    _eq(out, ref, "equal ranges")
 
 
 def test_planned_long_waves(cuda_device):
@@ -96,7 +124,7 @@ def test_planned_long_waves(cuda_device):
     ref = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale, SK)
     out = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table, wl.scale, plan=plan)
     torch.cuda.synchronize()
-    _eq(out, ref, "long waves")
+    _near(out, ref, "long waves")
     _parity(out[[0, 1, 35, 69]], decode_oracle(wl, rows=[0, 1, 35, 69]), "planned long waves")
 
 
@@ -153,10 +181,13 @@ def test_planned_append_forms_576(cuda_device, form):
     plan = q3attn.decode_plan(seqlens, L.block_table, wl.page_size, form=form)
     out = call(plan)
     torch.cuda.synchronize()
-    _eq(out, ref, form)
+    _near(out, ref, form)
     _eq(kflat.index_select(0, idx), ref_k, f"{form} k slots")
     _eq(vflat.index_select(0, idx), ref_v, f"{form} v slots")
     assert torch.isfinite(out.float()).all()
+    again = call(plan)
+    torch.cuda.synchronize()
+    _eq(again, out, f"{form} repeated")
 
 
 def test_plan_refuses_other_calls(cuda_device):
@@ -222,5 +253,8 @@ def test_planned_graph_replays_follow_new_lengths(cuda_device):
         torch.cuda.synchronize()
         for li, L in enumerate(wl.layers):
             ref = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, seqlens, bts[li], wl.scale, SK)
+            plans = q3attn.decode_plan(seqlens, bts, wl.page_size)
+            eager = q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, seqlens, bts[li], wl.scale, plan=plans[li])
             torch.cuda.synchronize()
-            _eq(outs[li], ref, f"replay {rep} layer {li}")
+            _eq(outs[li], eager, f"replay {rep} layer {li}")
+            _near(outs[li], ref, f"replay {rep} layer {li} against unplanned")
