@@ -1040,7 +1040,8 @@ def bench_probe(args, dev):
 
     plib = ctypes.CDLL(os.path.join(ROOT, "qwen3-tts-engine_amd", "q3attn", "libq3probe.so"))
     vp, i64, ci, u32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32
-    plib.q3p_tile_read.argtypes = [vp, vp, i64, i64, i64, ci, ci, ci, vp, ci, ci, u32, vp, vp]
+    plib.q3p_tile_read.argtypes = [vp, vp, i64, i64, i64, ci, ci, ci, vp, ci, ci, u32, vp, vp, vp]
+    plib.q3p_clear_flags.argtypes = [vp, ci, vp]
     plib.q3p_stream_read.argtypes = [vp, ctypes.c_size_t, ci, ci, u32, vp, vp]
     plib.q3p_resident_grid.argtypes = [ci, ci]
     magic = 0x9E3779B9
@@ -1058,10 +1059,15 @@ def bench_probe(args, dev):
     sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)   # one word per workgroup of either probe
     stream = lambda: torch.cuda.current_stream(dev).cuda_stream
 
-    def probe_frame():
-        for t in tiles:
+    flags = torch.zeros(LAYERS * grid, dtype=torch.int32, device=dev)
+
+    def probe_frame(by_xcd=False):
+        if by_xcd and plib.q3p_clear_flags(flags.data_ptr(), flags.numel(), stream()):
+            raise RuntimeError("q3p_clear_flags failed")
+        for i, t in enumerate(tiles):
+            fl = flags[i * grid:].data_ptr() if by_xcd else None
             rc = plib.q3p_tile_read(kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
-                                    kc.shape[0], 16, 8, t.data_ptr(), nt, grid, magic, sink.data_ptr(), stream())
+                                    kc.shape[0], 16, 8, t.data_ptr(), nt, grid, magic, sink.data_ptr(), fl, stream())
             if rc:
                 raise RuntimeError(f"q3p_tile_read failed ({rc})")
         return [sink]
@@ -1069,8 +1075,17 @@ def bench_probe(args, dev):
     def decode_frame():
         return [q3attn.paged_decode(L.q, kc, vc, wl.cache_seqlens, L.block_table, wl.scale, 0) for L in wl.layers]
 
+    bts = torch.stack([L.block_table for L in wl.layers])
+
+    def planned_decode_frame():
+        plans = q3attn.decode_plan(wl.cache_seqlens, bts, wl.page_size)
+        return [q3attn.paged_decode(L.q, kc, vc, wl.cache_seqlens, bts[i], wl.scale, plan=plans[i])
+                for i, L in enumerate(wl.layers)]
+
     res = {}
-    for name, fn in (("tile_read", probe_frame), ("decode", decode_frame), ("tile_read_again", probe_frame)):
+    for name, fn in (("tile_read", probe_frame), ("tile_read_by_xcd", lambda: probe_frame(True)),
+                     ("decode", decode_frame), ("decode_planned", planned_decode_frame),
+                     ("tile_read_again", probe_frame), ("tile_read_by_xcd_again", lambda: probe_frame(True))):
         _, frame_ms, _ = time_graph(dev, fn, args.steps, args.warmup, 1.0)
         us = statistics.median(frame_ms) * 1e3 / LAYERS
         res[name] = {"us_per_call": round(us, 2), "kv_gbps": round(kv_bytes / (us * 1e-6) / 1e9, 1)}
@@ -1079,6 +1094,8 @@ def bench_probe(args, dev):
     torch.cuda.empty_cache()
     ceiling = min(res["tile_read"]["us_per_call"], res["tile_read_again"]["us_per_call"])
     res["decode_over_probe"] = round(ceiling / res["decode"]["us_per_call"], 4)
+    ceiling_x = min(res["tile_read_by_xcd"]["us_per_call"], res["tile_read_by_xcd_again"]["us_per_call"])
+    res["planned_decode_over_probe_by_xcd"] = round(ceiling_x / res["decode_planned"]["us_per_call"], 4)
 
     sgrid = plib.q3p_resident_grid(0, 0) * 2
     n = 4 << 30

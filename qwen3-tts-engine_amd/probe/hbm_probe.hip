@@ -5,7 +5,8 @@
 // q3p_stream_read: every 16-byte word of a buffer once, grid-stride, 16 B per lane per load, with or without the
 //   non-temporal hint.
 // q3p_tile_read: the talker decode's K/V access pattern.  A resident grid cuts a flattened list of 16-token tiles
-//   (page id, valid tokens; rows one after another) into equal contiguous ranges; the workgroup's wave g streams KV
+//   (page id, valid tokens; rows one after another) into equal contiguous ranges (or, with flags, the planned
+//   decode's XCD-weighted ranges, each taken by a workgroup of its XCD); the workgroup's wave g streams KV
 //   head g of each tile in its range: 4 loads of K and 4 of V per tile, lane l fetching token 4i + l/16, dims
 //   8 (l % 16) .. +8 (256 B head rows at the token stride), through a buffer descriptor covering exactly one page, so
 //   tokens past the tile's valid count and invalid pages are bounds-failed loads; non-temporal; tile j+1 issued before
@@ -63,6 +64,7 @@ struct TileArgs {
   int num_pages;
   const int2* tiles;             // [nt]: (page id, valid tokens 1..16)
   int nt, grid;
+  int* flags;                    // nullptr: equal ranges by workgroup index; else one zeroed flag per range (below)
   uint32_t magic;
   uint32_t* sink;
 };
@@ -85,17 +87,53 @@ __device__ __forceinline__ void issue(const TileArgs& a, int2 t, uint32_t lane_o
   }
 }
 
+// Range k of the XCD-weighted split (as the planned decode's): ranges of even index 67/64 of the mean, odd 61/64,
+// with at least 4 tiles per range (the probe's resident grid is larger than the decode's); equal ranges otherwise.
+__device__ __forceinline__ int range_lo(int k, int nt, int grid, bool weighted) {
+  if (!weighted) return (int)((int64_t)k * nt / grid);
+  const uint64_t wk = 64ull * (uint64_t)k + 3ull * (uint64_t)(k & 1), wg = 64ull * (uint64_t)grid + 3ull * (uint64_t)(grid & 1);
+  return (int)((uint64_t)nt * wk / wg);
+}
+
 __global__ __launch_bounds__(1024) void tile_read_kernel(const TileArgs a) {
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int grp = lane >> 4;
-  const int lo = (int)((int64_t)blockIdx.x * a.nt / a.grid);
-  const int hi = (int)((int64_t)(blockIdx.x + 1) * a.nt / a.grid);
+  // With flags, the workgroup takes range j mod 8 == its XCD id the way the planned decode does: it guesses the range a
+  // round-robin placement gives it, prefetches that range's first tile entries and claims the range's flag with one
+  // exchange (a collision takes the next free flag); ranges weighted by XCD.
+  __shared__ int s_claim;
+  int k = blockIdx.x;
+  bool weighted = false;
+  int2 pre = make_int2(-1, 0);
+  int kspec = -1;
+  if (a.flags != nullptr) {
+    const int xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 7;  // HW_REG_XCC_ID, bits 0-3
+    weighted = a.nt >= 4 * a.grid;
+    kspec = min((int)(blockIdx.x & ~7u) + xcc, a.grid - 1);
+    const int lo_s = range_lo(kspec, a.nt, a.grid, weighted), hi_s = range_lo(kspec + 1, a.nt, a.grid, weighted);
+    if (lane < min(64, hi_s - lo_s)) pre = a.tiles[lo_s + lane];
+    if (threadIdx.x == 0) {
+      int got = -1;
+      for (int d = 0; d < a.grid && got < 0; ++d) {
+        const int kk = kspec + d < a.grid ? kspec + d : kspec + d - a.grid;
+        if (__hip_atomic_exchange(a.flags + kk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) got = kk;
+      }
+      s_claim = got;
+    }
+    __syncthreads();
+    k = s_claim;
+    if (k < 0) return;
+  }
+  const int lo = range_lo(k, a.nt, a.grid, weighted);
+  const int hi = range_lo(k + 1, a.nt, a.grid, weighted);
   const uint32_t lane_off = (uint32_t)((grp * a.kv_st + g * a.kv_sh + (lane & 15) * 8) * 2);
   uint32_t acc = 0;
   for (int cb = lo; cb < hi; cb += 64) {
     const int n = min(64, hi - cb);
-    const int2 mine = lane < n ? a.tiles[cb + lane] : make_int2(-1, 0);  // lane i describes tile cb + i
+    // lane i describes tile cb + i (the first list of a correctly guessed range was prefetched)
+    const int2 mine = (cb == lo && k == kspec) ? (lane < n ? pre : make_int2(-1, 0))
+                                               : (lane < n ? a.tiles[cb + lane] : make_int2(-1, 0));
     auto tile = [&](int j) {
       const int jj = j < n ? j : 0;
       int2 t;
@@ -139,9 +177,10 @@ extern "C" int q3p_stream_read(const void* buf, size_t n16, int grid, int nt, ui
 // Streams the K/V head rows of nt tiles (tiles: [nt] int2 of (page id, valid tokens)) from the paged pools
 // [num_pages, 16, hkv, 128] bf16 (16-token pages) with `grid` workgroups of 64 * hkv threads, each over an equal contiguous
 // range of the list.  sink: at least `grid` words.  0 or a HIP error.
+// flags: nullptr, or `grid` ints that are zero at launch (q3p_clear_flags): the XCD-weighted ranges taken by XCD.
 extern "C" int q3p_tile_read(const void* k_cache, const void* v_cache, int64_t kv_stride_page, int64_t kv_stride_tok,
                              int64_t kv_stride_head, int num_pages, int page_size, int hkv, const int32_t* tiles,
-                             int nt, int grid, uint32_t magic, uint32_t* sink, void* stream) {
+                             int nt, int grid, uint32_t magic, uint32_t* sink, int* flags, void* stream) {
   // A tile is one whole 16-token page (its loads start at token 0 of the page).
   if (!k_cache || !v_cache || !tiles || !sink || nt < 0 || grid <= 0 || hkv < 1 || hkv > 16 || page_size != 16)
     return (int)hipErrorInvalidValue;
@@ -159,7 +198,21 @@ extern "C" int q3p_tile_read(const void* k_cache, const void* v_cache, int64_t k
   a.grid = grid;
   a.magic = magic;
   a.sink = sink;
+  a.flags = flags;
   hipLaunchKernelGGL(tile_read_kernel, dim3(grid), dim3(64 * hkv), 0, static_cast<hipStream_t>(stream), a);
+  return (int)hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void clear_kernel(int* flags, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) flags[i] = 0;
+}
+
+// Zeroes n ints (the range flags of q3p_tile_read calls) with a kernel (capturable, no memset node).
+extern "C" int q3p_clear_flags(int* flags, int n, void* stream) {
+  if (!flags || n < 0) return (int)hipErrorInvalidValue;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(clear_kernel, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), flags, n);
   return (int)hipGetLastError();
 }
 
