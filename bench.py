@@ -278,6 +278,21 @@ def bench_decode(args, dev, name, cpu_budget_s: float = 12.0):
     return rec
 
 
+def make_planned_frame(wl, bts):
+    """A frame of the workload's layer calls with the frame's plan (q3attn.decode_plan over the stacked per-layer
+    tables, built inside the frame), or None when the library has no plan for the shape."""
+    import q3attn
+
+    if q3attn.decode_plan(wl.cache_seqlens, bts, wl.page_size) is None:
+        return None
+
+    def frame():
+        plans = q3attn.decode_plan(wl.cache_seqlens, bts, wl.page_size)
+        return [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, bts[i], wl.scale, plan=plans[i])
+                for i, L in enumerate(wl.layers)]
+    return frame
+
+
 def decode_kernel_name(wl, split, planned=False):
     """The kernels one decode call of this workload launches (the library needs no workspace exactly when it takes
     the row-parallel path, for split 0)."""
@@ -325,6 +340,8 @@ def bench_decode_scaling(args, dev):
         wls[scale] = W.make_decode("decode576", dev, layers=LAYERS, seed=args.seed, ctx=ctx,
                                    max_ctx=int(math.ceil(W.MAX_CTX["decode576"] * scale)))
     times = {scale: [] for scale in scales}
+    ptimes = {scale: [] for scale in scales}   # the same frames with the frame's plan
+    bts = {scale: torch.stack([L.block_table for L in wls[scale].layers]) for scale in scales}
     for scale in (1.0, 0.5, 2.0, 2.0, 0.5, 1.0):
         wl = wls[scale]
         _, frame_ms, _ = time_graph(dev, lambda: [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens,
@@ -332,7 +349,13 @@ def bench_decode_scaling(args, dev):
                                                   for L in wl.layers], args.steps, args.warmup, 1.0)
         us = statistics.mean(frame_ms) * 1e3 / LAYERS
         times[scale].append(us)
-        log(f"[bench] contexts x{scale}: {us:.1f} us/call")
+        pf = make_planned_frame(wl, bts[scale])
+        pus = float("nan")
+        if pf is not None:
+            _, frame_ms, _ = time_graph(dev, pf, args.steps, args.warmup, 1.0)
+            pus = statistics.mean(frame_ms) * 1e3 / LAYERS
+            ptimes[scale].append(pus)
+        log(f"[bench] contexts x{scale}: {us:.1f} us/call, {pus:.1f} with the frame's plan")
     pts = []
     for scale in scales:
         wl = wls[scale]
@@ -350,9 +373,21 @@ def bench_decode_scaling(args, dev):
     rate = 1.0 / slope / 1e3  # bytes per us -> GB/s
     log(f"[bench] least squares over the three scales: marginal rate {rate:.0f} GB/s = {rate / HBM_PEAK_GBPS:.1%} of "
         f"peak, fixed cost {icpt:.1f} us per call")
-    return {"metric": "paged decode us/call against bytes/call at context scales 1/2, 1, 2 (576 rows)",
-            "points": pts, "marginal_gbps": round(float(rate), 1),
-            "marginal_pct_peak": round(float(rate) / HBM_PEAK_GBPS * 100, 2), "fixed_us_per_call": round(float(icpt), 2)}
+    rec = {"metric": "paged decode us/call against bytes/call at context scales 1/2, 1, 2 (576 rows)",
+           "points": pts, "marginal_gbps": round(float(rate), 1),
+           "marginal_pct_peak": round(float(rate) / HBM_PEAK_GBPS * 100, 2), "fixed_us_per_call": round(float(icpt), 2)}
+    if all(ptimes[sc] for sc in scales):
+        yp = np.array([statistics.mean(ptimes[p["ctx_scale"]]) for p in pts], dtype=np.float64)
+        pslope, picpt = np.polyfit(x, yp, 1)
+        prate = 1.0 / pslope / 1e3
+        for p in pts:
+            p["us_per_layer_call_planned"] = [round(t, 2) for t in ptimes[p["ctx_scale"]]]
+        rec["planned"] = {"marginal_gbps": round(float(prate), 1),
+                          "marginal_pct_peak": round(float(prate) / HBM_PEAK_GBPS * 100, 2),
+                          "fixed_us_per_call": round(float(picpt), 2)}
+        log(f"[bench] with the frame's plan: marginal rate {prate:.0f} GB/s = {prate / HBM_PEAK_GBPS:.1%} of peak, "
+            f"fixed cost {picpt:.1f} us per call")
+    return rec
 
 
 def bench_decode_small(args, dev):
