@@ -145,6 +145,50 @@ def test_compiled_decode_plain_form(cuda_device):
         assert torch.equal(static, o)
 
 
+def test_compiled_decode_with_a_plan(cuda_device):
+    """The frame's plan built outside the compiled layers and passed in as scheduler_metadata (the way flash-attn 3's
+    get_scheduler_metadata is used): two compiled layer calls sharing the plan equal the eager planned calls bit for
+    bit and the oracle, the compiled module allocates nothing of the plan's size (the op declares no mutation of it:
+    it only uses the buffer behind the plan as scratch within a call), and a graph of the plan launch and the compiled
+    layers replays bit for bit."""
+    from torch._inductor.utils import run_and_get_code
+
+    dev = cuda_device
+    torch._dynamo.reset()
+    kc, vc = _pools(dev, 7)
+    B, P = 80, 32                      # 80 rows of 512-token tables: the library decodes them with stream-K
+    rng = np.random.default_rng(8)
+    bt = torch.from_numpy(rng.permutation(NUM_PAGES)[: B * P].reshape(B, P).astype(np.int32)).to(dev)
+    ctx = torch.from_numpy(rng.integers(1, P * PAGE + 1, B).astype(np.int32)).to(dev)
+    g = torch.Generator(device=dev).manual_seed(9)
+    q1 = torch.randn(B, NH, HD, generator=g, device=dev).to(torch.bfloat16)
+    q2 = torch.randn(B, NH, HD, generator=g, device=dev).to(torch.bfloat16)
+
+    def two_layers(q1, q2, ctx, bt, plan):
+        o1 = q3attn.flash_attn_with_kvcache(q1.unsqueeze(1), kc, vc, cache_seqlens=ctx, block_table=bt,
+                                            softmax_scale=SCALE, causal=True, scheduler_metadata=plan)
+        o2 = q3attn.flash_attn_with_kvcache(q2.unsqueeze(1), kc, vc, cache_seqlens=ctx, block_table=bt,
+                                            softmax_scale=SCALE, causal=True, scheduler_metadata=plan)
+        return o1, o2
+
+    plan = q3attn.decode_plan(ctx, bt, PAGE)
+    assert plan is not None
+    step = torch.compile(two_layers, dynamic=False)
+    (o1, o2), codes = run_and_get_code(step, q1, q2, ctx, bt, plan)
+    e1, e2 = two_layers(q1, q2, ctx, bt, plan)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, e1) and torch.equal(o2, e2)
+    assert not _big_allocations(codes, plan.numel() // 8)
+    ref = ora.paged_decode(to_np(q1), to_np(kc), to_np(vc), ctx.cpu().numpy(), bt.cpu().numpy(), SCALE)
+    check(o1[:, 0], ref, "compiled planned decode")
+    gr, static = _capture(lambda: step(q1, q2, ctx, bt, q3attn.decode_plan(ctx, bt, PAGE)), dev)
+    for _ in range(3):
+        torch.randn(1 << 18, device=dev)
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static[0], o1) and torch.equal(static[1], o2)
+
+
 def test_compiled_decode_append_form(cuda_device):
     """The same layer with the scatters folded into the call (flash-attn's k=/v= form): compiled, the op mutates the
     caller's pools in place; bitwise equal to index_copy_ + decode on the same q/k/v."""
