@@ -319,6 +319,59 @@ SMALL_SHAPES = ((1, 64), (1, 256), (1, 1024), (1, 1800), (2, 1800), (4, 1024), (
 SMALL_PATHS = (("row_parallel", -1), ("chunks", -2), ("stream_k", -3), ("auto", 0))
 
 
+PLAN_SWEEP = ((96, "log"), (128, "log"), (256, "uniform"), (384, "log"), (576, "log"), (1024, "log"),
+              (2048, "uniform"), (4096, "short"))
+
+
+def bench_decode_plan_sweep(args, dev):
+    """The frame's plan against no plan over batch sizes the library decodes with stream-K: rows' contexts
+    log-uniform in [64, 1800] ("log"), uniform in [200, 1200] ("uniform") or in [16, 300] ("short"); 8 layer calls per
+    graph replay, each with its own random table over a pool sized to the batch; unplanned and planned frames timed
+    twice each, alternating."""
+    import numpy as np
+    import torch
+
+    import q3attn
+    from q3attn import workloads as W
+
+    layers = 8
+    out = {}
+    for B, kind in PLAN_SWEEP:
+        rng = np.random.default_rng(B)
+        if kind == "log":
+            ctx = np.exp(rng.uniform(np.log(64), np.log(1800), B)).astype(np.int64)
+        elif kind == "uniform":
+            ctx = rng.integers(200, 1201, B)
+        else:
+            ctx = rng.integers(16, 300, B)
+        maxc = int(ctx.max()) + 16
+        wl = W.make_decode("plan-sweep", dev, layers=layers, ctx=ctx, num_pages=B * -(-maxc // 16) + 64,
+                           max_ctx=maxc, seed=B)
+        bts = torch.stack([L.block_table for L in wl.layers])
+        unplanned = lambda: [q3attn.paged_decode(L.q, wl.k_cache, wl.v_cache, wl.cache_seqlens, L.block_table,
+                                                 wl.scale, 0) for L in wl.layers]
+        planned = make_planned_frame(wl, bts)
+        t = {"unplanned": [], "planned": []}
+        for name, fn in (("unplanned", unplanned), ("planned", planned)) * 2:
+            if fn is not None:
+                _, ms, _ = time_graph(dev, fn, args.steps, args.warmup, 0.5)
+                t[name].append(round(statistics.mean(ms) * 1e3 / layers, 2))
+        out[f"{B}x{kind}"] = {"tiles": int(((ctx + 15) // 16).sum()), "unplanned_us_per_call": t["unplanned"],
+                              "planned_us_per_call": t["planned"]}
+        log(f"[bench] {B} rows ({kind}): unplanned {t['unplanned']} planned {t['planned']} us/call")
+        del wl
+        torch.cuda.empty_cache()
+    gains = [statistics.mean(r["unplanned_us_per_call"]) / statistics.mean(r["planned_us_per_call"])
+             for r in out.values() if r["planned_us_per_call"]]
+    rec = base_record("paged decode attn speed-up of the frame's plan (mean over batch sizes), 1×MI355X",
+                      round(statistics.mean(gains), 4), "x", args, 0.0, True, {
+                          "workload": "talker paged decode attention, 96-4,096 rows, 8 layer calls per step with "
+                                      "per-layer random tables, with and without the frame's plan",
+                          "shapes": list(out), "parallelism": "single GPU"})
+    rec["per_shape"] = out
+    return rec
+
+
 def bench_decode_scaling(args, dev):
     """The 576-row workload with every row's context scaled by 1/2, 1 and 2 (the same rows, each scale its own
     131,072-page pool and tables of the scaled capacity, all three built first; 28 layer calls per graph replay, each
@@ -1256,7 +1309,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="decode576",
-                    choices=["decode576", "decode256", "decode1x64", "decode-small", "decode-scaling", "cp512",
+                    choices=["decode576", "decode256", "decode1x64", "decode-small", "decode-scaling",
+                             "decode-plan-sweep", "cp512",
                              "prefill32", "admit", "probe"],
                     help="c5 (default, the headline metric), c3 decode, c1 decode, decode at small batches (each "
                          "decode kernel by path code and the library's choice), c5 with its contexts scaled by 1/2, "
@@ -1316,6 +1370,8 @@ def main() -> int:
         rec = bench_decode_small(args, dev)
     elif args.workload == "decode-scaling":
         rec = bench_decode_scaling(args, dev)
+    elif args.workload == "decode-plan-sweep":
+        rec = bench_decode_plan_sweep(args, dev)
     elif args.workload == "probe":
         rec = bench_probe(args, dev)
     elif args.workload == "cp512":
