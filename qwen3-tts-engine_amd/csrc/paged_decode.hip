@@ -1298,44 +1298,63 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_combine_kernel(const Dec
   store_slot();
 }
 
-// Planned calls: one workgroup per row (zero rows, and in the append forms the new rows' slot stores, as in the
-// combine above) and then one per possible cut row.  A cut row's first two records sit at positions 2c and 2c + 1
-// (c: its index among the cut rows), so they are loaded beside its descriptor, before the row is known: the merge
-// waits for one memory round trip (a second only for rows cut into more than two pieces), where the unplanned
-// combine first loads the prefix sums and then the records.  The merge itself is merge_records' arithmetic over the
-// same records in the same order, so the output equals the unplanned call's bit for bit.
+// Planned calls: workgroups of kPlanRowsPerWg rows first (zero rows, and in the append forms the new rows' slot
+// stores, as in the combine above; every load of the rows goes out at once), then one per possible cut row.  A cut
+// row's first two records sit at positions 2c and 2c + 1 (c: its index among the cut rows), so they are loaded beside
+// its descriptor, before the row is known: the merge waits for one memory round trip (a second only for rows cut into
+// more than two pieces), where the unplanned combine first loads the prefix sums and then the records.  The merge
+// itself is merge_records' arithmetic over the same records in the same order, so the output equals the unplanned
+// call's on the same ranges bit for bit.
+constexpr int kPlanRowsPerWg = 4;
+
 template <bool kAppend, bool kRope = false>
 __global__ __launch_bounds__(1024) void paged_decode_plan_combine_kernel(const DecodeArgs a) {
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // wave-uniform KV head
   const int lane = threadIdx.x & 63;
-  if ((int)blockIdx.x < a.batch) {
-    const int b = blockIdx.x;
+  const int nrw = (a.batch + kPlanRowsPerWg - 1) / kPlanRowsPerWg;
+  if ((int)blockIdx.x < nrw) {
     const int cap = a.max_pages * a.page_size;
-    const int c = a.seqlens[b];
-    if constexpr (kAppend) {
-      uint32_t kw = reinterpret_cast<const uint32_t*>(a.k_new + (int64_t)b * a.kn_sb + g * kD)[lane];
-      const uint32_t vw = reinterpret_cast<const uint32_t*>(a.v_new + (int64_t)b * a.vn_sb + g * kD)[lane];
-      if constexpr (kRope)
-        kw = qk_norm_rope64(kw, reinterpret_cast<const uint32_t*>(a.kn_w)[lane],
-                            reinterpret_cast<const uint32_t*>(a.rcos + (int64_t)b * a.rs_sb)[lane],
-                            reinterpret_cast<const uint32_t*>(a.rsin + (int64_t)b * a.rs_sb)[lane], a.eps);
-      if (c < 0 || c >= cap) {
-        write_zero_row(a, b, g, lane);
-        return;
+    int c[kPlanRowsPerWg], page[kPlanRowsPerWg];
+    uint32_t kw[kPlanRowsPerWg], vw[kPlanRowsPerWg];
+    uint32_t wk = 0u;
+    if constexpr (kRope) wk = reinterpret_cast<const uint32_t*>(a.kn_w)[lane];
+#pragma unroll
+    for (int u = 0; u < kPlanRowsPerWg; ++u) {
+      const int b = min((int)blockIdx.x * kPlanRowsPerWg + u, a.batch - 1);
+      c[u] = a.seqlens[b];
+      if constexpr (kAppend) {
+        kw[u] = reinterpret_cast<const uint32_t*>(a.k_new + (int64_t)b * a.kn_sb + g * kD)[lane];
+        vw[u] = reinterpret_cast<const uint32_t*>(a.v_new + (int64_t)b * a.vn_sb + g * kD)[lane];
+        page[u] = a.slot_page[b];
+        if constexpr (kRope)
+          kw[u] = qk_norm_rope64(kw[u], wk, reinterpret_cast<const uint32_t*>(a.rcos + (int64_t)b * a.rs_sb)[lane],
+                                 reinterpret_cast<const uint32_t*>(a.rsin + (int64_t)b * a.rs_sb)[lane], a.eps);
       }
-      const int page = a.slot_page[b];
-      if ((unsigned)page < (unsigned)a.num_pages) {
-        const int pidx = c / a.page_size;
-        const int64_t dst = (int64_t)page * a.kv_sp + (int64_t)(c - pidx * a.page_size) * a.kv_st + (int64_t)g * a.kv_sh;
-        __builtin_nontemporal_store(kw, reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.kc) + dst) + lane);
-        __builtin_nontemporal_store(vw, reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.vc) + dst) + lane);
+    }
+#pragma unroll
+    for (int u = 0; u < kPlanRowsPerWg; ++u) {
+      const int b = (int)blockIdx.x * kPlanRowsPerWg + u;
+      if (b >= a.batch) break;
+      if constexpr (kAppend) {
+        if (c[u] < 0 || c[u] >= cap) {
+          write_zero_row(a, b, g, lane);
+          continue;
+        }
+        // (the slot's page id was written by the decode kernel for every row it attended, so it is only read here)
+        if ((unsigned)page[u] < (unsigned)a.num_pages) {
+          const int pidx = c[u] / a.page_size;
+          const int64_t dst = (int64_t)page[u] * a.kv_sp + (int64_t)(c[u] - pidx * a.page_size) * a.kv_st +
+                              (int64_t)g * a.kv_sh;
+          __builtin_nontemporal_store(kw[u], reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.kc) + dst) + lane);
+          __builtin_nontemporal_store(vw[u], reinterpret_cast<uint32_t*>(const_cast<uint16_t*>(a.vc) + dst) + lane);
+        }
+      } else {
+        if (ctx_of<false>(c[u], cap) == 0) write_zero_row(a, b, g, lane);
       }
-    } else {
-      if (ctx_of<false>(c, cap) == 0) write_zero_row(a, b, g, lane);
     }
     return;
   }
-  const int ci = blockIdx.x - a.batch;
+  const int ci = blockIdx.x - nrw;
   // The decode kernel's range flags, cleared for the next call on the plan (one per possible range).
   if (threadIdx.x == 0) __hip_atomic_store(a.plan_claim + ci, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int4 d = a.plan_cut[ci];
@@ -2188,7 +2207,7 @@ static int launch_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
         hipLaunchKernelGGL((paged_decode_sk_kernel<false, false, 2, true>), dim3(a.grid), block2, 0, st, a);
       e = hipGetLastError();
       if (e != hipSuccess) return fail(Q3A_ELAUNCH, "%s: planned launch failed: %s", who, hipGetErrorString(e));
-      const dim3 cgrid(batch + PL.grid);
+      const dim3 cgrid((batch + kPlanRowsPerWg - 1) / kPlanRowsPerWg + PL.grid);
       if (rope)
         hipLaunchKernelGGL((paged_decode_plan_combine_kernel<true, true>), cgrid, block, 0, st, a);
       else if (append)
