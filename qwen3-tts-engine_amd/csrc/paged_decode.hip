@@ -68,10 +68,10 @@ struct DecodeArgs {
   int64_t kn_sb, vn_sb;
   int num_pages, page_size;
   uint32_t page_bytes;  // byte extent of one page's tokens (bounds of the buffer loads)
+  int max_pages;        // table entries per row
   const int32_t* seqlens;
   const int32_t* bt;
   int64_t bt_sb;
-  int max_pages;
   uint16_t* out;
   int64_t o_sb, o_sh;
   float* ws;            // partial records
@@ -877,10 +877,10 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   const int B = a.batch;
 
   if constexpr (kRope) {
-    if (tid < 2 * kD / 8) {
-      const uint16_t* w = tid < kD / 8 ? a.qn_w : a.kn_w;
-      st16(&s_nw[tid / (kD / 8)][(tid % (kD / 8)) * 8], ld16(w + (tid % (kD / 8)) * 8));
-    }
+    // Waves 0 and 1 copy the q-norm and k-norm weights straight into LDS (the first barrier waits for them), so
+    // wave 0 reaches the prologue's other loads without waiting for these.
+    if (wv < 2 && lane < kD / 8)
+      lds_copy16(make_rsrc(wv == 0 ? a.qn_w : a.kn_w, kD * 2), &s_nw[kRope ? (wv & 1) : 0][0], (uint32_t)lane * 16);
   }
 
   // Prologue: tiles per row and their exclusive prefix sum (block-wide scan).  A planned call reads its range and
@@ -903,32 +903,48 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   // first tile list, on a flag no other workgroup touches, so it costs no round trip of its own; the planned combine
   // clears the flags for the next call.
   __shared__ int s_claim;
+  // Planned calls: the taken range's plan item (kPlanWgInts values), read by one thread with the claim.
+  __shared__ int s_pwg[kPlan ? kPlanWgInts : 1];
   [[maybe_unused]] int krange = blockIdx.x;
-  const int* pwg = nullptr;
+  [[maybe_unused]] const int* const pwg = s_pwg;
   if constexpr (kPlan) {
+    // The kernel arguments of the tile loop are read in the same batch as the claim's: left to itself the compiler
+    // reads them after the claim's exchange has returned, one more round trip ahead of the first K/V load.
+    __asm__ volatile("" ::"s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.num_pages), "s"(a.page_bytes), "s"(a.out),
+                     "s"(a.ws), "s"(a.hkv), "s"(a.grid), "s"(a.plan_wg), "s"(a.plan_first), "s"(a.plan_claim));
     const int xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 7;  // HW_REG_XCC_ID, bits 0-3
     const int kspec = min((int)(blockIdx.x & ~7u) + xcc, a.grid - 1);
-    auto load_range = [&](int k) {
-      pwg = a.plan_wg + (int64_t)k * kPlanWgInts;
+    auto load_list = [&](int k) {
       // The wave's first tile list goes straight into LDS (lanes 0-31 copy 16 B each; the other lanes' out-of-range
       // copies write zeros over the next 512 B): no register holds it through the tile loop.
       lds_copy16(make_rsrc(a.plan_first + ((int64_t)k * kHalves + half) * 64, 64 * sizeof(int2)),
                  &s_plan[kPlan ? wv : 0][0], lane < 32 ? (uint32_t)lane * 16 : kOutOfRange);
     };
-    load_range(kspec);
+    load_list(kspec);
     if (tid == 0) {
+      // The guessed range's item is read beside the exchange (one round trip for both); another range's only after
+      // a collision.
+      const int4* w = reinterpret_cast<const int4*>(a.plan_wg + (int64_t)kspec * kPlanWgInts);
+      int4 w0 = w[0], w1 = w[1];
       int got = -1;
       for (int d = 0; d < a.grid && got < 0; ++d) {
         const int k = kspec + d < a.grid ? kspec + d : kspec + d - a.grid;
         if (__hip_atomic_exchange(a.plan_claim + k, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) got = k;
       }
+      if (got >= 0 && got != kspec) {
+        w = reinterpret_cast<const int4*>(a.plan_wg + (int64_t)got * kPlanWgInts);
+        w0 = w[0];
+        w1 = w[1];
+      }
       s_claim = got;
+      *reinterpret_cast<int4*>(&s_pwg[0]) = w0;
+      *reinterpret_cast<int4*>(&s_pwg[kPlan ? 4 : 0]) = w1;
     }
     __syncthreads();
-    krange = s_claim;
+    krange = __builtin_amdgcn_readfirstlane(s_claim);
     if (krange != kspec) {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the guessed list's copy has landed before it is replaced
-      if (krange >= 0) load_range(krange);
+      if (krange >= 0) load_list(krange);
     }
     if (krange < 0) return;  // no free range (one flag per launched workgroup: does not happen)
   }
@@ -938,10 +954,10 @@ __global__ __launch_bounds__(1024) void paged_decode_sk_kernel(const DecodeArgs 
   // mid_cut_tile, the midpoint when a row runs across it, else -1.
   auto range_of = [&](int& lo_w, int& hi_w, int& mid, int& mid_row) __attribute__((always_inline)) {
     if constexpr (kPlan) {
-      lo_w = pwg[0];
-      hi_w = pwg[1];
-      mid = pwg[2];
-      mid_row = pwg[3];
+      lo_w = __builtin_amdgcn_readfirstlane(pwg[0]);
+      hi_w = __builtin_amdgcn_readfirstlane(pwg[1]);
+      mid = __builtin_amdgcn_readfirstlane(pwg[2]);
+      mid_row = __builtin_amdgcn_readfirstlane(pwg[3]);
       return;
     }
     lo_w = (int)sk_lo(blockIdx.x, NT, ge);
@@ -1525,7 +1541,11 @@ __global__ __launch_bounds__(64 * row_max_waves(kMulti)) void paged_decode_row_k
   // Every load that does not depend on the context goes out together with the row's cache_seqlens entry: the
   // table entry of this lane's tile, q, (append form) the new k/v rows, (norm/rope form) the weights and cos/sin.
   // The empty asm with a memory clobber keeps the compiler from sinking them below the exit test of chunks past the
-  // row's end, which would put the table and q behind the seqlens round trip.
+  // row's end, which would put the table and q behind the seqlens round trip.  The kernel arguments these loads
+  // and the exit test need are read in one batch (left to itself the compiler reads them in two, a wait between).
+  __asm__ volatile("" ::"s"(a.seqlens), "s"(a.bt), "s"(a.bt_sb), "s"(a.max_pages), "s"(a.page_size), "s"(a.row_per),
+                   "s"(a.q), "s"(a.q_sb), "s"(a.q_sh), "s"(a.scale_log2), "s"(a.kc), "s"(a.vc), "s"(a.kv_sp),
+                   "s"(a.kv_st), "s"(a.kv_sh));
   const int c_row = a.seqlens[b];
   const int cap = a.max_pages * a.page_size;
   const int t = kTile * (tb + w + lane * W);  // first token of this lane's tile
