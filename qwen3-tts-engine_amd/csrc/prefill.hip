@@ -679,6 +679,14 @@ __global__ __launch_bounds__(64 * (kRope ? kResRopeWaves : kResMaxGroups)) void 
   // Copies: the 16-key groups of K and V (2 per tile and operand) are dealt round-robin to the waves; four
   // direct-to-LDS loads each, same layout and swizzle as the tiled kernel.
   const int ngroups = 4 * ntiles;
+  // The copies' kernel arguments (and the append form's table arguments) are read with the others, in one batch:
+  // left to itself the compiler reads them after the first batch has returned, one more round trip before the first
+  // copy.  (Not in the norm/rope form, whose registers the compiler then splits the first batch over.)
+  if constexpr (!kRope) {
+    __asm__ volatile("" ::"s"(a.k), "s"(a.v), "s"(a.k_st), "s"(a.k_sh), "s"(a.k_ss), "s"(a.v_st), "s"(a.v_sh),
+                     "s"(a.v_ss));
+    if constexpr (kAppend) __asm__ volatile("" ::"s"(a.pbt), "s"(a.pbt_sb), "s"(a.p_max_pages));
+  }
   const int P = kRope ? a.P : 0;  // fused admission form: key rows below P come from the prefix bank
   int64_t psrc = -1;              // its prefix row (-1: zeros)
   if constexpr (kRope) {
