@@ -1371,8 +1371,6 @@ __global__ __launch_bounds__(1024) void paged_decode_plan_combine_kernel(const D
     return;
   }
   const int ci = blockIdx.x - nrw;
-  // The decode kernel's range flags, cleared for the next call on the plan (one per possible range).
-  if (threadIdx.x == 0) __hip_atomic_store(a.plan_claim + ci, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int4 d = a.plan_cut[ci];
   const int h = lane >> 5;
   const int d0 = (lane & 31) * 4;
@@ -1385,6 +1383,12 @@ __global__ __launch_bounds__(1024) void paged_decode_plan_combine_kernel(const D
     mr[u] = P[kPartML + h];
     lr[u] = P[kPartML + kG + h];
   }
+  // The first two records' loads go out with the descriptor's: the empty asm with a memory clobber keeps the compiler
+  // from sinking them below the tests on the descriptor, which would make them a second round trip.
+  __asm__ volatile("" ::: "memory");
+  // The decode kernel's range flags, cleared for the next call on the plan (one per possible range); the store is
+  // issued after the loads, so waiting for the descriptor does not wait for it.
+  if (threadIdx.x == 0) __hip_atomic_store(a.plan_claim + ci, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int b = d.x, count = d.y, ob = d.z;
   if (b < 0) return;
   float M = kMaxSeed, L = 0.f;
